@@ -1,0 +1,369 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+* block-mask oracle  -> the literal fixtures of the reference's
+  tests/test_block_mask.py (line numbers cited per test) and torch's own
+  ``torch.nn.attention.flex_attention.create_block_mask`` on the CPU;
+* dense attention    -> torch scaled_dot_product_attention / autograd in float64
+  (the closed form the reference's own tests use, test_mapped_attention.py:31-300),
+  plus closed forms (zero inputs, constant scores, empty rows);
+* window rule        -> the reference tests' relations
+  (test_mapped_attention.py:1552-1648, 1762-1798) and its documented clamp;
+* blockwise restatement -> the dense float64 closed form and block-size
+  invariance (test_mapped_attention.py:433-452, 1176-1195).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention_oracle as ao
+from oracle import block_mask_oracle as bo
+
+
+# --------------------------------------------------------------------------
+# block mask oracle vs the reference's literal fixtures
+# --------------------------------------------------------------------------
+
+CAUSAL8 = np.tril(np.ones((8, 8), np.int32))   # test_block_mask.py:36-49 / :286-299
+
+
+def test_bm_causal_literal():
+    bm = bo.create_block_mask(lambda b, h, q, k: q >= k, 2, 2, 8, 8, 4)   # :15-51
+    assert (bm["B"], bm["H"], bm["Q_LEN"], bm["KV_LEN"]) == (2, 2, 8, 8)
+    assert np.array_equal(bo.materialize(bm), np.broadcast_to(CAUSAL8, (2, 2, 8, 8)))
+
+
+def test_bm_partial_pattern():
+    f = lambda b, h, q, k: (q + k) % 3 == 0                              # :54-72
+    dense = bo.materialize(bo.create_block_mask(f, 1, 1, 8, 8, 4))
+    for q in range(8):
+        for k in range(8):
+            assert dense[0, 0, q, k] == ((q + k) % 3 == 0)
+
+
+def test_bm_from_kv_blocks_literal():
+    # :75-113, kv index 4 lies past the last key block and is dropped
+    bm = dict(B=1, H=1, Q_LEN=8, KV_LEN=8, Q_BLOCK_SIZE=2, KV_BLOCK_SIZE=2,
+              kv_num_blocks=np.array([[[2, 2, 2, 2]]]),
+              kv_indices=np.array([[[[0, 1], [1, 2], [2, 3], [3, 4]]]]),
+              full_kv_num_blocks=np.array([[[0, 0]]]),
+              full_kv_indices=np.array([[[[0, 0], [0, 0]]]]),
+              mask_mod=lambda b, h, q, k: (k // 2 >= q // 2) & (k // 2 <= q // 2 + 1))
+    dense = bo.materialize(bm)
+    for q in range(8):
+        for k in range(8):
+            assert dense[0, 0, q, k] == ((k // 2 >= q // 2) & (k // 2 < q // 2 + 2))
+
+
+def test_bm_infer_lengths_literal():
+    # :116-169: Q_LEN = 3 * 2, KV_LEN = (3 + 1) * 2
+    kv_num = np.array([[[1, 2, 1]]])
+    kv_idx = np.array([[[[0, 3], [1, 2], [3, 3]]]])
+    fkv_num = np.array([[[1, 0, 1]]])
+    fkv_idx = np.array([[[[2, 0], [0, 0], [1, 0]]]])
+    assert kv_idx.shape[2] * 2 == 6
+    assert bo.infer_kv_len(kv_num, kv_idx, fkv_num, fkv_idx, 2) == 8
+
+
+def test_bm_get_partial_block_literal():
+    blk = bo.get_partial_block(lambda b, h, q, k: (q + k) % 2 == 0, 0, 0, 0, 0, 4, 4)  # :172-185
+    assert np.array_equal(blk, [[1, 0, 1, 0], [0, 1, 0, 1], [1, 0, 1, 0], [0, 1, 0, 1]])
+
+
+def test_bm_sparse_lists_literal():
+    num, idx = bo.sparse_lists(np.array([[[[1, 0], [1, 1]]]]))                    # :188-222
+    rel = np.array([[True, False], [True, True]])
+    assert np.array_equal(num, [[[1, 2]]])
+    assert np.array_equal(idx * rel, np.array([[[[0, 2], [0, 1]]]]) * rel)
+    num2, idx2 = bo.sparse_lists(np.array([[1, 0], [1, 1]]))
+    assert np.array_equal(num2, [[[1, 2]]])
+    assert np.array_equal(idx2 * rel, np.array([[[[0, 2], [0, 1]]]]) * rel)
+    qn, qi = bo.sparse_lists(np.array([[[[1, 0], [1, 1]]]]).transpose(0, 1, 3, 2))  # :225-246
+    relq = np.array([[True, True], [True, False]])
+    assert np.array_equal(qn, [[[2, 1]]])
+    assert np.array_equal(qi * relq, np.array([[[[0, 1], [1, 2]]]]) * relq)
+
+
+def test_bm_dense_from_lists_literal():
+    dense = bo.dense_from_lists(1, 1, 2, 2, np.array([[[1, 2]]]), np.array([[[[0, 0], [0, 1]]]]))
+    assert np.array_equal(dense, [[[[1, 0], [1, 1]]]])                             # :249-265
+
+
+def test_bm_full_literal():
+    bm = bo.create_block_mask(lambda b, h, q, k: True, 2, 2, 8, 8, 4)           # :304-323
+    assert np.array_equal(bo.materialize(bm), np.ones((2, 2, 8, 8), np.int32))
+    assert bm["kv_num_blocks"].sum() == 0
+
+
+MASKS = {
+    "causal": lambda b, h, q, k: q >= k,
+    "window": lambda b, h, q, k: (q >= k) & (q - k <= 5),
+    "checker": lambda b, h, q, k: ((q // 4 + k // 4) % 2 == 0) | (q == k),
+    "head": lambda b, h, q, k: (q + h * 3) >= k,
+    "batch_doc": lambda b, h, q, k: (q // (5 + b) == k // (5 + b)) & (q >= k),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MASKS))
+def test_bm_vs_torch_create_block_mask(name):
+    from torch.nn.attention.flex_attention import create_block_mask as tcbm
+    f = MASKS[name]
+    B, H, QL, KL, BS = 2, 2, 24, 32, 4
+    mine = bo.create_block_mask(f, B, H, QL, KL, BS)
+    ref = tcbm(lambda b, h, q, k: f(b, h, q, k), B, H, QL, KL, device="cpu", BLOCK_SIZE=BS,
+               _compile=False)
+    for a, t in (("kv_num_blocks", "kv_num_blocks"), ("full_kv_num_blocks", "full_kv_num_blocks"),
+                 ("q_num_blocks", "q_num_blocks"), ("full_q_num_blocks", "full_q_num_blocks")):
+        assert np.array_equal(mine[a], getattr(ref, t).numpy()), a
+    for num, idx, tnum, tidx in (("kv_num_blocks", "kv_indices", "kv_num_blocks", "kv_indices"),
+                                 ("full_kv_num_blocks", "full_kv_indices", "full_kv_num_blocks",
+                                  "full_kv_indices")):
+        n = mine[num]
+        for pos in np.ndindex(*n.shape):
+            k = int(n[pos])
+            assert sorted(mine[idx][pos][:k]) == sorted(getattr(ref, tidx).numpy()[pos][:k])
+
+
+def test_bm_brute_force_classification():
+    rng = np.random.default_rng(3)
+    tbl = rng.random((16, 16)) < 0.4
+    f = lambda b, h, q, k: tbl[q, k]
+    part, full = bo.classify(f, 1, 1, 16, 16, 4, 4)
+    for i in range(4):
+        for j in range(4):
+            t = tbl[4 * i:4 * i + 4, 4 * j:4 * j + 4]
+            assert full[0, 0, i, j] == int(t.all())
+            assert part[0, 0, i, j] == int(t.any() and not t.all())
+
+
+# --------------------------------------------------------------------------
+# dense attention oracle vs torch (float64) and closed forms
+# --------------------------------------------------------------------------
+
+
+def torch_sdpa(Q, K, V, allowed):
+    """Q [B,N,Hq,d], allowed [B,Hq,N,L]; GQA via head expansion."""
+    Hq, Hkv = Q.shape[2], K.shape[2]
+    G = Hq // Hkv
+    q = torch.tensor(Q).permute(0, 2, 1, 3)
+    k = torch.tensor(K).repeat_interleave(G, dim=2).permute(0, 2, 1, 3)
+    v = torch.tensor(V).repeat_interleave(G, dim=2).permute(0, 2, 1, 3)
+    out = F.scaled_dot_product_attention(q, k, v, attn_mask=torch.tensor(allowed))
+    return out.permute(0, 2, 1, 3).numpy()
+
+
+def rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+@pytest.mark.parametrize("name", sorted(MASKS))
+@pytest.mark.parametrize("gqa", [1, 2])
+def test_dense_forward_vs_torch(name, gqa):
+    B, N, L, Hq, d = 2, 24, 32, 4, 16
+    Q, K, V = rand((B, N, Hq, d), 1), rand((B, L, Hq // gqa, d), 2), rand((B, L, Hq // gqa, d), 3)
+    plan = ao.canonical_plan(Q.shape, K.shape, V.shape, mask_fn=MASKS[name], block_size=8)
+    allowed = ao.effective_mask(plan)
+    O, lse = ao.dense_forward(Q, K, V, allowed)
+    np.testing.assert_allclose(O, torch_sdpa(Q, K, V, allowed), rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("name", sorted(MASKS))
+@pytest.mark.parametrize("gqa", [1, 2])
+def test_dense_backward_vs_torch_autograd(name, gqa):
+    B, N, L, Hq, d = 2, 24, 32, 4, 16
+    Q, K, V = rand((B, N, Hq, d), 4), rand((B, L, Hq // gqa, d), 5), rand((B, L, Hq // gqa, d), 6)
+    dO = rand((B, N, Hq, d), 7)
+    plan = ao.canonical_plan(Q.shape, K.shape, V.shape, mask_fn=MASKS[name], block_size=8)
+    allowed = ao.effective_mask(plan)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (Q, K, V))
+    G = Hq // K.shape[2]
+    out = F.scaled_dot_product_attention(
+        tq.permute(0, 2, 1, 3), tk.repeat_interleave(G, 2).permute(0, 2, 1, 3),
+        tv.repeat_interleave(G, 2).permute(0, 2, 1, 3), attn_mask=torch.tensor(allowed))
+    (out.permute(0, 2, 1, 3) * torch.tensor(dO)).sum().backward()
+    dQ, dK, dV = ao.dense_backward(Q, K, V, allowed, dO)
+    for mine, ref in ((dQ, tq.grad), (dK, tk.grad), (dV, tv.grad)):
+        np.testing.assert_allclose(mine, ref.numpy(), rtol=1e-9, atol=1e-11)
+
+
+def test_dense_lse_closed_form():
+    B, N, L, H, d = 1, 5, 7, 2, 8
+    Q, K, V = rand((B, N, H, d), 8), rand((B, L, H, d), 9), rand((B, L, H, d), 10)
+    allowed = np.ones((B, H, N, L), bool)
+    _, lse = ao.dense_forward(Q, K, V, allowed)
+    S = np.einsum("bqhd,bkhd->bhqk", Q, K) / math.sqrt(d)
+    np.testing.assert_allclose(lse, np.log(np.exp(S).sum(-1)), rtol=1e-12)
+
+
+def test_dense_empty_rows_zero():
+    """attention.py:93-100: a row with no allowed key outputs 0 and has zero grads."""
+    B, N, L, H, d = 1, 6, 6, 2, 8
+    Q, K, V, dO = (rand((B, N if i in (0, 3) else L, H, d), 11 + i) for i in range(4))
+    allowed = np.ones((B, H, N, L), bool)
+    allowed[:, :, 2] = False
+    O, lse = ao.dense_forward(Q, K, V, allowed)
+    assert np.all(O[:, 2] == 0) and np.all(np.isneginf(lse[:, :, 2]))
+    dQ, dK, dV = ao.dense_backward(Q, K, V, allowed, dO)
+    assert np.all(dQ[:, 2] == 0)
+    # the empty row contributes nothing to dK/dV: removing its dO changes nothing
+    dO2 = dO.copy()
+    dO2[:, 2] = 0
+    _, dK2, dV2 = ao.dense_backward(Q, K, V, allowed, dO2)
+    np.testing.assert_array_equal(dK, dK2)
+    np.testing.assert_array_equal(dV, dV2)
+
+
+def test_dense_constant_scores_uniform():
+    """Q = 0 gives constant scores, so O is the mean of the allowed values."""
+    B, N, L, H, d = 1, 4, 8, 1, 4
+    V = rand((B, L, H, d), 20)
+    K = rand((B, L, H, d), 21)
+    Q = np.zeros((B, N, H, d))
+    allowed = ao.effective_mask(ao.canonical_plan(Q.shape, K.shape, V.shape, is_causal=True))
+    O, _ = ao.dense_forward(Q, K, V, allowed)
+    for q in range(N):
+        np.testing.assert_allclose(O[0, q, 0], V[0, :q + 1, 0].mean(0), rtol=1e-12)
+
+
+def test_dense_zero_inputs_zero_output():
+    """test_mapped_attention.py:1024-1039."""
+    z = np.zeros((1, 4, 2, 8))
+    O = ao.reference_attention(z[0], z[0], z[0])
+    assert O.shape == (4, 2, 8) and np.allclose(O, 0, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# canonicalisation, padding, window rule
+# --------------------------------------------------------------------------
+
+
+def test_errors_match_reference():
+    """test_mapped_attention.py:1051-1073 and attention.py:385-391."""
+    q = np.zeros((8, 4, 16))
+    with pytest.raises(ValueError):
+        ao.canonical_plan(q.shape, q.shape, q.shape, is_causal=True, mask_fn=lambda h, a, b: True)
+    with pytest.raises(AssertionError):
+        ao.canonical_plan(q.shape, (8, 4, 17), q.shape)
+    with pytest.raises(ValueError):
+        ao.canonical_plan((8, 16), (8, 16), (8, 16))
+    with pytest.raises(AssertionError):
+        ao.canonical_plan((8, 6, 16), (8, 4, 16), (8, 4, 16))      # Hq % Hkv
+
+
+def test_padding_vs_torch():
+    """test_mapped_attention.py:1076-1112: N=10, L=13, block 4."""
+    Q, K, V = rand((10, 4, 16), 30), rand((13, 4, 16), 31), rand((13, 4, 16), 32)
+    for kw, allowed in (({}, np.ones((1, 4, 10, 13), bool)),
+                        ({"is_causal": True}, np.broadcast_to(np.tril(np.ones((10, 13), bool)), (1, 4, 10, 13))),
+                        ({"mask_fn": lambda h, q, k: abs(q - k) <= 2},
+                         np.broadcast_to(abs(np.arange(10)[:, None] - np.arange(13)[None]) <= 2, (1, 4, 10, 13)))):
+        O = ao.reference_attention(Q, K, V, block_size=4, **kw)
+        np.testing.assert_allclose(O, torch_sdpa(Q[None], K[None], V[None], allowed)[0], rtol=1e-10, atol=1e-12)
+
+
+def test_padding_extra_block_changes_window_clamp():
+    """Padding adds a whole key block when L % bs == 0 (attention.py:432), which moves
+    the clamped window of the last query block."""
+    plan = ao.canonical_plan((10, 1, 4), (12, 1, 4), (12, 1, 4), block_size=4, window_size=(0, 0))
+    assert (plan.Npad, plan.Lpad) == (12, 16)
+    assert list(ao.visited_key_blocks(2, plan.Lpad // 4, plan.window)) == [2]
+    plan2 = ao.canonical_plan((10, 1, 4), (12, 1, 4), (12, 1, 4), block_size=4, window_size=(4, 4))
+    # lwb=1, rwb=2: the last query block (2) scans blocks 1..3, block 3 being pure padding
+    assert list(ao.visited_key_blocks(2, plan2.Lpad // 4, plan2.window)) == [1, 2, 3]
+
+
+def test_window_scans_constant_block_count():
+    """The docstring (attention.py:375-381): the window is a lower bound, widened near
+    the sequence edges -- every query block scans exactly lwb + rwb key blocks."""
+    for nk in range(3, 9):
+        for lwb in range(0, 3):
+            for rwb in range(1, 3):
+                if lwb + rwb > nk:
+                    continue
+                for i in range(nk):
+                    r = list(ao.visited_key_blocks(i, nk, (lwb, rwb)))
+                    assert len(r) == lwb + rwb and r[0] >= 0 and r[-1] < nk
+                    assert i in r
+
+
+def _ref(Q, K, V, **kw):
+    return ao.reference_attention(Q, K, V, **kw)
+
+
+def test_window_relations_from_reference_tests():
+    Q, K, V = rand((32, 4, 16), 40), rand((32, 4, 16), 41), rand((32, 4, 16), 42)
+    sw = lambda h, q, k: (q - 3 <= k) & (k <= q + 2)
+    a = _ref(Q, K, V, mask_fn=sw, block_size=8)
+    b = _ref(Q, K, V, mask_fn=sw, block_size=8, window_size=(3, 2))
+    np.testing.assert_allclose(a, b, rtol=1e-12)                      # :1552-1590
+    Q, K, V = rand((64, 4, 16), 43), rand((64, 4, 16), 44), rand((64, 4, 16), 45)
+    no_w = _ref(Q, K, V, block_size=16)
+    w11 = _ref(Q, K, V, block_size=16, window_size=(1, 1))
+    w161 = _ref(Q, K, V, block_size=16, window_size=(16, 1))
+    w171 = _ref(Q, K, V, block_size=16, window_size=(17, 1))
+    assert np.abs(no_w - w11).max() > 1e-3                            # :1593-1648
+    assert np.abs(w161 - w11).max() < 1e-3
+    assert np.abs(w161 - w171).max() > 1e-3
+    Q, K, V = rand((32, 4, 16), 46), rand((32, 4, 16), 47), rand((32, 4, 16), 48)
+    rm = lambda h, q, k: abs(q - k) <= 3
+    np.testing.assert_allclose(_ref(Q, K, V, mask_fn=rm, block_size=8, window_size=(8, 8)),
+                               _ref(Q, K, V, mask_fn=rm, block_size=8), rtol=1e-12)   # :1762-1798
+
+
+def test_window_too_wide_raises():
+    with pytest.raises(TypeError):
+        ao.canonical_plan((8, 1, 4), (8, 1, 4), (8, 1, 4), window_size=(1, 0))   # bs = N: 1 block
+
+
+def test_unpadded_ragged_keys_raise():
+    with pytest.raises(RuntimeError):
+        ao.canonical_plan((8, 1, 4), (12, 1, 4), (12, 1, 4), block_size=8)
+
+
+# --------------------------------------------------------------------------
+# blockwise restatement vs the dense closed form
+# --------------------------------------------------------------------------
+
+CASES = [
+    dict(N=32, L=32, Hq=4, Hkv=4, bs=8, kw=dict(is_causal=True)),
+    dict(N=32, L=32, Hq=4, Hkv=2, bs=8, kw=dict(mask_fn=lambda h, q, k: (q - k) % 3 != 1)),
+    dict(N=10, L=13, Hq=2, Hkv=1, bs=4, kw=dict(mask_fn=lambda b, h, q, k: abs(q - k) <= 2)),
+    dict(N=64, L=64, Hq=2, Hkv=2, bs=16, kw=dict(window_size=(1, 1))),
+    dict(N=24, L=24, Hq=2, Hkv=2, bs=8, kw=dict(mask_fn=lambda b, h, q, k: (q > 10) & (k <= q))),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_blockwise_matches_dense(case):
+    c = CASES[case]
+    B, d = 2, 8
+    Q, K, V = rand((B, c["N"], c["Hq"], d), 50), rand((B, c["L"], c["Hkv"], d), 51), rand((B, c["L"], c["Hkv"], d), 52)
+    dO = rand((B, c["N"], c["Hq"], d), 53)
+    plan = ao.canonical_plan(Q.shape, K.shape, V.shape, block_size=c["bs"], **c["kw"])
+    allowed = ao.effective_mask(plan)
+    O_d, _ = ao.dense_forward(Q, K, V, allowed)
+    O_b = ao.blockwise_forward(Q, K, V, plan, dtype=np.float64)[:, :c["N"]]
+    np.testing.assert_allclose(O_b, O_d, rtol=1e-10, atol=1e-12)
+    g_d = ao.dense_backward(Q, K, V, allowed, dO)
+    g_b = ao.blockwise_backward(Q, K, V, dO, plan, dtype=np.float64)
+    np.testing.assert_allclose(g_b[0][:, :c["N"]], g_d[0], rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(g_b[1][:, :c["L"]], g_d[1], rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(g_b[2][:, :c["L"]], g_d[2], rtol=1e-9, atol=1e-11)
+
+
+def test_block_size_invariance():
+    """test_mapped_attention.py:433-452 / :1176-1195."""
+    Q, K, V = rand((1, 128, 8, 32), 60), rand((1, 128, 8, 32), 61), rand((1, 128, 8, 32), 62)
+    outs = []
+    for bs in (16, 32, 128):
+        plan = ao.canonical_plan(Q.shape, K.shape, V.shape, is_causal=True, block_size=bs)
+        outs.append(ao.blockwise_forward(Q, K, V, plan, dtype=np.float64))
+    np.testing.assert_allclose(outs[0], outs[1], rtol=1e-10)
+    np.testing.assert_allclose(outs[0], outs[2], rtol=1e-10)
+
+
+def test_count_pairs_causal_closed_form():
+    plan = ao.canonical_plan((2, 128, 8, 64), (2, 128, 8, 64), (2, 128, 8, 64), is_causal=True, block_size=32)
+    assert ao.count_pairs(ao.effective_mask(plan)) == 2 * 8 * 128 * 129 // 2 == 132096
