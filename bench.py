@@ -1,0 +1,278 @@
+"""Benchmark: masked attention forward + backward on one MI355X.
+
+Metric: attention fwd+bwd TFLOP/s counting only unmasked
+FLOPs (fwd 4*d*pairs + bwd 10*d*pairs, pairs = allowed (b, h, q, k)
+positions), and its fraction of the bf16 dense MFMA peak.
+
+A step is one forward + backward pass (mattn_fwd, then the three mattn_bwd
+stages) over one batch of synthetic bf16 inputs resident in HBM.  The
+workload is BASELINE configs[1] (causal, bf16, B=4, L=4096, H=32, d=128,
+block 128); the north-star target shape (B=1, L=8192, H=32, d=128, causal) is
+measured the same way and reported under "target".
+
+The dominant kernel's time is measured with HIP events on the stream the
+kernels run on (torch's current stream, which the C ABI launches on).
+The CPU baseline is the restatement of the reference algorithm in
+oracle/attention_oracle.py (blockwise, dense per-tile mask, no tile skipping,
+per-query-block recompute in the backward pass), timed on a bounded sample of
+query blocks of one (batch, head) slice and scaled by the exact block count.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|target|cfg3|cfg4|cfg5]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+PEAK_HBM_GBS = 8000.0
+
+
+def _docs(L, seed, mean=2048, minlen=64):
+    rng = np.random.default_rng(seed)
+    lens = []
+    while sum(lens) < L:
+        lens.append(max(minlen, int(rng.geometric(1.0 / mean))))
+    return np.repeat(np.arange(len(lens)), lens)[:L]
+
+
+def workload(name):
+    """(B, L, H, d, kwargs, description) of a BASELINE configuration."""
+    if name == "cfg2":
+        return 4, 4096, 32, 128, dict(is_causal=True, block_size=128), \
+            "cfg2: causal bf16 B=4 L=4096 H=32 d=128 block 128, fwd+bwd"
+    if name == "target":
+        return 1, 8192, 32, 128, dict(is_causal=True, block_size=128), \
+            "target: causal bf16 B=1 L=8192 H=32 d=128 block 128, fwd+bwd"
+    if name == "cfg3":
+        return 2, 16384, 16, 128, dict(mask_fn=lambda b, h, q, k: (q >= k) & (q - k <= 512),
+                                       window_size=(512, 0), block_size=128), \
+            "cfg3: sliding window (q>=k)&(q-k<=512), window (512,0), bf16 B=2 L=16384 H=16 d=128"
+    if name == "cfg4":
+        nt, H = 8192 // 128, 32
+        rng = np.random.default_rng(4)
+        tbl = rng.random((H, nt, nt)) < 0.25
+        tbl[:, np.arange(nt), np.arange(nt)] = True
+        mask = lambda b, h, q, k: tbl[h, q // 128, k // 128] & ((q // 128 != k // 128) | (q >= k))
+        return 1, 8192, H, 64, dict(mask_fn=mask, block_size=128), \
+            "cfg4: per-head random 128x128 tiles at 25% (full grid), diagonal causal, bf16 B=1 L=8192 H=32 d=64"
+    if name == "cfg5":
+        doc = _docs(32768, 5)
+        mask = lambda b, h, q, k: (doc[q] == doc[k]) & (q >= k)
+        return 1, 32768, 8, 128, dict(mask_fn=mask, block_size=128), \
+            f"cfg5: packed documents ({doc.max() + 1} docs, geometric mean 2048, min 64) & causal, bf16 B=1 L=32768 H=8 d=128"
+    raise SystemExit(f"unknown config {name}")
+
+
+class Runner:
+    """Preallocated buffers and direct C ABI calls for one configuration."""
+
+    def __init__(self, name, seed=0):
+        import torch
+
+        from jaxmodules_amd import _lib
+        from jaxmodules_amd import attention as A
+
+        self.torch, self.A, self._lib = torch, A, _lib
+        self.lib = _lib.load()
+        B, L, H, d, kw, desc = workload(name)
+        self.desc, self.d = desc, d
+        t0 = time.perf_counter()
+        plan, tm = A.trace_call((B, L, H, d), (B, L, H, d), (B, L, H, d), **kw)
+        self.trace_s = time.perf_counter() - t0
+        self.tm = tm
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        f = d ** -0.25
+        bf = torch.bfloat16
+        self.q = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
+        self.k = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
+        self.v = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
+        self.do = torch.randn((B, L, H, d), generator=g, device=dev)           # float32, like O
+        self.o = torch.empty((B, L, H, d), dtype=torch.float32, device=dev)
+        self.lse = torch.empty((B, H, L), dtype=torch.float32, device=dev)
+        self.dq = torch.empty_like(self.q)
+        self.dk = torch.empty_like(self.k)
+        self.dv = torch.empty_like(self.v)
+        self.p = A._problem(self.q, self.k, self.v, self.o, 1.0 / d ** 0.5, do=self.do, dq=self.dq,
+                            dk=self.dk, dv=self.dv)
+        nws = int(self.lib.mattn_workspace_bytes(ctypes.byref(self.p)))
+        self.ws = torch.empty(nws + 256, dtype=torch.uint8, device=dev)
+        self.wptr = (self.ws.data_ptr() + 255) & ~255
+        self.bm = A.device_blockmap(tm, dev)
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.pairs = tm.pairs
+        self.fwd_flop = 4 * d * tm.pairs
+        self.bwd_flop = 10 * d * tm.pairs
+
+    def fwd(self):
+        self._lib.check(self.lib.mattn_fwd(ctypes.byref(self.p), ctypes.byref(self.bm),
+                                           self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                                           self.o.data_ptr(), self.lse.data_ptr(), self.stream), "fwd")
+
+    def bwd(self, stage):
+        self._lib.check(self.lib.mattn_bwd_stage(
+            ctypes.byref(self.p), ctypes.byref(self.bm), stage, self.q.data_ptr(), self.k.data_ptr(),
+            self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(), self.lse.data_ptr(), self.wptr,
+            self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.stream), f"bwd stage {stage}")
+
+    def measure(self, steps, warmup):
+        torch = self.torch
+        names = ["fwd", "bwd_pre", "bwd_dkdv", "bwd_dq"]
+        for _ in range(warmup):
+            self.fwd()
+            for s in range(3):
+                self.bwd(s)
+        torch.cuda.synchronize()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            e = ev[i]
+            e[0].record()
+            self.fwd()
+            e[1].record()
+            for s in range(3):
+                self.bwd(s)
+                e[2 + s].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = {n: [] for n in names}
+        for e in ev:
+            for j, n in enumerate(names):
+                per[n].append(e[j].elapsed_time(e[j + 1]))
+        kern_ms = {n: float(np.median(v)) for n, v in per.items()}
+        return wall * 1e3 / steps, kern_ms
+
+
+def cpu_baseline(name, budget_s=12.0):
+    """The CPU restatement of the reference algorithm on a bounded sample."""
+    from oracle import attention_oracle as ao
+
+    B, L, H, d, kw, _ = workload(name)
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    f = d ** -0.25
+    Q = (rng.standard_normal((1, L, 1, d)) * f).astype(np.float32)
+    K = (rng.standard_normal((1, L, 1, d)) * f).astype(np.float32)
+    V = (rng.standard_normal((1, L, 1, d)) * f).astype(np.float32)
+    dO = rng.standard_normal((1, L, 1, d)).astype(np.float32)
+    plan = ao.canonical_plan(Q.shape, K.shape, V.shape, **kw)
+    nq = plan.Npad // plan.bs
+    blocks, t_used = [], 0.0
+    order = list(np.linspace(0, nq - 1, nq).astype(int))
+    rng.shuffle(order)
+    for i in order:
+        t0 = time.perf_counter()
+        ao.blockwise_forward(Q, K, V, plan, q_blocks=[int(i)])
+        ao.blockwise_backward(Q, K, V, dO, plan, q_blocks=[int(i)])
+        t_used += time.perf_counter() - t0
+        blocks.append(int(i))
+        if t_used > budget_s:
+            break
+    # the reference does the same work for every query block (no tile skipping),
+    # so the full job takes (all blocks of all B*H slices) / sampled blocks as long
+    scale = (nq * B * H) / len(blocks)
+    t_total = t_used * scale
+    flop = 14 * d * _pairs_of(name)
+    return {"value": flop / t_total / 1e12, "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
+            "sample": f"{len(blocks)} of {nq} query blocks of 1 of {B * H} (batch, head) slices, "
+                      f"fwd+bwd, float32 numpy restatement of attention.py:52-342, "
+                      f"{t_used:.1f} s measured, scaled x{scale:.0f}",
+            "seconds_extrapolated": t_total}
+
+
+_PAIRS = {}
+
+
+def _pairs_of(name):
+    return _PAIRS[name]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--no-target", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the (b, kv head) sharding needs no collective and is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    r = Runner(args.config)
+    _PAIRS[args.config] = r.pairs
+    ms, kern = r.measure(args.steps, args.warmup)
+    total = r.fwd_flop + r.bwd_flop
+    value = total / (ms * 1e-3) / 1e12
+    # dominant kernel and its algorithmic FLOPs per launch
+    alg = {"fwd": r.fwd_flop, "bwd_dkdv": 8 * r.d * r.pairs, "bwd_dq": 2 * r.d * r.pairs}
+    dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern[n])
+    ach = alg[dom] / (kern[dom] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "kernel_ms": round(kern[dom], 4),
+            "flop_per_launch": alg[dom]}
+    out = {
+        "metric": "attn fwd+bwd TFLOP/s (unmasked FLOPs) + % bf16 MFMA peak, 1 MI355X",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q,K,V ~ N(0,1)*d^-0.25 (bf16), dO ~ N(0,1) (float32, the output dtype)",
+        "config": {"workload": r.desc, "pairs": r.pairs, "flop_per_step": total,
+                   "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+                   "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
+                   "fwd_tflops": round(r.fwd_flop / (kern["fwd"] * 1e-3) / 1e12, 2),
+                   "bwd_tflops": round(r.bwd_flop / ((kern["bwd_pre"] + kern["bwd_dkdv"] +
+                                                      kern["bwd_dq"]) * 1e-3) / 1e12, 2),
+                   "tile_map": {"nnz": r.tm.nnz, "full": r.tm.n_full, "partial": r.tm.n_partial,
+                                "masks": r.tm.n_masks, "trace_s": round(r.trace_s, 3)}},
+        "roofline": roof,
+    }
+    if not args.no_target and args.config != "target":
+        del r
+        torch.cuda.empty_cache()
+        t = Runner("target")
+        tms, tk = t.measure(args.steps, args.warmup)
+        tv = (t.fwd_flop + t.bwd_flop) / (tms * 1e-3) / 1e12
+        out["target"] = {"workload": t.desc, "value": round(tv, 2), "unit": "TFLOP/s",
+                         "ms_per_step": round(tms, 4),
+                         "pct_of_bf16_peak": round(100 * tv / PEAK_BF16_TFLOPS, 2),
+                         "kernel_ms": {k: round(v, 4) for k, v in tk.items()}}
+        del t
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
+        out["cpu_baseline"].pop("seconds_extrapolated", None)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

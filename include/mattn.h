@@ -1,0 +1,158 @@
+/*
+ * mattn.h -- C ABI of the MI355X (gfx950) masked-attention library.
+ *
+ * This is the drop-in boundary for jaxmodules' memory-efficient masked
+ * attention.  The reference implements the path in pure JAX:
+ *
+ *   masked_attention_via_map   /root/reference/jaxmodules/attention.py:347-455
+ *   _masked_attention_via_map  attention.py:180-241   (custom_vjp primal)
+ *   custom_vjp fwd rule        attention.py:244-264
+ *   custom_vjp bwd rule        attention.py:266-342
+ *   BlockMask tile lists       /root/reference/jaxmodules/block_mask.py:17-42
+ *
+ * The reference has no FFI, custom call or plugin registry of its own; these
+ * entry points are what a jax.ffi / XLA custom-call target for the custom_vjp
+ * rules binds (the primal -> mattn_fwd, the bwd rule -> mattn_bwd).  The host
+ * layer (Python) keeps the reference's signature, traces mask_fn into the
+ * tile map described by mattn_blockmap and calls these functions.
+ *
+ * Conventions
+ *   - Q is [B, Lq, Hq, D], K and V are [B, Lk, Hkv, D] (the reference's BLHD
+ *     layout).  The innermost (D) dimension is contiguous; the batch, sequence
+ *     and head strides are given in ELEMENTS.
+ *   - Query head h reads key/value head h / (Hq / Hkv) (attention.py:66-68).
+ *   - The attention weights are exp(scale * q.k) normalised over the allowed
+ *     keys of the row; a row with no allowed key yields O = 0 and zero
+ *     gradients (attention.py:91-100).
+ *   - All buffers are caller-owned device memory.  The library never
+ *     allocates, frees or synchronises on the call path; every launch is
+ *     enqueued on the caller's stream.  No atomics are used, so results are
+ *     bitwise reproducible.
+ *   - Return value 0 is success, a negative value is an error code whose text
+ *     is given by mattn_strerror().
+ */
+#ifndef MATTN_H
+#define MATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  Q, K, V, dQ, dK, dV share `dtype`; O and dO share `o_dtype`
+ * (the reference returns float32 O for bfloat16 inputs, attention.py:173). */
+enum mattn_dtype { MATTN_BF16 = 0, MATTN_F16 = 1, MATTN_F32 = 2 };
+
+enum mattn_status {
+  MATTN_OK = 0,
+  MATTN_ERR_NULL = -1,          /* a required pointer is NULL                  */
+  MATTN_ERR_SHAPE = -2,         /* non-positive size or Hq % Hkv != 0          */
+  MATTN_ERR_HEAD_DIM = -3,      /* D not in {64, 128}                          */
+  MATTN_ERR_DTYPE = -4,         /* unsupported dtype / o_dtype combination     */
+  MATTN_ERR_STRIDE = -5,        /* misaligned pointer or stride                */
+  MATTN_ERR_BLOCKMAP = -6,      /* tile map inconsistent with the problem      */
+  MATTN_ERR_LAUNCH = -7,        /* the HIP runtime rejected a launch           */
+  MATTN_ERR_TOO_LARGE = -8      /* a size exceeds 32-bit index ranges          */
+};
+
+/* Tile size of the block map, in queries x keys. */
+#define MATTN_TILE_Q 128
+#define MATTN_TILE_K 128
+
+typedef struct mattn_problem {
+  int32_t B, Lq, Lk, Hq, Hkv, D;
+  int32_t dtype;     /* enum mattn_dtype of Q, K, V, dQ, dK, dV            */
+  int32_t o_dtype;   /* enum mattn_dtype of O and dO: dtype, or MATTN_F32  */
+  float scale;       /* softmax scale; the reference's default_kernel uses
+                        1/sqrt(D) (attention.py:39-50)                     */
+  int32_t reserved;
+  /* element strides {batch, sequence, head}; D is contiguous */
+  int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3];
+  int64_t do_stride[3], dq_stride[3], dk_stride[3], dv_stride[3];
+} mattn_problem;
+
+/*
+ * Tile map of the effective mask (mask_fn AND the window's visited key blocks
+ * AND the unpadded range), at MATTN_TILE_Q x MATTN_TILE_K granularity.  Tiles
+ * that are fully masked are absent.  Present tiles are either full (mask id
+ * -1) or partial (mask id >= 0 into the bit arrays).  This is the reference
+ * BlockMask (block_mask.py:17-42: kv_num_blocks/kv_indices and
+ * full_kv_num_blocks/full_kv_indices, plus the transposed q_* lists) in CSR
+ * form with the partial tiles' element masks attached.
+ *
+ * The map may be broadcast over batch and/or heads (map_b == 1, map_h == 1),
+ * the way the reference's create_block_mask takes B and H (block_mask.py:454).
+ * Map row index of (b, h, tile) = ((b % map_b) * map_h + h % map_h) * n + tile.
+ * Every pointer is device memory.
+ */
+typedef struct mattn_blockmap {
+  int32_t map_b, map_h;      /* 1 or B, 1 or Hq                             */
+  int32_t nqt, nkt;          /* ceil(Lq / TILE_Q), ceil(Lk / TILE_K)        */
+  int32_t n_masks;           /* number of distinct partial-tile masks       */
+  int32_t nnz;               /* number of present tiles in the whole map    */
+  const int32_t* row_ptr;    /* [map_b*map_h*nqt + 1]                        */
+  const int32_t* row_ent;    /* [2*nnz]: (key tile, mask id) per row entry   */
+  const int32_t* col_ptr;    /* [map_b*map_h*nkt + 1]                        */
+  const int32_t* col_ent;    /* [2*nnz]: (query tile, mask id) per column    */
+  /* row_bits[m][q][w]: bit j of word w = key 64*w + j of tile m allowed for
+   * query row q; col_bits[m][k][w]: bit j of word w = query 64*w + j allowed
+   * for key k.  [n_masks][128][2] uint64 each.                              */
+  const uint64_t* row_bits;
+  const uint64_t* col_bits;
+  /* Launch order of the work items, one workgroup each, -1 = idle slot.
+   * q item   = (b * Hq  + h ) * nqt + query tile   (forward and dQ)
+   * kv item  = (b * Hkv + hk) * nkt + key tile     (dK/dV)                  */
+  const int32_t* q_order;
+  const int32_t* kv_order;
+  int32_t n_q_order, n_kv_order;
+} mattn_blockmap;
+
+/* Host-only check of a problem (and, when bm != NULL, of the map's sizes).
+ * No GPU call; usable without a device. */
+int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
+
+/* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer). */
+size_t mattn_workspace_bytes(const mattn_problem* p);
+
+/* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).
+ *   o   : [B, Lq, Hq, D] of o_dtype
+ *   lse : [B, Hq, Lq] float32, base-2 log-sum-exp of the scaled scores
+ *         (-inf for a row with no allowed key); a residual for mattn_bwd. */
+int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
+              const void* q, const void* k, const void* v,
+              void* o, float* lse, void* stream);
+
+/* Backward (replaces the custom_vjp bwd rule, attention.py:266-342).
+ *   do_       : upstream gradient, [B, Lq, Hq, D] of o_dtype
+ *   o, lse    : the forward's outputs
+ *   workspace : mattn_workspace_bytes(p) bytes
+ *   dq, dk, dv: gradients of dtype, every element written (no pre-zeroing). */
+int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
+              const void* q, const void* k, const void* v,
+              const void* o, const void* do_, const float* lse,
+              void* workspace, void* dq, void* dk, void* dv, void* stream);
+
+/* The three kernels of mattn_bwd, in the order they must run on one stream:
+ * MATTN_BWD_PRE (delta = rowsum(dO * O), dO in the MFMA dtype, into the
+ * workspace), then MATTN_BWD_DKDV and MATTN_BWD_DQ (independent of each other;
+ * both read the workspace).  mattn_bwd == the three stages in order.  Same
+ * arguments as mattn_bwd; exposed so a caller can time or overlap the stages. */
+enum mattn_bwd_stage { MATTN_BWD_PRE = 0, MATTN_BWD_DKDV = 1, MATTN_BWD_DQ = 2 };
+int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
+                    const void* q, const void* k, const void* v,
+                    const void* o, const void* do_, const float* lse,
+                    void* workspace, void* dq, void* dk, void* dv, void* stream);
+
+/* Static text of a status code. */
+const char* mattn_strerror(int status);
+
+/* Library ABI version (bumped on any change of the structs above). */
+int mattn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MATTN_H */

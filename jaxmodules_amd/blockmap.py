@@ -1,0 +1,335 @@
+"""Host-side tracer: turns the reference's ``mask_fn`` into the kernels' tile map.
+
+The reference evaluates ``mask_fn(b, h, q, k)`` element by element inside every
+(query block, key block) step and multiplies the scores by it, visiting every
+key block (``/root/reference/jaxmodules/attention.py:52-105,133-177``).  Its
+``block_mask.py`` classifies tiles as empty / full / partial
+(``create_block_mask``, block_mask.py:454-498), but only ``flex_attention``
+consumes that.  Here the two are joined: the effective mask of a call --
+``mask_fn`` AND the window's visited key blocks (attention.py:161-167,199-204)
+AND the unpadded range (attention.py:426-437) -- is traced once on the host
+into 128 x 128 tiles:
+
+* empty tiles are dropped (the kernels never visit them);
+* full tiles are listed with mask id -1 (no per-element work);
+* partial tiles carry packed element bitmasks, de-duplicated by content
+  (all diagonal tiles of a causal mask share one mask).
+
+``mask_fn`` is called with numpy index arrays that broadcast against each
+other (b: [B,1,1,1], h: [1,H,1,1], q: [1,1,Q,1], k: [1,1,1,K]); the reference
+calls it with scalars under nested ``vmap`` (vectorize.py:407-527), so any
+elementwise function of the indices works in both.  The shape of the result
+shows whether the mask depends on b and h; a mask that does not is traced once
+and broadcast (``map_b == 1`` / ``map_h == 1``), like the B/H arguments of the
+reference's ``create_block_mask``.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable, Optional, Tuple
+
+import numpy as np
+
+TILE = 128
+NUM_XCD = 8  # MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
+
+
+# ---------------------------------------------------------------------------
+# call canonicalisation (attention.py:385-437 and :195-217)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Plan:
+    B: int
+    N: int               # query length
+    L: int               # key length
+    Hq: int
+    Hkv: int
+    d: int
+    bs: int              # the reference's block size (query and key blocks)
+    Npad: int            # padded lengths the reference works on
+    Lpad: int
+    mask4: Callable      # canonical 4-argument mask (b, h, q, k)
+    window: Optional[Tuple[int, int]]  # (left blocks, right blocks) or None
+    squeeze_batch: bool  # inputs were 3-D
+
+
+def canonical_mask(is_causal: bool, mask_fn):
+    """attention.py:404-419: 3-argument masks ignore b; causal is q >= k."""
+    if mask_fn is not None and mask_fn.__code__.co_argcount == 3:
+        three = mask_fn
+        mask_fn = lambda b, h, q, k: three(h, q, k)  # noqa: E731
+    if is_causal and mask_fn is not None:
+        raise ValueError("cannot specify both 'is_causal' and 'mask_fn'!")
+    if is_causal:
+        mask_fn = _causal
+    if mask_fn is None:
+        mask_fn = _everything
+    return mask_fn
+
+
+def _causal(b, h, q, k):
+    return q >= k
+
+
+def _everything(b, h, q, k):
+    return True
+
+
+def make_plan(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, block_size=None,
+              window_size=None) -> Plan:
+    """Validation and set-up with the reference's exception types.
+
+    attention.py:385-391 (ndim -> ValueError), :394-399 (3-D inputs gain a batch
+    dim), :404-419 (mask), :421-437 (padding to a block multiple: Q by
+    bs - N % bs and K/V by bs - L % bs, a whole extra block when L % bs == 0),
+    :195-217 (block size, window blocks, shape asserts -> AssertionError).
+    """
+    for name, s in (("K", k_shape), ("Q", q_shape), ("V", v_shape)):
+        if len(s) not in (3, 4):
+            raise ValueError(f"{name} must have 3 or 4 dimensions")
+    assert len(k_shape) == len(q_shape) and len(v_shape) == len(q_shape), \
+        "Q, K, and V must have the same number of dimensions"
+    squeeze = len(q_shape) == 3
+    if squeeze:
+        q_shape, k_shape, v_shape = (1, *q_shape), (1, *k_shape), (1, *v_shape)
+    mask4 = canonical_mask(is_causal, mask_fn)
+    assert k_shape[0] == q_shape[0] == v_shape[0], "Q, K, and V must have the same batch dimension"
+    B, N, Hq, dq = q_shape
+    _, L, Hk, d = k_shape
+    _, Lv, Hv, dv = v_shape
+    Npad, Lpad = N, L
+    if block_size is not None and N % block_size != 0:
+        Npad = N + block_size - N % block_size
+        Lpad = L + block_size - L % block_size
+    bs = Npad if block_size is None else block_size
+    assert d == dq and Lv == L and dv == d, \
+        f"shape mismatch in K {tuple(k_shape)}, Q {tuple(q_shape)} and V {tuple(v_shape)}"
+    assert Hq % Hk == 0, "Hq must be divisible by Hk"
+    assert Hv == Hk, "Hv must be equal to Hk"
+    if Lpad % bs != 0:
+        # the reference's rearrange of K into blocks of the query block size fails here
+        raise RuntimeError(f"key length {Lpad} is not a multiple of the block size {bs}")
+    window = None
+    if window_size is not None:
+        left, right = window_size
+        lwb = (left + bs - 1) // bs
+        rwb = 1 + (right + bs - 1) // bs
+        if lwb + rwb > Lpad // bs:
+            # lax.dynamic_slice_in_dim rejects a slice longer than the operand
+            raise TypeError(f"window of {lwb + rwb} key blocks exceeds the {Lpad // bs} blocks present")
+        window = (lwb, rwb)
+    return Plan(B, N, L, Hq, Hk, d, bs, Npad, Lpad, mask4, window, squeeze)
+
+
+def window_key_range(plan: Plan, q: np.ndarray):
+    """[lo, hi) key range each query's block scans (attention.py:160-167).
+
+    The scan covers ``lwb + rwb`` key blocks starting at max(0, i - lwb), and
+    ``dynamic_slice_in_dim`` clamps that start into [0, nk - size]."""
+    lwb, rwb = plan.window
+    nk = plan.Lpad // plan.bs
+    i = q // plan.bs
+    start = np.minimum(np.maximum(0, i - lwb), nk - (lwb + rwb))
+    return start * plan.bs, (start + lwb + rwb) * plan.bs
+
+
+# ---------------------------------------------------------------------------
+# tile map
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class TileMap:
+    B: int
+    Hq: int
+    Hkv: int
+    Lq: int
+    Lk: int
+    map_b: int
+    map_h: int
+    nqt: int
+    nkt: int
+    row_ptr: np.ndarray     # int32 [map_b*map_h*nqt + 1]
+    row_ent: np.ndarray     # int32 [nnz, 2] (key tile, mask id)
+    col_ptr: np.ndarray     # int32 [map_b*map_h*nkt + 1]
+    col_ent: np.ndarray     # int32 [nnz, 2] (query tile, mask id)
+    row_bits: np.ndarray    # uint64 [n_masks, 128, 2]
+    col_bits: np.ndarray    # uint64 [n_masks, 128, 2]
+    q_order: np.ndarray     # int32 launch order of (b, h, query tile) items
+    kv_order: np.ndarray    # int32 launch order of (b, kv head, key tile) items
+    pairs: int              # allowed (b, h, q, k) positions over all B x Hq
+    n_full: int = 0         # present tiles of each kind, over the (broadcast) map
+    n_partial: int = 0
+    trace_seconds: float = 0.0
+    device: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def nnz(self) -> int:
+        return int(self.row_ent.shape[0])
+
+    @property
+    def n_masks(self) -> int:
+        return int(self.row_bits.shape[0])
+
+    def states(self) -> np.ndarray:
+        """int8 [map_b, map_h, nqt, nkt]: 0 skipped, 1 full, 2 partial."""
+        st = np.zeros((self.map_b * self.map_h * self.nqt, self.nkt), np.int8)
+        rows = np.repeat(np.arange(self.map_b * self.map_h * self.nqt), np.diff(self.row_ptr))
+        st[rows, self.row_ent[:, 0]] = np.where(self.row_ent[:, 1] < 0, 1, 2)
+        return st.reshape(self.map_b, self.map_h, self.nqt, self.nkt)
+
+    def dense(self) -> np.ndarray:
+        """The traced mask as bool [map_b, map_h, Lq, Lk] (for checking)."""
+        out = np.zeros((self.map_b * self.map_h * self.nqt, TILE, self.nkt * TILE), bool)
+        rows = np.repeat(np.arange(self.map_b * self.map_h * self.nqt), np.diff(self.row_ptr))
+        for r, (kt, mid) in zip(rows, self.row_ent):
+            if mid < 0:
+                out[r, :, kt * TILE:(kt + 1) * TILE] = True
+            else:
+                bits = np.unpackbits(self.row_bits[mid].view(np.uint8).reshape(TILE, 16), axis=1,
+                                     bitorder="little").astype(bool)
+                out[r, :, kt * TILE:(kt + 1) * TILE] = bits
+        out = out.reshape(self.map_b, self.map_h, self.nqt * TILE, self.nkt * TILE)
+        return out[:, :, :self.Lq, :self.Lk]
+
+
+def _probe_dependence(mask4, B, Hq, N, L):
+    """Which of (b, h) the mask's value can depend on, read off the broadcast
+    shape of one small evaluation."""
+    b = np.arange(B, dtype=np.int64)[:, None, None, None]
+    h = np.arange(Hq, dtype=np.int64)[None, :, None, None]
+    q = np.arange(min(N, 4), dtype=np.int64)[None, None, :, None]
+    k = np.arange(min(L, 4), dtype=np.int64)[None, None, None, :]
+    shape = np.shape(np.asarray(mask4(b, h, q, k)))
+    shape = (1,) * (4 - len(shape)) + tuple(shape)
+    return (B if shape[0] != 1 else 1), (Hq if shape[1] != 1 else 1)
+
+
+def _strip_mask(plan: Plan, map_b, map_h, q0, nkt):
+    """Effective mask of query rows [q0, q0+128): bool [map_b, map_h, 128, nkt*128]."""
+    rows = min(TILE, plan.N - q0)
+    b = np.arange(map_b, dtype=np.int64)[:, None, None, None]
+    h = np.arange(map_h, dtype=np.int64)[None, :, None, None]
+    q = np.arange(q0, q0 + rows, dtype=np.int64)[None, None, :, None]
+    k = np.arange(plan.L, dtype=np.int64)[None, None, None, :]
+    m = np.broadcast_to(np.asarray(plan.mask4(b, h, q, k), dtype=bool), (map_b, map_h, rows, plan.L))
+    if plan.window is not None:
+        lo, hi = window_key_range(plan, q[0, 0, :, 0])
+        kk = k[0, 0]
+        m = m & ((kk >= lo[:, None]) & (kk < hi[:, None]))[None, None]
+    out = np.zeros((map_b, map_h, TILE, nkt * TILE), bool)
+    out[:, :, :rows, :plan.L] = m
+    return out
+
+
+def _lpt_xcd_order(weights: np.ndarray, groups: np.ndarray) -> np.ndarray:
+    """Launch order of work items: items of one group (a (b, head) pair) are
+    kept on one XCD (workgroup i runs on XCD i % 8, so a group's K/V stay in
+    that die's L2), and inside each XCD the heaviest items go first (longest
+    processing time first).  Idle slots are -1."""
+    bins = [[] for _ in range(NUM_XCD)]
+    order = np.lexsort((np.arange(len(weights)), -weights))  # heavy first, stable
+    for it in order:
+        bins[int(groups[it]) % NUM_XCD].append(int(it))
+    width = max(len(b) for b in bins)
+    out = np.full((width, NUM_XCD), -1, np.int32)
+    for x, b in enumerate(bins):
+        out[:len(b), x] = b
+    return out.reshape(-1)
+
+
+def trace(plan: Plan) -> TileMap:
+    """Traces the effective mask of ``plan`` into a TileMap."""
+    import time
+
+    t0 = time.perf_counter()
+    B, Hq, Hkv, N, L = plan.B, plan.Hq, plan.Hkv, plan.N, plan.L
+    nqt, nkt = -(-N // TILE), -(-L // TILE)
+    map_b, map_h = _probe_dependence(plan.mask4, B, Hq, N, L)
+    nmap = map_b * map_h
+
+    masks: dict = {}
+    row_bits, col_bits = [], []
+    ent_row, ent_kt, ent_mid = [], [], []   # map row index, key tile, mask id
+    pairs_map = 0
+    n_full = n_partial = 0
+    for qt in range(nqt):
+        m = _strip_mask(plan, map_b, map_h, qt * TILE, nkt)
+        pairs_map += int(np.count_nonzero(m))
+        t = m.reshape(map_b, map_h, TILE, nkt, TILE)
+        anyb = t.any(axis=(2, 4))
+        allb = t.all(axis=(2, 4))
+        mb, mh, kt = np.nonzero(anyb)
+        if len(kt) == 0:
+            continue
+        full = allb[mb, mh, kt]
+        mids = np.full(len(kt), -1, np.int64)
+        part = np.nonzero(~full)[0]
+        if len(part):
+            tiles = t[mb[part], mh[part], :, kt[part], :]          # [P, 128 q, 128 k]
+            rb = np.ascontiguousarray(np.packbits(tiles, axis=2, bitorder="little")).view(np.uint64)
+            cb = np.ascontiguousarray(np.packbits(tiles.transpose(0, 2, 1), axis=2,
+                                                  bitorder="little")).view(np.uint64)  # [P,128,2]
+            for i, p in enumerate(part):
+                key = rb[i].tobytes()
+                mid = masks.get(key)
+                if mid is None:
+                    mid = len(row_bits)
+                    masks[key] = mid
+                    row_bits.append(rb[i])
+                    col_bits.append(cb[i])
+                mids[p] = mid
+        n_full += int(full.sum())
+        n_partial += int((~full).sum())
+        ent_row.append((mb * map_h + mh) * nqt + qt)
+        ent_kt.append(kt)
+        ent_mid.append(mids)
+
+    if ent_row:
+        r = np.concatenate(ent_row)
+        kt = np.concatenate(ent_kt)
+        mid = np.concatenate(ent_mid)
+    else:
+        r = kt = mid = np.zeros(0, np.int64)
+    o = np.lexsort((kt, r))                 # rows ascending, key tiles ascending
+    r, kt, mid = r[o], kt[o], mid[o]
+    row_ptr = np.zeros(nmap * nqt + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=nmap * nqt), out=row_ptr[1:])
+    row_ent = np.stack([kt, mid], axis=1).astype(np.int32).reshape(-1, 2)
+
+    mapi, qt_of = r // nqt, r % nqt
+    c = mapi * nkt + kt
+    oc = np.lexsort((qt_of, c))             # columns ascending, query tiles ascending
+    col_ptr = np.zeros(nmap * nkt + 1, np.int64)
+    np.cumsum(np.bincount(c, minlength=nmap * nkt), out=col_ptr[1:])
+    col_ent = np.stack([qt_of[oc], mid[oc]], axis=1).astype(np.int32).reshape(-1, 2)
+
+    # launch order (weights = present tiles per work item, +1 for the epilogue)
+    row_cnt = np.diff(row_ptr).reshape(map_b, map_h, nqt)
+    col_cnt = np.diff(col_ptr).reshape(map_b, map_h, nkt)
+    bi = np.arange(B) % map_b
+    hi = np.arange(Hq) % map_h
+    qw = row_cnt[bi][:, hi].reshape(B * Hq * nqt) + 1                  # item (b*Hq + h)*nqt + qt
+    qgroups = np.repeat(np.arange(B * Hq), nqt)
+    G = Hq // Hkv
+    cc = col_cnt[bi][:, hi]                                            # [B, Hq, nkt]
+    kvw = cc.reshape(B, Hkv, G, nkt).sum(axis=2).reshape(B * Hkv * nkt) + 1
+    kvgroups = np.repeat(np.arange(B * Hkv), nkt)
+    q_order = _lpt_xcd_order(qw, qgroups)
+    kv_order = _lpt_xcd_order(kvw, kvgroups)
+
+    pairs = pairs_map * (B // map_b) * (Hq // map_h)
+    rb = np.stack(row_bits) if row_bits else np.zeros((0, TILE, 2), np.uint64)
+    cb = np.stack(col_bits) if col_bits else np.zeros((0, TILE, 2), np.uint64)
+    return TileMap(B, Hq, Hkv, N, L, map_b, map_h, nqt, nkt,
+                   row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent,
+                   np.ascontiguousarray(rb), np.ascontiguousarray(cb), q_order, kv_order, pairs,
+                   n_full=n_full, n_partial=n_partial, trace_seconds=time.perf_counter() - t0)
+
+
+def flops(tm: TileMap, d: int):
+    """Algorithmic FLOPs counted on unmasked pairs: fwd 4*d*pairs, bwd 10*d*pairs."""
+    return 4 * d * tm.pairs, 10 * d * tm.pairs

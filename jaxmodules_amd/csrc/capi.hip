@@ -1,0 +1,207 @@
+// C ABI of the library (declared in include/mattn.h): argument validation,
+// kernel-argument packing and launch selection.  Host code only; the kernels
+// live in fwd.hip and bwd.hip.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace mattn {
+hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st);
+hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,
+                            int kv_grid, hipStream_t st);
+}  // namespace mattn
+
+using namespace mattn;
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool strides_ok(const int64_t s[3], int esz) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] * esz) % 16 != 0) return false;
+  return true;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Backward workspace: delta (f32 per query row), the partial maxima of |dO|
+// and the scale pair, dO * s in float16, and (bfloat16 inputs) dO in bfloat16.
+struct WsLayout {
+  size_t delta, part, scale, doh, do16, total;
+};
+
+WsLayout ws_layout(const mattn_problem* p) {
+  const size_t rows = (size_t)p->B * p->Hq * p->Lq;
+  WsLayout w{};
+  w.delta = 0;
+  w.part = align256(rows * sizeof(float));
+  w.scale = w.part + align256(NPART * sizeof(float));
+  w.doh = w.scale + 256;
+  w.do16 = w.doh + (p->dtype == MATTN_F32 ? 0 : align256(rows * p->D * 2));
+  w.total = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
+  return w;
+}
+
+KArgs make_args(const mattn_problem* p, const mattn_blockmap* bm) {
+  KArgs a{};
+  for (int i = 0; i < 3; ++i) {
+    a.qs[i] = p->q_stride[i];
+    a.ks[i] = p->k_stride[i];
+    a.vs[i] = p->v_stride[i];
+    a.os[i] = p->o_stride[i];
+    a.dos[i] = p->do_stride[i];
+    a.dqs[i] = p->dq_stride[i];
+    a.dks[i] = p->dk_stride[i];
+    a.dvs[i] = p->dv_stride[i];
+  }
+  a.B = p->B;
+  a.Lq = p->Lq;
+  a.Lk = p->Lk;
+  a.Hq = p->Hq;
+  a.Hkv = p->Hkv;
+  a.G = p->Hq / p->Hkv;
+  a.scale = p->scale;
+  a.scale_log2 = p->scale * 1.4426950408889634f;
+  a.map_b = bm->map_b;
+  a.map_h = bm->map_h;
+  a.nqt = bm->nqt;
+  a.nkt = bm->nkt;
+  a.row_ptr = bm->row_ptr;
+  a.row_ent = bm->row_ent;
+  a.col_ptr = bm->col_ptr;
+  a.col_ent = bm->col_ent;
+  a.row_bits = bm->row_bits;
+  a.col_bits = bm->col_bits;
+  a.q_order = bm->q_order;
+  a.kv_order = bm->kv_order;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mattn_abi_version(void) { return kAbiVersion; }
+
+const char* mattn_strerror(int status) {
+  switch (status) {
+    case MATTN_OK: return "success";
+    case MATTN_ERR_NULL: return "a required pointer is NULL";
+    case MATTN_ERR_SHAPE: return "invalid shape (sizes must be positive and Hq divisible by Hkv)";
+    case MATTN_ERR_HEAD_DIM: return "unsupported head dimension (supported: 64, 128)";
+    case MATTN_ERR_DTYPE: return "unsupported dtype combination";
+    case MATTN_ERR_STRIDE: return "pointer or stride not 16-byte aligned";
+    case MATTN_ERR_BLOCKMAP: return "block map inconsistent with the problem";
+    case MATTN_ERR_LAUNCH: return "kernel launch failed";
+    case MATTN_ERR_TOO_LARGE: return "problem exceeds 32-bit index ranges";
+    default: return "unknown status";
+  }
+}
+
+int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
+  if (!p) return MATTN_ERR_NULL;
+  if (p->B <= 0 || p->Lq <= 0 || p->Lk <= 0 || p->Hq <= 0 || p->Hkv <= 0 || p->D <= 0)
+    return MATTN_ERR_SHAPE;
+  if (p->Hq % p->Hkv != 0) return MATTN_ERR_SHAPE;
+  if (p->D != 64 && p->D != 128) return MATTN_ERR_HEAD_DIM;
+  if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
+  if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
+  if (!(p->scale == p->scale) || isinf(p->scale)) return MATTN_ERR_SHAPE;
+  const int es = elem_size(p->dtype), eo = elem_size(p->o_dtype);
+  if (!strides_ok(p->q_stride, es) || !strides_ok(p->k_stride, es) || !strides_ok(p->v_stride, es) ||
+      !strides_ok(p->dq_stride, es) || !strides_ok(p->dk_stride, es) ||
+      !strides_ok(p->dv_stride, es) || !strides_ok(p->o_stride, eo) || !strides_ok(p->do_stride, eo))
+    return MATTN_ERR_STRIDE;
+  const int64_t nqt = cdiv(p->Lq, MATTN_TILE_Q), nkt = cdiv(p->Lk, MATTN_TILE_K);
+  if ((int64_t)p->B * p->Hq * nqt >= (1ll << 31) || (int64_t)p->B * p->Hkv * nkt >= (1ll << 31) ||
+      (int64_t)p->Lq + MATTN_TILE_Q >= (1ll << 31) || (int64_t)p->Lk + MATTN_TILE_K >= (1ll << 31))
+    return MATTN_ERR_TOO_LARGE;
+  if (!bm) return MATTN_OK;
+  if (bm->nqt != nqt || bm->nkt != nkt) return MATTN_ERR_BLOCKMAP;
+  if (!(bm->map_b == 1 || bm->map_b == p->B) || !(bm->map_h == 1 || bm->map_h == p->Hq))
+    return MATTN_ERR_BLOCKMAP;
+  if (bm->n_masks < 0 || bm->nnz < 0 || bm->n_q_order <= 0 || bm->n_kv_order <= 0)
+    return MATTN_ERR_BLOCKMAP;
+  if (bm->n_q_order < p->B * p->Hq * nqt || bm->n_kv_order < p->B * p->Hkv * nkt)
+    return MATTN_ERR_BLOCKMAP;
+  if (!bm->row_ptr || !bm->col_ptr || !bm->q_order || !bm->kv_order) return MATTN_ERR_NULL;
+  if (bm->nnz > 0 && (!bm->row_ent || !bm->col_ent)) return MATTN_ERR_NULL;
+  if (bm->n_masks > 0 && (!bm->row_bits || !bm->col_bits)) return MATTN_ERR_NULL;
+  return MATTN_OK;
+}
+
+size_t mattn_workspace_bytes(const mattn_problem* p) {
+  if (mattn_validate(p, nullptr) != MATTN_OK) return 0;
+  return ws_layout(p).total;
+}
+
+int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
+              const void* v, void* o, float* lse, void* stream) {
+  int rc = mattn_validate(p, bm);
+  if (rc != MATTN_OK) return rc;
+  if (!bm) return MATTN_ERR_NULL;
+  if (!q || !k || !v || !o || !lse) return MATTN_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MATTN_ERR_STRIDE;
+  KArgs a = make_args(p, bm);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = o;
+  a.lse = lse;
+  hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, bm->n_q_order, (hipStream_t)stream);
+  return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
+}
+
+int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage, const void* q,
+                    const void* k, const void* v, const void* o, const void* do_, const float* lse,
+                    void* workspace, void* dq, void* dk, void* dv, void* stream) {
+  int rc = mattn_validate(p, bm);
+  if (rc != MATTN_OK) return rc;
+  if (!bm) return MATTN_ERR_NULL;
+  if (stage != MATTN_BWD_PRE && stage != MATTN_BWD_DKDV && stage != MATTN_BWD_DQ) return MATTN_ERR_SHAPE;
+  if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
+      !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u))
+    return MATTN_ERR_STRIDE;
+  KArgs a = make_args(p, bm);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.dO = do_;
+  a.lse = const_cast<float*>(lse);
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  const WsLayout w = ws_layout(p);
+  char* ws = (char*)workspace;
+  a.delta = (float*)(ws + w.delta);
+  a.part = (float*)(ws + w.part);
+  a.dscale = (float*)(ws + w.scale);
+  a.dOhw = ws + w.doh;
+  a.dOh = a.dOhw;
+  a.dO16w = ws + w.do16;
+  a.dO16 = a.dO16w;
+  hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
+                                  bm->n_kv_order, (hipStream_t)stream);
+  return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
+}
+
+int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
+              const void* v, const void* o, const void* do_, const float* lse, void* workspace,
+              void* dq, void* dk, void* dv, void* stream) {
+  for (int stage = MATTN_BWD_PRE; stage <= MATTN_BWD_DQ; ++stage) {
+    const int rc = mattn_bwd_stage(p, bm, stage, q, k, v, o, do_, lse, workspace, dq, dk, dv, stream);
+    if (rc != MATTN_OK) return rc;
+  }
+  return MATTN_OK;
+}
+
+}  // extern "C"

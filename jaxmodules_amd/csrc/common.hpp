@@ -1,0 +1,151 @@
+// Shared definitions of the gfx950 masked-attention kernels.
+//
+// Tile vocabulary (all kernels):
+//   * map tile   : 128 queries x 128 keys, the granularity of the block map
+//                  (mattn_blockmap in include/mattn.h);
+//   * sub-block  : 64 keys (forward, dQ) or 64 queries (dK/dV), the unit one
+//                  pipeline stage stages through LDS;
+//   * MFMA tile  : 32 x 32 outputs of v_mfma_f32_32x32x16_{bf16,f16}.
+//
+// MFMA 32x32x16 operand layout (lane l, l32 = l % 32, hi = l / 32):
+//   A[32 x 16]: lane holds row l32, k = 8*hi .. 8*hi+7   (16 contiguous bytes)
+//   B[16 x 32]: lane holds col l32, k = 8*hi .. 8*hi+7
+//   C[32 x 32]: lane holds col l32, register r holds row 8*(r/4) + 4*hi + r%4
+// A C-tile's registers [8*j, 8*j+8) of lane (l32, hi) therefore cover rows
+// 16*j + {0..3, 8..11} (hi = 0) or 16*j + {4..7, 12..15} (hi = 1): exactly
+// the 8 values a B (or A) operand of the next product needs for a 16-deep
+// k-step, provided the matching operand is read with the same row
+// permutation.  Transposed LDS buffers store rows in that permuted order
+// (tslot) so that each lane's 8 operand values are one 16-byte read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mattn.h"
+
+namespace mattn {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int TILE = 128;  // map tile edge (MATTN_TILE_Q == MATTN_TILE_K)
+constexpr int NPART = 512;  // workgroups of the max |dO| pass
+constexpr float NEG_INF = -__builtin_inff();
+
+// Arguments of every kernel (passed by value in the kernarg segment).
+struct KArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;     // forward output (read by the backward preprocess)
+  const void* dO;    // upstream gradient in o_dtype
+  const void* dO16;  // upstream gradient in bfloat16 (workspace; bf16 inputs only)
+  const void* dOh;   // upstream gradient * dscale[0] in float16 (workspace)
+  float* dscale;     // [2] (s, 1/s): power-of-two scale of dOh (workspace)
+  float* part;       // [NPART] partial max |dO| (workspace)
+  void* out;         // forward output O
+  float* lse;        // [B, Hq, Lq] base-2 log-sum-exp
+  float* delta;      // [B, Hq, Lq] rowsum(dO * O) (workspace)
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dO16w;       // writable aliases for the preprocess kernel
+  void* dOhw;
+  int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3];
+  int B, Lq, Lk, Hq, Hkv, G;
+  float scale;       // softmax scale
+  float scale_log2;  // scale * log2(e)
+  int map_b, map_h, nqt, nkt;
+  const int* row_ptr;
+  const int* row_ent;
+  const int* col_ptr;
+  const int* col_ent;
+  const uint64_t* row_bits;
+  const uint64_t* col_bits;
+  const int* q_order;
+  const int* kv_order;
+};
+
+struct bf16_tag {};
+struct f16_tag {};
+
+template <class Tag>
+struct Elt;
+
+template <>
+struct Elt<bf16_tag> {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32)
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint32_t bits16) {
+    return __builtin_bit_cast(float, bits16 << 16);
+  }
+};
+
+template <>
+struct Elt<f16_tag> {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-bit element j (0..7) of a 16-byte chunk.
+__device__ __forceinline__ uint32_t elt16(const u32x4& x, int j) {
+  return (x[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
+}
+
+// Permuted position of row r (0..63) of a sub-block inside a transposed row:
+// within every group of 16, rows {0-3, 8-11, 4-7, 12-15} are stored in that
+// order (bits 2 and 3 swapped), so the 8 rows one lane's C registers hold for
+// a 16-deep k-step are contiguous.
+__device__ __forceinline__ int tslot(int r) {
+  const int w = r & 15;
+  return (r & ~15) | (w & 3) | ((w & 4) << 1) | ((w & 8) >> 1);
+}
+
+// Element offset of (row d, slot s) in a transposed [D][64] LDS buffer of
+// 16-bit values.  Each 128-byte row is 8 chunks of 16 bytes; the chunk index is
+// XOR-swizzled with d % 8 so that 8 lanes reading consecutive d at the same
+// slot, and 16 lanes writing consecutive slots of one d, hit distinct banks.
+__device__ __forceinline__ int tpos(int d, int s) {
+  return d * 64 + ((((s >> 3) ^ (d & 7))) << 3) + (s & 7);
+}
+
+// Offset of the 16-byte operand chunk for k-step ks (16 rows) and lane half hi.
+__device__ __forceinline__ int tchunk(int d, int ks, int hi) {
+  return d * 64 + (((2 * ks + hi) ^ (d & 7)) << 3);
+}
+
+__device__ __forceinline__ float wave_max32(float x) {
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int t) {
+  return ((a.map_b == 1 ? 0 : b) * a.map_h + (a.map_h == 1 ? 0 : h)) * n + t;
+}
+
+}  // namespace mattn

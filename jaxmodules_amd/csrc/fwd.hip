@@ -1,0 +1,311 @@
+// Forward pass of the masked attention (the custom_vjp primal,
+// /root/reference/jaxmodules/attention.py:180-241, per-tile maths :52-105).
+//
+// One workgroup (4 waves) owns a 128-query map row of one (b, h) and walks the
+// row's present key tiles from the block map; fully masked tiles are never
+// visited.  Each wave owns 32 queries and computes, per 64-key sub-block,
+//     S^T = K Q^T        (MFMA, K from LDS, Q^T kept in registers)
+//     online softmax     (each lane owns one query, so the row max needs one
+//                         cross-lane exchange and the row sum none)
+//     O^T += V^T P^T     (MFMA, V^T from a transposed LDS copy)
+// K and V^T are double-buffered in LDS; the next sub-block's global loads are
+// in flight while the current one is computed.
+#include "common.hpp"
+
+namespace mattn {
+
+template <int D, class Tag, bool OUT_F32>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+void fwd_mfma(KArgs a) {
+  using E = Elt<Tag>;
+  constexpr int BN = 64;           // keys per sub-block
+  constexpr int KP = D + 8;        // padded K row pitch (elements)
+  constexpr int NKD = D / 16;      // k-steps of S^T over the head dimension
+  constexpr int NMD = D / 32;      // M-tiles of O^T over the head dimension
+  constexpr int CH = D / 8;        // 16-byte chunks per row
+  constexpr int KRP = 256 / CH;    // K rows one pass of the workgroup loads
+  constexpr int KPASS = BN / KRP;  // K passes per sub-block
+  constexpr int KG = BN * CH / 256;  // consecutive V rows per thread (4 or 2)
+  constexpr int NKG = BN / KG;       // V row groups per sub-block
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * BN];
+
+  const int item = a.q_order[blockIdx.x];
+  if (item < 0) return;
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int nsb = 2 * (e1 - e0);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int qloc = wave * 32 + l32;
+  const int q = qt * TILE + qloc;
+  const int qc = min(q, a.Lq - 1);
+
+  // Q^T operands: lane holds query q, head dims 16*kd + 8*hi .. +7.
+  u32x4 qf[NKD];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
+                         (int64_t)h * a.qs[2] + 8 * hi;
+#pragma unroll
+    for (int kd = 0; kd < NKD; ++kd) qf[kd] = *(const u32x4*)(qp + 16 * kd);
+  }
+
+  const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
+  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
+  const int kc = tid % CH, kr0 = tid / CH;       // K loader: chunk, first row
+  const int vg = tid % NKG, vc = tid / NKG;      // V loader: row group, chunk
+
+  u32x4 kreg[KPASS], vreg[KG];
+  auto load = [&](int s) {
+    const int kt = a.row_ent[2 * (e0 + (s >> 1))];
+    const int key0 = kt * TILE + (s & 1) * BN;
+#pragma unroll
+    for (int i = 0; i < KPASS; ++i) {
+      const int key = min(key0 + kr0 + KRP * i, a.Lk - 1);
+      kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * kc);
+    }
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      const int key = min(key0 + vg * KG + i, a.Lk - 1);
+      vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * vc);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPASS; ++i) *(u32x4*)&Ks[buf][(kr0 + KRP * i) * KP + 8 * kc] = kreg[i];
+    const int s0 = tslot(vg * KG);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 8 * vc + j;
+      if constexpr (KG == 4) {
+        u32x2 w = {elt16(vreg[0], j) | (elt16(vreg[1], j) << 16),
+                   elt16(vreg[2], j) | (elt16(vreg[3], j) << 16)};
+        *(u32x2*)&Vt[buf][tpos(d, s0)] = w;
+      } else {
+        *(uint32_t*)&Vt[buf][tpos(d, s0)] = elt16(vreg[0], j) | (elt16(vreg[1], j) << 16);
+      }
+    }
+  };
+
+  f32x16 acc[NMD];
+#pragma unroll
+  for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
+  float m = NEG_INF, l = 0.f;
+
+  if (nsb > 0) load(0);
+  for (int s = 0; s < nsb; ++s) {
+    const int buf = s & 1;
+    store(buf);
+    __syncthreads();
+    const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
+    uint64_t mw = ~0ull;
+    if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
+    if (s + 1 < nsb) load(s + 1);
+
+    f32x16 st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      st[t] = f32x16{};
+      const uint16_t* kp = &Ks[buf][(32 * t + l32) * KP + 8 * hi];
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(*(const u32x4*)(kp + 16 * kd), qf[kd], st[t]);
+    }
+
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = st[t][r] * a.scale_log2;
+        if (mask >= 0) {
+          const int kk = 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if (!((mw >> kk) & 1ull)) x = NEG_INF;
+        }
+        st[t][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = wave_max32(mx);
+    const float mn = fmaxf(m, mx);
+    const float mu = (mn == NEG_INF) ? 0.f : mn;
+    const float alpha = fast_exp2(m - mu);
+    m = mn;
+    float ls = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(st[t][r] - mu);
+        st[t][r] = p;
+        ls += p;
+      }
+    }
+    l = l * alpha + ls;
+#pragma unroll
+    for (int i = 0; i < NMD; ++i) acc[i] *= alpha;
+
+    u32x4 pk[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pk[ks][i] = E::pack2(st[ks >> 1][8 * (ks & 1) + 2 * i], st[ks >> 1][8 * (ks & 1) + 2 * i + 1]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMD; ++mt) {
+      const int d = 32 * mt + l32;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        acc[mt] = E::mfma(*(const u32x4*)&Vt[buf][tchunk(d, ks, hi)], pk[ks], acc[mt]);
+    }
+  }
+
+  l += __shfl_xor(l, 32);
+  if (q >= a.Lq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (hi == 0)
+    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + __builtin_log2f(l) : NEG_INF;
+  char* op = (char*)a.out;
+  const int64_t orow = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2];
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * mt + 8 * j + 4 * hi;
+      const float o0 = acc[mt][4 * j] * inv, o1 = acc[mt][4 * j + 1] * inv;
+      const float o2 = acc[mt][4 * j + 2] * inv, o3 = acc[mt][4 * j + 3] * inv;
+      if constexpr (OUT_F32) {
+        *(f32x4*)(op + 4 * (orow + d)) = f32x4{o0, o1, o2, o3};
+      } else {
+        *(u32x2*)(op + 2 * (orow + d)) = u32x2{E::pack2(o0, o1), E::pack2(o2, o3)};
+      }
+    }
+  }
+}
+
+// float32 forward (SIMT, no MFMA): 512 threads own the 128 queries of a map
+// row, 4 threads per query, each holding D/4 head dims.  Used for float32
+// inputs, whose tolerance (1e-5) rules out 16-bit operands.
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
+void fwd_simt(KArgs a) {
+  constexpr int SB = 32;     // keys per sub-block
+  constexpr int DP = D / 4;  // dims per thread
+  __shared__ __attribute__((aligned(16))) float Ks[SB * D];
+  __shared__ __attribute__((aligned(16))) float Vs[SB * D];
+
+  const int item = a.q_order[blockIdx.x];
+  if (item < 0) return;
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int tid = threadIdx.x, row = tid >> 2, part = tid & 3;
+  const int q = qt * TILE + row;
+  const int qc = min(q, a.Lq - 1);
+
+  float qv[DP], ov[DP];
+  {
+    const float* qp = (const float*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
+                      (int64_t)h * a.qs[2] + part * DP;
+#pragma unroll
+    for (int i = 0; i < DP; i += 4) {
+      const f32x4 x = *(const f32x4*)(qp + i);
+      qv[i] = x[0]; qv[i + 1] = x[1]; qv[i + 2] = x[2]; qv[i + 3] = x[3];
+      ov[i] = ov[i + 1] = ov[i + 2] = ov[i + 3] = 0.f;
+    }
+  }
+  const float* kb = (const float*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
+  const float* vb = (const float*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
+  float m = NEG_INF, l = 0.f;
+
+  for (int e = e0; e < e1; ++e) {
+    const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
+    for (int sb = 0; sb < TILE / SB; ++sb) {
+      const int key0 = kt * TILE + sb * SB;
+      if (key0 >= a.Lk) break;
+      __syncthreads();
+      for (int c = tid; c < SB * D / 4; c += 512) {
+        const int r = c / (D / 4), col = 4 * (c % (D / 4));
+        const int key = min(key0 + r, a.Lk - 1);
+        *(f32x4*)&Ks[r * D + col] = *(const f32x4*)(kb + (int64_t)key * a.ks[1] + col);
+        *(f32x4*)&Vs[r * D + col] = *(const f32x4*)(vb + (int64_t)key * a.vs[1] + col);
+      }
+      __syncthreads();
+      uint32_t bits = 0xffffffffu;
+      if (mask >= 0)
+        bits = (uint32_t)(a.row_bits[((int64_t)mask * TILE + row) * 2 + (sb >> 1)] >> (32 * (sb & 1)));
+      float sc[SB];
+      float mx = NEG_INF;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        float p = 0.f;
+#pragma unroll
+        for (int i = 0; i < DP; ++i) p = fmaf(qv[i], Ks[j * D + part * DP + i], p);
+        p += __shfl_xor(p, 1);
+        p += __shfl_xor(p, 2);
+        float x = p * a.scale_log2;
+        if (!((bits >> j) & 1u)) x = NEG_INF;
+        sc[j] = x;
+        mx = fmaxf(mx, x);
+      }
+      const float mn = fmaxf(m, mx);
+      const float mu = (mn == NEG_INF) ? 0.f : mn;
+      const float alpha = exp2f(m - mu);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < DP; ++i) ov[i] *= alpha;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float p = exp2f(sc[j] - mu);
+        l += p;
+#pragma unroll
+        for (int i = 0; i < DP; ++i) ov[i] = fmaf(p, Vs[j * D + part * DP + i], ov[i]);
+      }
+    }
+  }
+  if (q >= a.Lq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (part == 0) a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + log2f(l) : NEG_INF;
+  float* op = (float*)a.out + (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] +
+              part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; i += 4)
+    *(f32x4*)(op + i) = f32x4{ov[i] * inv, ov[i + 1] * inv, ov[i + 2] * inv, ov[i + 3] * inv};
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+template <int D, class Tag>
+static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStream_t st) {
+  if (out_f32)
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, false>), dim3(grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st) {
+  const bool of32 = (o_dtype == MATTN_F32);
+  if (dtype == MATTN_F32) {
+    if (D == 64) hipLaunchKernelGGL((fwd_simt<64>), dim3(grid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((fwd_simt<128>), dim3(grid), dim3(512), 0, st, a);
+    return hipGetLastError();
+  }
+  if (dtype == MATTN_BF16)
+    return D == 64 ? launch_fwd_mfma<64, bf16_tag>(a, grid, of32, st)
+                   : launch_fwd_mfma<128, bf16_tag>(a, grid, of32, st);
+  return D == 64 ? launch_fwd_mfma<64, f16_tag>(a, grid, of32, st)
+                 : launch_fwd_mfma<128, f16_tag>(a, grid, of32, st);
+}
+
+}  // namespace mattn

@@ -367,3 +367,23 @@ def test_block_size_invariance():
 def test_count_pairs_causal_closed_form():
     plan = ao.canonical_plan((2, 128, 8, 64), (2, 128, 8, 64), (2, 128, 8, 64), is_causal=True, block_size=32)
     assert ao.count_pairs(ao.effective_mask(plan)) == 2 * 8 * 128 * 129 // 2 == 132096
+
+
+def test_oracle_rounding_floor():
+    """Why the parity gate carries a half-ulp output-rounding term: the fp64
+    exact result, correctly rounded to bfloat16, violates the bare
+    |a - b| <= 2e-3 + 2e-3 |b| for values in [2, 2.9) that fall near the middle
+    between two bfloat16 neighbours (spacing 2^-6 there), and passes once half
+    an ulp of the output dtype is allowed."""
+    from tests.helpers import half_ulp
+
+    b = np.array([2.0 + 2 ** -7 - 1e-6, -(2.5 + 2 ** -7 - 1e-6), 0.75 + 1e-5, 1e-3])
+    r = torch.tensor(b, dtype=torch.float32).to(torch.bfloat16).double().numpy()
+    err = np.abs(r - b)
+    bare = 2e-3 + 2e-3 * np.abs(b)
+    assert (err > bare).any()
+    assert (err <= bare + half_ulp(b, "bfloat16")).all()
+    # half_ulp is exactly the RNE bound: 2^(e-8) for bf16, 2^(e-11) for fp16
+    assert half_ulp(np.array([1.0, 3.0, 0.3]), "bfloat16").tolist() == [2 ** -8, 2 ** -7, 2 ** -10]
+    assert half_ulp(np.array([1.0, 3.0]), "float16").tolist() == [2 ** -11, 2 ** -10]
+    assert half_ulp(np.array([5.0]), "float32").tolist() == [0.0]
