@@ -147,13 +147,15 @@ void bwd_pre(KArgs a) {
 //   dP^T = V dO^T        (A: V rows from LDS, B: dO^T in registers)
 //   dS^T = P^T * (dP^T - delta)    (each lane owns one query: lse, delta scalars)
 //   dQ^T += K^T dS^T     (A: K^T from a transposed LDS copy)
+// K, V and K^T are double-buffered in LDS.  K is loaded twice per sub-block:
+// row-major by a coalesced mapping, and four rows per thread for the
+// transposed copy.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bwd_dq_mfma(KArgs a) {
   using E = Elt<Tag>;
   constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BN = 64;
-  constexpr int KP = D + 8;
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
   constexpr int CH = D / 8;
@@ -161,10 +163,11 @@ void bwd_dq_mfma(KArgs a) {
   constexpr int KPASS = BN / KRP;
   constexpr int KG = BN * CH / 256;
   constexpr int NKG = BN / KG;
+  constexpr int P = D + 8;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * P];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * P];
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[2][D * BN];
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0) return;
@@ -180,6 +183,7 @@ void bwd_dq_mfma(KArgs a) {
   const int qloc = wave * 32 + l32;
   const int q = qt * TILE + qloc;
   const int qc = min(q, a.Lq - 1);
+  const float c2 = a.scale_log2;
 
   u32x4 qf[NKD], df[NKD];
   {
@@ -195,102 +199,126 @@ void bwd_dq_mfma(KArgs a) {
     }
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
-  const float lse = a.lse[rs];
+  const float nlse = -a.lse[rs];
   const float dl = a.delta[rs];
   const float dps = IS_BF16 ? 1.f : a.dscale[1];  // undoes the dO scale of float16 inputs
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  const int vc_ = tid % CH, vr0 = tid / CH;    // V loader (row-major, coalesced)
-  const int kg = tid % NKG, kc = tid / NKG;    // K loader (feeds K and K^T)
+  const int rc = tid % CH, rr0 = tid / CH;    // coalesced loader: chunk, first row
+  const int tg = tid % NKG, tc = tid / NKG;   // transposed loader: row group, chunk
+  uint32_t koff[KPASS], voff[KPASS], toff[KG];
+#pragma unroll
+  for (int i = 0; i < KPASS; ++i) {
+    koff[i] = (uint32_t)((rr0 + KRP * i) * a.ks[1] + 8 * rc);
+    voff[i] = (uint32_t)((rr0 + KRP * i) * a.vs[1] + 8 * rc);
+  }
+#pragma unroll
+  for (int i = 0; i < KG; ++i) toff[i] = (uint32_t)((tg * KG + i) * a.ks[1] + 8 * tc);
 
-  u32x4 kreg[KG], vreg[KPASS];
+  u32x4 kreg[KPASS], vreg[KPASS], treg[KG];
   auto load = [&](int s) {
     const int kt = a.row_ent[2 * (e0 + (s >> 1))];
     const int key0 = kt * TILE + (s & 1) * BN;
+    const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];
+    const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
+    if (key0 + BN <= a.Lk) {
 #pragma unroll
-    for (int i = 0; i < KG; ++i) {
-      const int key = min(key0 + kg * KG + i, a.Lk - 1);
-      kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * kc);
-    }
+      for (int i = 0; i < KPASS; ++i) {
+        kreg[i] = *(const u32x4*)(kp + koff[i]);
+        vreg[i] = *(const u32x4*)(vp + voff[i]);
+      }
 #pragma unroll
-    for (int i = 0; i < KPASS; ++i) {
-      const int key = min(key0 + vr0 + KRP * i, a.Lk - 1);
-      vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * vc_);
-    }
-  };
-  auto store = [&]() {
+      for (int i = 0; i < KG; ++i) treg[i] = *(const u32x4*)(kp + toff[i]);
+    } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
 #pragma unroll
-    for (int i = 0; i < KPASS; ++i) *(u32x4*)&Vs[(vr0 + KRP * i) * KP + 8 * vc_] = vreg[i];
+      for (int i = 0; i < KPASS; ++i) {
+        const int key = min(key0 + rr0 + KRP * i, a.Lk - 1);
+        kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * rc);
+        vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * rc);
+      }
 #pragma unroll
-    for (int i = 0; i < KG; ++i) *(u32x4*)&Ks[(kg * KG + i) * KP + 8 * kc] = kreg[i];
-    const int s0 = tslot(kg * KG);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 8 * kc + j;
-      if constexpr (KG == 4) {
-        u32x2 w = {elt16(kreg[0], j) | (elt16(kreg[1], j) << 16),
-                   elt16(kreg[2], j) | (elt16(kreg[3], j) << 16)};
-        *(u32x2*)&Kt[tpos(d, s0)] = w;
-      } else {
-        *(uint32_t*)&Kt[tpos(d, s0)] = elt16(kreg[0], j) | (elt16(kreg[1], j) << 16);
+      for (int i = 0; i < KG; ++i) {
+        const int key = min(key0 + tg * KG + i, a.Lk - 1);
+        treg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * tc);
       }
     }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPASS; ++i) {
+      *(u32x4*)&Ks[buf][rm_off<D>(rr0 + KRP * i, rc)] = kreg[i];
+      *(u32x4*)&Vs[buf][rm_off<D>(rr0 + KRP * i, rc)] = vreg[i];
+    }
+    tr_write<KG>(Kt[buf], treg, tg * KG, tc);
   };
 
   f32x16 acc[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
 
-  if (nsb > 0) load(0);
-  for (int s = 0; s < nsb; ++s) {
-    __syncthreads();  // the previous sub-block's readers are done
-    store();
-    __syncthreads();
-    const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
-    uint64_t mw = ~0ull;
-    if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
-    if (s + 1 < nsb) load(s + 1);
-
+  auto step = [&](int buf, bool masked, uint64_t mw) {
     f32x16 st[2], dp[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      st[t] = f32x16{};
-      dp[t] = f32x16{};
-      const uint16_t* kp = &Ks[(32 * t + l32) * KP + 8 * hi];
-      const uint16_t* vp = &Vs[(32 * t + l32) * KP + 8 * hi];
+      u32x4 ka[NKD], va[NKD];
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) {
-        st[t] = E::mfma(*(const u32x4*)(kp + 16 * kd), qf[kd], st[t]);
-        dp[t] = E::mfma(*(const u32x4*)(vp + 16 * kd), df[kd], dp[t]);
+        ka[kd] = *(const u32x4*)&Ks[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+        va[kd] = *(const u32x4*)&Vs[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+      }
+      st[t] = f32x16{};
+      dp[t] = f32x16{};
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd) {
+        st[t] = E::mfma(ka[kd], qf[kd], st[t]);
+        dp[t] = E::mfma(va[kd], df[kd], dp[t]);
       }
     }
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(st[t][r] * a.scale_log2 - lse);
-        if (mask >= 0) {
-          const int kk = 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
-          if (!((mw >> kk) & 1ull)) p = 0.f;
-        }
-        st[t][r] = p * (dp[t][r] * dps - dl);
+      for (int r = 0; r < 16; ++r) st[t][r] = fast_exp2(fmaf(st[t][r], c2, nlse));
+    if (masked) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!mask_bit(w32, r)) st[t][r] = 0.f;
       }
     }
     u32x4 pk[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pk[ks][i] = E::pack2(st[ks >> 1][8 * (ks & 1) + 2 * i], st[ks >> 1][8 * (ks & 1) + 2 * i + 1]);
+      for (int r = 0; r < 16; r += 2) {
+        const float d0 = st[t][r] * fmaf(dp[t][r], dps, -dl);
+        const float d1 = st[t][r + 1] * fmaf(dp[t][r + 1], dps, -dl);
+        pk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(d0, d1);
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
       const int d = 32 * mt + l32;
+      u32x4 ta[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc[mt] = E::mfma(*(const u32x4*)&Kt[tchunk(d, ks, hi)], pk[ks], acc[mt]);
+      for (int ks = 0; ks < 4; ++ks) ta[ks] = *(const u32x4*)&Kt[buf][tchunk(d, ks, hi)];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc[mt] = E::mfma(ta[ks], pk[ks], acc[mt]);
     }
+  };
+
+  if (nsb > 0) load(0);
+  for (int s = 0; s < nsb; ++s) {
+    const int buf = s & 1;
+    store(buf);
+    __syncthreads();
+    const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
+    uint64_t mw = 0;
+    if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
+    if (s + 1 < nsb) load(s + 1);
+    step(buf, mask >= 0, mw);
   }
 
   if (q >= a.Lq) return;
@@ -315,9 +343,11 @@ void bwd_dq_mfma(KArgs a) {
 //   S    = Q K^T          (A: Q rows from LDS, B: K^T in registers)
 //   dP   = dO V^T         (A: dO rows from LDS, B: V^T in registers)
 //   P    = exp2(scale_log2 S - lse),  dS = P * (dP - delta)
-//   dV^T += dO^T P        (A: dO^T from a transposed LDS copy)
+//   dV^T += dO^T P        (A: dO^T from a transposed LDS copy; float16 MFMA)
 //   dK^T += Q^T dS        (A: Q^T from a transposed LDS copy)
-// Q, dO, Q^T, dO^T, lse and delta are double-buffered in LDS.
+// Q, dO, Q^T, dO^T, lse and delta are double-buffered in LDS.  Q and dO are
+// loaded twice per sub-block: row-major by a coalesced mapping and four rows
+// per thread for the transposed copies.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bwd_dkdv_mfma(KArgs a) {
@@ -325,15 +355,17 @@ void bwd_dkdv_mfma(KArgs a) {
   using H = Elt<f16_tag>;
   constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BM = 64;           // queries per sub-block
-  constexpr int QP = D + 8;
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
   constexpr int CH = D / 8;
-  constexpr int QG = BM * CH / 256;  // consecutive query rows per loader thread
+  constexpr int RRP = 256 / CH;    // rows one coalesced pass loads
+  constexpr int RPASS = BM / RRP;
+  constexpr int QG = BM * CH / 256;  // consecutive rows per transposed-loader thread
   constexpr int NQG = BM / QG;
+  constexpr int P = D + 8;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * QP];
-  __shared__ __attribute__((aligned(16))) uint16_t Ds[2][BM * QP];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * P];
+  __shared__ __attribute__((aligned(16))) uint16_t Ds[2][BM * P];
   __shared__ __attribute__((aligned(16))) uint16_t Qt[2][D * BM];
   __shared__ __attribute__((aligned(16))) uint16_t Dt[2][D * BM];
   __shared__ __attribute__((aligned(16))) float Ls[2][BM];
@@ -350,6 +382,7 @@ void bwd_dkdv_mfma(KArgs a) {
   const int kloc = wave * 32 + l32;
   const int key = kt * TILE + kloc;
   const int kcl = min(key, a.Lk - 1);
+  const float c2 = a.scale_log2;
 
   u32x4 kf[NKD], vf[NKD];
   {
@@ -370,76 +403,101 @@ void bwd_dkdv_mfma(KArgs a) {
     const int mc = map_row(a, b, hk * a.G + g, a.nkt, kt);
     tot += 2 * (a.col_ptr[mc + 1] - a.col_ptr[mc]);
   }
-  // cursor state of the sub-block being loaded
+  // cursor of the next sub-block to load
   int lg = 0, le = 0, lend = 0, lhalf = 0;
-  auto seek = [&](int& g, int& e, int& eend) {
-    while (e >= eend) {
-      const int mc = map_row(a, b, hk * a.G + g, a.nkt, kt);
-      e = a.col_ptr[mc];
-      eend = a.col_ptr[mc + 1];
-      if (e < eend) break;
-      ++g;
-    }
-  };
   {
     const int mc = map_row(a, b, hk * a.G, a.nkt, kt);
     le = a.col_ptr[mc];
     lend = a.col_ptr[mc + 1];
   }
+  auto seek = [&]() {
+    while (le >= lend) {
+      ++lg;
+      const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
+      le = a.col_ptr[mc];
+      lend = a.col_ptr[mc + 1];
+    }
+  };
 
-  const int qg = tid % NQG, qc = tid / NQG;  // loader: row group, chunk
-  // dreg: dO for dP = dO V^T (bfloat16 copy, or dO * s for float16 inputs);
-  // hreg: dO * s in float16 for dV (bfloat16 inputs only; float16 inputs reuse dreg)
-  u32x4 qreg[QG], dreg[QG], hreg[IS_BF16 ? QG : 1];
+  const int rc = tid % CH, rr0 = tid / CH;    // coalesced loader
+  const int tg = tid % NQG, tc = tid / NQG;   // transposed loader
+  const int64_t drow = (int64_t)a.Hq * D;     // row stride of the dense dO copies
+  uint32_t qoff[RPASS], doff[RPASS], tqoff[QG], tdoff[QG];
+#pragma unroll
+  for (int i = 0; i < RPASS; ++i) {
+    qoff[i] = (uint32_t)((rr0 + RRP * i) * a.qs[1] + 8 * rc);
+    doff[i] = (uint32_t)((rr0 + RRP * i) * drow + 8 * rc);
+  }
+#pragma unroll
+  for (int i = 0; i < QG; ++i) {
+    tqoff[i] = (uint32_t)((tg * QG + i) * a.qs[1] + 8 * tc);
+    tdoff[i] = (uint32_t)((tg * QG + i) * drow + 8 * tc);
+  }
+  // qreg/dreg: row-major Q and dO (bfloat16 copy, or dO * s for float16 inputs);
+  // tqreg/tdreg: Q and dO * s (float16) for the transposed copies
+  u32x4 qreg[RPASS], dreg[RPASS], tqreg[QG], tdreg[QG];
   float lreg = 0.f;
   const float inv_s = a.dscale[1];
   const float dps = IS_BF16 ? 1.f : inv_s;
+  int cmask_e = 0, chalf = 0;  // entry and half of the sub-block being computed
   auto load = [&]() {  // loads the sub-block at the cursor
-    if (le >= lend) { ++lg; seek(lg, le, lend); }
+    seek();
     const int h = hk * a.G + lg;
-    const int qt = a.col_ent[2 * le];
-    const int q0 = qt * TILE + lhalf * BM;
+    const int q0 = a.col_ent[2 * le] * TILE + lhalf * BM;
     const uint16_t* qb = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
     const int64_t dro = ((int64_t)b * a.Lq * a.Hq + h) * D;
     const uint16_t* db = (const uint16_t*)(IS_BF16 ? a.dO16 : a.dOh) + dro;
     const uint16_t* hb = (const uint16_t*)a.dOh + dro;
+    if (q0 + BM <= a.Lq) {
+      const uint16_t* qp = qb + (int64_t)q0 * a.qs[1];
+      const uint16_t* dp = db + (int64_t)q0 * drow;
+      const uint16_t* hp = hb + (int64_t)q0 * drow;
 #pragma unroll
-    for (int i = 0; i < QG; ++i) {
-      const int qq = min(q0 + qg * QG + i, a.Lq - 1);
-      qreg[i] = *(const u32x4*)(qb + (int64_t)qq * a.qs[1] + 8 * qc);
-      dreg[i] = *(const u32x4*)(db + (int64_t)qq * a.Hq * D + 8 * qc);
-      if constexpr (IS_BF16) hreg[i] = *(const u32x4*)(hb + (int64_t)qq * a.Hq * D + 8 * qc);
+      for (int i = 0; i < RPASS; ++i) {
+        qreg[i] = *(const u32x4*)(qp + qoff[i]);
+        dreg[i] = *(const u32x4*)(dp + doff[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < QG; ++i) {
+        tqreg[i] = *(const u32x4*)(qp + tqoff[i]);
+        tdreg[i] = *(const u32x4*)(hp + tdoff[i]);
+      }
+    } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
+#pragma unroll
+      for (int i = 0; i < RPASS; ++i) {
+        const int qq = min(q0 + rr0 + RRP * i, a.Lq - 1);
+        qreg[i] = *(const u32x4*)(qb + (int64_t)qq * a.qs[1] + 8 * rc);
+        dreg[i] = *(const u32x4*)(db + (int64_t)qq * drow + 8 * rc);
+      }
+#pragma unroll
+      for (int i = 0; i < QG; ++i) {
+        const int qq = min(q0 + tg * QG + i, a.Lq - 1);
+        tqreg[i] = *(const u32x4*)(qb + (int64_t)qq * a.qs[1] + 8 * tc);
+        tdreg[i] = *(const u32x4*)(hb + (int64_t)qq * drow + 8 * tc);
+      }
     }
     if (tid < 2 * BM) {
       const int qq = min(q0 + (tid & (BM - 1)), a.Lq - 1);
       const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qq;
       lreg = tid < BM ? a.lse[rs] : a.delta[rs];
     }
-  };
-  auto advance = [&]() {
-    if (lhalf == 0) { lhalf = 1; } else { lhalf = 0; ++le; }
+    cmask_e = le;
+    chalf = lhalf;
+    if (lhalf == 0) {
+      lhalf = 1;
+    } else {
+      lhalf = 0;
+      ++le;
+    }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < QG; ++i) {
-      *(u32x4*)&Qs[buf][(qg * QG + i) * QP + 8 * qc] = qreg[i];
-      *(u32x4*)&Ds[buf][(qg * QG + i) * QP + 8 * qc] = dreg[i];
+    for (int i = 0; i < RPASS; ++i) {
+      *(u32x4*)&Qs[buf][rm_off<D>(rr0 + RRP * i, rc)] = qreg[i];
+      *(u32x4*)&Ds[buf][rm_off<D>(rr0 + RRP * i, rc)] = dreg[i];
     }
-    const int s0 = tslot(qg * QG);
-    const u32x4* treg = IS_BF16 ? hreg : dreg;  // float16 dO * s
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 8 * qc + j;
-      if constexpr (QG == 4) {
-        *(u32x2*)&Qt[buf][tpos(d, s0)] = u32x2{elt16(qreg[0], j) | (elt16(qreg[1], j) << 16),
-                                               elt16(qreg[2], j) | (elt16(qreg[3], j) << 16)};
-        *(u32x2*)&Dt[buf][tpos(d, s0)] = u32x2{elt16(treg[0], j) | (elt16(treg[1], j) << 16),
-                                               elt16(treg[2], j) | (elt16(treg[3], j) << 16)};
-      } else {
-        *(uint32_t*)&Qt[buf][tpos(d, s0)] = elt16(qreg[0], j) | (elt16(qreg[1], j) << 16);
-        *(uint32_t*)&Dt[buf][tpos(d, s0)] = elt16(treg[0], j) | (elt16(treg[1], j) << 16);
-      }
-    }
+    tr_write<QG>(Qt[buf], tqreg, tg * QG, tc);
+    tr_write<QG>(Dt[buf], IS_BF16 ? tdreg : tdreg, tg * QG, tc);
     if (tid < BM) Ls[buf][tid] = lreg;
     else if (tid < 2 * BM) Dl[buf][tid - BM] = lreg;
   };
@@ -448,38 +506,41 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
 
-  // the cursor of the sub-block being computed trails the load cursor by one
-  int cg = 0, ce = 0, chalf = 0;
-  if (tot > 0) {
-    load();
-    cg = lg; ce = le; chalf = lhalf;
-    advance();
-  }
-  for (int s = 0; s < tot; ++s) {
-    const int buf = s & 1;
-    store(buf);
-    __syncthreads();
-    const int mask = a.col_ent[2 * ce + 1];
-    uint64_t mw = ~0ull;
-    if (mask >= 0) mw = a.col_bits[((int64_t)mask * TILE + kloc) * 2 + chalf];
-    (void)cg;
-    if (s + 1 < tot) {
-      load();
-      cg = lg; ce = le; chalf = lhalf;
-      advance();
-    }
-
+  auto step = [&](int buf, bool masked, uint64_t mw) {
     f32x16 st[2], dp[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      st[t] = f32x16{};
-      dp[t] = f32x16{};
-      const uint16_t* qp = &Qs[buf][(32 * t + l32) * QP + 8 * hi];
-      const uint16_t* dpp = &Ds[buf][(32 * t + l32) * QP + 8 * hi];
+      u32x4 qa[NKD], da[NKD];
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) {
-        st[t] = E::mfma(*(const u32x4*)(qp + 16 * kd), kf[kd], st[t]);
-        dp[t] = E::mfma(*(const u32x4*)(dpp + 16 * kd), vf[kd], dp[t]);
+        qa[kd] = *(const u32x4*)&Qs[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+        da[kd] = *(const u32x4*)&Ds[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+      }
+      st[t] = f32x16{};
+      dp[t] = f32x16{};
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd) {
+        st[t] = E::mfma(qa[kd], kf[kd], st[t]);
+        dp[t] = E::mfma(da[kd], vf[kd], dp[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r0 = 32 * t + 8 * j + 4 * hi;  // first of 4 query rows
+        const f32x4 lv = *(const f32x4*)&Ls[buf][r0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[t][4 * j + i] = fast_exp2(fmaf(st[t][4 * j + i], c2, -lv[i]));
+      }
+    }
+    if (masked) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!mask_bit(w32, r)) st[t][r] = 0.f;
       }
     }
     u32x4 pk[4], sk[4];
@@ -487,38 +548,46 @@ void bwd_dkdv_mfma(KArgs a) {
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r0 = 32 * t + 8 * j + 4 * hi;  // first of 4 query rows
-        const f32x4 lv = *(const f32x4*)&Ls[buf][r0];
-        const f32x4 dv4 = *(const f32x4*)&Dl[buf][r0];
+        const f32x4 dv4 = *(const f32x4*)&Dl[buf][32 * t + 8 * j + 4 * hi];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 4 * j + i;
-          float p = fast_exp2(st[t][r] * a.scale_log2 - lv[i]);
-          if (mask >= 0) {
-            if (!((mw >> (r0 + i)) & 1ull)) p = 0.f;
-          }
-          st[t][r] = p;
-          dp[t][r] = p * (dp[t][r] * dps - dv4[i]);
+          dp[t][r] = st[t][r] * fmaf(dp[t][r], dps, -dv4[i]);
         }
       }
-    }
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pk[ks][i] = H::pack2(st[ks >> 1][8 * (ks & 1) + 2 * i], st[ks >> 1][8 * (ks & 1) + 2 * i + 1]);
-        sk[ks][i] = E::pack2(dp[ks >> 1][8 * (ks & 1) + 2 * i], dp[ks >> 1][8 * (ks & 1) + 2 * i + 1]);
+      for (int r = 0; r < 16; r += 2) {
+        pk[2 * t + (r >> 3)][(r & 7) >> 1] = H::pack2(st[t][r], st[t][r + 1]);
+        sk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(dp[t][r], dp[t][r + 1]);
       }
     }
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
       const int d = 32 * mt + l32;
+      u32x4 ta[4], tb[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        dv[mt] = H::mfma(*(const u32x4*)&Dt[buf][tchunk(d, ks, hi)], pk[ks], dv[mt]);
-        dk[mt] = E::mfma(*(const u32x4*)&Qt[buf][tchunk(d, ks, hi)], sk[ks], dk[mt]);
+        ta[ks] = *(const u32x4*)&Dt[buf][tchunk(d, ks, hi)];
+        tb[ks] = *(const u32x4*)&Qt[buf][tchunk(d, ks, hi)];
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        dv[mt] = H::mfma(ta[ks], pk[ks], dv[mt]);
+        dk[mt] = E::mfma(tb[ks], sk[ks], dk[mt]);
       }
     }
+  };
+
+  if (tot > 0) load();
+  for (int s = 0; s < tot; ++s) {
+    const int buf = s & 1;
+    store(buf);
+    __syncthreads();
+    const int mask = a.col_ent[2 * cmask_e + 1];
+    uint64_t mw = 0;
+    if (mask >= 0) mw = a.col_bits[((int64_t)mask * TILE + kloc) * 2 + chalf];
+    if (s + 1 < tot) load();
+    step(buf, mask >= 0, mw);
   }
 
   if (key >= a.Lk) return;

@@ -113,7 +113,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->D != 64 && p->D != 128) return MATTN_ERR_HEAD_DIM;
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
-  if (!(p->scale == p->scale) || isinf(p->scale)) return MATTN_ERR_SHAPE;
+  if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite
   const int es = elem_size(p->dtype), eo = elem_size(p->o_dtype);
   if (!strides_ok(p->q_stride, es) || !strides_ok(p->k_stride, es) || !strides_ok(p->v_stride, es) ||
       !strides_ok(p->dq_stride, es) || !strides_ok(p->dk_stride, es) ||
@@ -122,6 +122,12 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   const int64_t nqt = cdiv(p->Lq, MATTN_TILE_Q), nkt = cdiv(p->Lk, MATTN_TILE_K);
   if ((int64_t)p->B * p->Hq * nqt >= (1ll << 31) || (int64_t)p->B * p->Hkv * nkt >= (1ll << 31) ||
       (int64_t)p->Lq + MATTN_TILE_Q >= (1ll << 31) || (int64_t)p->Lk + MATTN_TILE_K >= (1ll << 31))
+    return MATTN_ERR_TOO_LARGE;
+  // kernels address rows inside one (batch, head) slice with 32-bit element offsets
+  const int64_t lim = (1ll << 31) - 1;
+  if ((int64_t)(nqt * MATTN_TILE_Q) * p->q_stride[1] > lim ||
+      (int64_t)(nkt * MATTN_TILE_K) * p->k_stride[1] > lim ||
+      (int64_t)(nkt * MATTN_TILE_K) * p->v_stride[1] > lim)
     return MATTN_ERR_TOO_LARGE;
   if (!bm) return MATTN_OK;
   if (bm->nqt != nqt || bm->nkt != nkt) return MATTN_ERR_BLOCKMAP;

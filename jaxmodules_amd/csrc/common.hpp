@@ -118,6 +118,20 @@ __device__ __forceinline__ uint32_t elt16(const u32x4& x, int j) {
   return (x[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
 }
 
+// LDS layouts.  gfx950 LDS has 64 banks of 4 bytes: a ds_read_b128 serves 16
+// lanes per cycle, a ds_write_b64 32 lanes, so a 16-lane group must touch 16
+// distinct 16-byte bank groups.
+//
+// Row-major tile [rows][D] of 16-bit values with rows padded to D + 8
+// elements (a 16-byte shift per row): 16 lanes reading 16 consecutive rows at
+// one chunk hit 16 distinct bank groups, a coalesced writer (consecutive lanes
+// on consecutive chunks of a row) writes contiguous banks, and every operand
+// address is a per-lane base plus an immediate offset.
+template <int D>
+__device__ __forceinline__ int rm_off(int r, int c) {
+  return r * (D + 8) + (c << 3);
+}
+
 // Permuted position of row r (0..63) of a sub-block inside a transposed row:
 // within every group of 16, rows {0-3, 8-11, 4-7, 12-15} are stored in that
 // order (bits 2 and 3 swapped), so the 8 rows one lane's C registers hold for
@@ -127,17 +141,46 @@ __device__ __forceinline__ int tslot(int r) {
   return (r & ~15) | (w & 3) | ((w & 4) << 1) | ((w & 8) >> 1);
 }
 
-// Element offset of (row d, slot s) in a transposed [D][64] LDS buffer of
-// 16-bit values.  Each 128-byte row is 8 chunks of 16 bytes; the chunk index is
-// XOR-swizzled with d % 8 so that 8 lanes reading consecutive d at the same
-// slot, and 16 lanes writing consecutive slots of one d, hit distinct banks.
+// Transposed tile [D][64]: row d (128 bytes = 32 banks) holds 64 sequence
+// positions in tslot order, its 16-byte chunks XOR-swizzled with (d >> 1) & 7
+// so that 16 lanes reading rows d..d+15 at one chunk hit 16 distinct bank
+// groups (the row parity picks the bank half).
 __device__ __forceinline__ int tpos(int d, int s) {
-  return d * 64 + ((((s >> 3) ^ (d & 7))) << 3) + (s & 7);
+  return d * 64 + (((s >> 3) ^ ((d >> 1) & 7)) << 3) + (s & 7);
 }
 
 // Offset of the 16-byte operand chunk for k-step ks (16 rows) and lane half hi.
 __device__ __forceinline__ int tchunk(int d, int ks, int hi) {
-  return d * 64 + (((2 * ks + hi) ^ (d & 7)) << 3);
+  return d * 64 + (((2 * ks + hi) ^ ((d >> 1) & 7)) << 3);
+}
+
+// Transposed write of G consecutive sequence rows r0..r0+G-1 (r0 % G == 0) of
+// head dims [8c, 8c+8), held as G 16-byte chunks.  Iteration j writes dim
+// 8c + (j ^ (c & 1)): the loaders give consecutive 16-lane groups consecutive
+// c, so the two halves of a 32-lane write cycle land on opposite row parities.
+template <int G>
+__device__ __forceinline__ void tr_write(uint16_t* T, const u32x4* x, int r0, int c) {
+  const int p = c & 1;
+  const int s0 = tslot(r0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int jj = j ^ p;
+    const int sh = (jj & 1) * 16;
+    const int d = 8 * c + jj;
+    if constexpr (G == 4) {
+      const u32x2 w = {((x[0][j >> 1] >> sh) & 0xffffu) | ((x[1][j >> 1] >> sh) << 16),
+                       ((x[2][j >> 1] >> sh) & 0xffffu) | ((x[3][j >> 1] >> sh) << 16)};
+      *(u32x2*)&T[tpos(d, s0)] = w;
+    } else {
+      *(uint32_t*)&T[tpos(d, s0)] = ((x[0][j >> 1] >> sh) & 0xffffu) | ((x[1][j >> 1] >> sh) << 16);
+    }
+  }
+}
+
+// Bit of a 64-bit tile-mask word for C-register r of MFMA row tile t (rows
+// 32t + 8(r/4) + 4hi + r%4): w32 is the word's half for t, pre-shifted by 4hi.
+__device__ __forceinline__ bool mask_bit(uint32_t w32, int r) {
+  return (w32 >> (8 * (r >> 2) + (r & 3))) & 1u;
 }
 
 __device__ __forceinline__ float wave_max32(float x) {

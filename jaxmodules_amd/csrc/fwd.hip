@@ -10,6 +10,8 @@
 //     O^T += V^T P^T     (MFMA, V^T from a transposed LDS copy)
 // K and V^T are double-buffered in LDS; the next sub-block's global loads are
 // in flight while the current one is computed.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace mattn {
@@ -18,17 +20,19 @@ template <int D, class Tag, bool OUT_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
   using E = Elt<Tag>;
-  constexpr int BN = 64;           // keys per sub-block
-  constexpr int KP = D + 8;        // padded K row pitch (elements)
-  constexpr int NKD = D / 16;      // k-steps of S^T over the head dimension
-  constexpr int NMD = D / 32;      // M-tiles of O^T over the head dimension
-  constexpr int CH = D / 8;        // 16-byte chunks per row
-  constexpr int KRP = 256 / CH;    // K rows one pass of the workgroup loads
-  constexpr int KPASS = BN / KRP;  // K passes per sub-block
+  constexpr int BN = 64;             // keys per sub-block
+  constexpr int NKD = D / 16;        // k-steps of S^T over the head dimension
+  constexpr int NMD = D / 32;        // M-tiles of O^T over the head dimension
+  constexpr int CH = D / 8;          // 16-byte chunks per row
+  constexpr int KRP = 256 / CH;      // K rows one pass of the workgroup loads
+  constexpr int KPASS = BN / KRP;    // K passes per sub-block
   constexpr int KG = BN * CH / 256;  // consecutive V rows per thread (4 or 2)
   constexpr int NKG = BN / KG;       // V row groups per sub-block
+  // The running max is only raised when a row's max grows by more than 2^8
+  // (base-2 units); until then P may reach 2^8, harmless in 16-bit and fp32.
+  constexpr float RESCALE_SLACK = 8.f;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * BN];
 
   const int item = a.q_order[blockIdx.x];
@@ -45,6 +49,7 @@ void fwd_mfma(KArgs a) {
   const int qloc = wave * 32 + l32;
   const int q = qt * TILE + qloc;
   const int qc = min(q, a.Lq - 1);
+  const float c2 = a.scale_log2;
 
   // Q^T operands: lane holds query q, head dims 16*kd + 8*hi .. +7.
   u32x4 qf[NKD];
@@ -57,45 +62,110 @@ void fwd_mfma(KArgs a) {
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  const int kc = tid % CH, kr0 = tid / CH;       // K loader: chunk, first row
+  const int kc = tid % CH, kr0 = tid / CH;       // K loader: chunk, first row (coalesced)
   const int vg = tid % NKG, vc = tid / NKG;      // V loader: row group, chunk
+
+  // loop-invariant 32-bit element offsets of each thread's rows within a sub-block
+  uint32_t koff[KPASS], voff[KG];
+#pragma unroll
+  for (int i = 0; i < KPASS; ++i) koff[i] = (uint32_t)((kr0 + KRP * i) * a.ks[1] + 8 * kc);
+#pragma unroll
+  for (int i = 0; i < KG; ++i) voff[i] = (uint32_t)((vg * KG + i) * a.vs[1] + 8 * vc);
 
   u32x4 kreg[KPASS], vreg[KG];
   auto load = [&](int s) {
     const int kt = a.row_ent[2 * (e0 + (s >> 1))];
     const int key0 = kt * TILE + (s & 1) * BN;
+    const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];   // wave-uniform bases
+    const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
+    if (key0 + BN <= a.Lk) {
 #pragma unroll
-    for (int i = 0; i < KPASS; ++i) {
-      const int key = min(key0 + kr0 + KRP * i, a.Lk - 1);
-      kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * kc);
-    }
+      for (int i = 0; i < KPASS; ++i) kreg[i] = *(const u32x4*)(kp + koff[i]);
 #pragma unroll
-    for (int i = 0; i < KG; ++i) {
-      const int key = min(key0 + vg * KG + i, a.Lk - 1);
-      vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * vc);
+      for (int i = 0; i < KG; ++i) vreg[i] = *(const u32x4*)(vp + voff[i]);
+    } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
+#pragma unroll
+      for (int i = 0; i < KPASS; ++i) {
+        const int key = min(key0 + kr0 + KRP * i, a.Lk - 1);
+        kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * kc);
+      }
+#pragma unroll
+      for (int i = 0; i < KG; ++i) {
+        const int key = min(key0 + vg * KG + i, a.Lk - 1);
+        vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * vc);
+      }
     }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < KPASS; ++i) *(u32x4*)&Ks[buf][(kr0 + KRP * i) * KP + 8 * kc] = kreg[i];
-    const int s0 = tslot(vg * KG);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 8 * vc + j;
-      if constexpr (KG == 4) {
-        u32x2 w = {elt16(vreg[0], j) | (elt16(vreg[1], j) << 16),
-                   elt16(vreg[2], j) | (elt16(vreg[3], j) << 16)};
-        *(u32x2*)&Vt[buf][tpos(d, s0)] = w;
-      } else {
-        *(uint32_t*)&Vt[buf][tpos(d, s0)] = elt16(vreg[0], j) | (elt16(vreg[1], j) << 16);
-      }
-    }
+    for (int i = 0; i < KPASS; ++i) *(u32x4*)&Ks[buf][rm_off<D>(kr0 + KRP * i, kc)] = kreg[i];
+    tr_write<KG>(Vt[buf], vreg, vg * KG, vc);
   };
 
   f32x16 acc[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
-  float m = NEG_INF, l = 0.f;
+  float m2 = NEG_INF, l = 0.f;  // running max (base-2 units) and partial row sum
+
+  auto step = [&](int buf, bool masked, uint64_t mw) {
+    // S^T = K Q^T, one row tile's K operands staged ahead of its MFMA chain
+    f32x16 st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      u32x4 ka[NKD];
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd)
+        ka[kd] = *(const u32x4*)&Ks[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+      st[t] = f32x16{};
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(ka[kd], qf[kd], st[t]);
+    }
+    if (masked) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!mask_bit(w32, r)) st[t][r] = NEG_INF;
+      }
+    }
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
+    const float mx2 = wave_max32(mx) * c2;
+    if (__any(mx2 > m2 + RESCALE_SLACK)) {
+      const float mn = fmaxf(m2, mx2);
+      const float alpha = (mn == NEG_INF) ? 1.f : fast_exp2(m2 - mn);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < NMD; ++i) acc[i] *= alpha;
+      m2 = mn;
+    }
+    const float nmu = (m2 == NEG_INF) ? 0.f : -m2;
+    u32x4 pk[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(fmaf(st[t][r], c2, nmu));
+        const float p1 = fast_exp2(fmaf(st[t][r + 1], c2, nmu));
+        l += p0 + p1;
+        pk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(p0, p1);
+      }
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int mt = 0; mt < NMD; ++mt) {
+      const int d = 32 * mt + l32;
+      u32x4 va[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) va[ks] = *(const u32x4*)&Vt[buf][tchunk(d, ks, hi)];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc[mt] = E::mfma(va[ks], pk[ks], acc[mt]);
+    }
+  };
 
   if (nsb > 0) load(0);
   for (int s = 0; s < nsb; ++s) {
@@ -103,73 +173,17 @@ void fwd_mfma(KArgs a) {
     store(buf);
     __syncthreads();
     const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
-    uint64_t mw = ~0ull;
+    uint64_t mw = 0;
     if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
     if (s + 1 < nsb) load(s + 1);
-
-    f32x16 st[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      st[t] = f32x16{};
-      const uint16_t* kp = &Ks[buf][(32 * t + l32) * KP + 8 * hi];
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(*(const u32x4*)(kp + 16 * kd), qf[kd], st[t]);
-    }
-
-    float mx = NEG_INF;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = st[t][r] * a.scale_log2;
-        if (mask >= 0) {
-          const int kk = 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
-          if (!((mw >> kk) & 1ull)) x = NEG_INF;
-        }
-        st[t][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    }
-    mx = wave_max32(mx);
-    const float mn = fmaxf(m, mx);
-    const float mu = (mn == NEG_INF) ? 0.f : mn;
-    const float alpha = fast_exp2(m - mu);
-    m = mn;
-    float ls = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(st[t][r] - mu);
-        st[t][r] = p;
-        ls += p;
-      }
-    }
-    l = l * alpha + ls;
-#pragma unroll
-    for (int i = 0; i < NMD; ++i) acc[i] *= alpha;
-
-    u32x4 pk[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pk[ks][i] = E::pack2(st[ks >> 1][8 * (ks & 1) + 2 * i], st[ks >> 1][8 * (ks & 1) + 2 * i + 1]);
-    }
-#pragma unroll
-    for (int mt = 0; mt < NMD; ++mt) {
-      const int d = 32 * mt + l32;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc[mt] = E::mfma(*(const u32x4*)&Vt[buf][tchunk(d, ks, hi)], pk[ks], acc[mt]);
-    }
+    step(buf, mask >= 0, mw);
   }
 
   l += __shfl_xor(l, 32);
   if (q >= a.Lq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (hi == 0)
-    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + __builtin_log2f(l) : NEG_INF;
+    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
   char* op = (char*)a.out;
   const int64_t orow = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2];
 #pragma unroll

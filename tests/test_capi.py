@@ -1,0 +1,152 @@
+"""The C ABI without a GPU: the library loads, exports every symbol
+include/mattn.h declares, its structs match the header byte for byte, and the
+host-only validation returns the documented codes."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mattn.h")
+
+from jaxmodules_amd import _lib  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libmattn.so not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mattn_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_exports():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    syms = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    for name in declared_functions():
+        assert name in syms, name
+        assert hasattr(lib, name)
+
+
+def test_abi_version(lib):
+    assert lib.mattn_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """Compile a probe against the header and compare sizeof/offsetof with ctypes."""
+    fields = {"mattn_problem": _lib.MattnProblem, "mattn_blockmap": _lib.MattnBlockmap}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mattn.h"', "int main(void){"]
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    got = {}
+    for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        c, f, v = l.split()
+        got[(c, f)] = int(v)
+    for cname, cls in fields.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def _problem(**kw):
+    p = _lib.MattnProblem(B=2, Lq=300, Lk=300, Hq=8, Hkv=2, D=128, dtype=_lib.MATTN_BF16,
+                          o_dtype=_lib.MATTN_F32, scale=0.088)
+    for name in ("q", "k", "v", "dq", "dk", "dv"):
+        setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(300 * 8 * 128, 8 * 128, 128))
+    for name in ("o", "do"):
+        setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(300 * 8 * 128, 8 * 128, 128))
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def _validate(lib, p, bm=None):
+    return lib.mattn_validate(ctypes.byref(p), ctypes.byref(bm) if bm is not None else None)
+
+
+def test_validate_codes(lib):
+    assert _validate(lib, _problem()) == 0
+    assert _validate(lib, _problem(Hkv=3)) == -2          # Hq % Hkv
+    assert _validate(lib, _problem(B=0)) == -2
+    assert _validate(lib, _problem(D=96)) == -3
+    assert _validate(lib, _problem(dtype=7)) == -4
+    assert _validate(lib, _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_BF16)) == -4
+    assert _validate(lib, _problem(o_dtype=_lib.MATTN_F16)) == -4   # bf16 in, fp16 out
+    p = _problem()
+    p.q_stride = (ctypes.c_int64 * 3)(300 * 8 * 128, 8 * 128 + 3, 128)
+    assert _validate(lib, p) == -5
+    assert lib.mattn_validate(None, None) == -1
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, 123):
+        assert isinstance(lib.mattn_strerror(code), bytes)
+
+
+def test_validate_blockmap(lib):
+    p = _problem()
+    bm = _lib.MattnBlockmap(map_b=1, map_h=1, nqt=3, nkt=3, n_masks=0, nnz=0, row_ptr=8, col_ptr=8,
+                            q_order=8, kv_order=8, n_q_order=2 * 8 * 3, n_kv_order=2 * 2 * 3)
+    assert _validate(lib, p, bm) == 0
+    bm.nqt = 2
+    assert _validate(lib, p, bm) == -6
+    bm.nqt = 3
+    bm.map_h = 4
+    assert _validate(lib, p, bm) == -6
+    bm.map_h = 8
+    assert _validate(lib, p, bm) == 0
+    bm.n_q_order = 10
+    assert _validate(lib, p, bm) == -6
+    bm.n_q_order = 48
+    bm.nnz = 5
+    assert _validate(lib, p, bm) == -1                     # entries missing
+    bm.row_ent = bm.col_ent = 8
+    bm.n_masks = 1
+    assert _validate(lib, p, bm) == -1                     # bit arrays missing
+
+
+def test_workspace_bytes(lib):
+    p = _problem()
+    rows = 2 * 8 * 300
+    n = lib.mattn_workspace_bytes(ctypes.byref(p))
+    # delta + partial maxima + scale + two 16-bit copies of dO (float16 scaled, bfloat16)
+    assert n >= rows * 4 + 2 * rows * 128 * 2
+    p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == n - rows * 128 * 2
+    assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
+
+
+def test_entry_points_reject_before_launch(lib):
+    """Error paths return codes without touching the GPU (no device here)."""
+    p = _problem(D=96)
+    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None)
+    assert rc == -3
+    p = _problem()
+    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None)
+    assert rc == -1
+    rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 11))
+    assert rc == -1
+
+
+def test_library_missing_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError):
+        _lib.load()
