@@ -10,7 +10,10 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmattn.so")
+# MATTN_LIBRARY selects another build of the same library (e.g. to compare
+# compiler settings); the default is the in-tree build.
+LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libmattn.so")
 
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 TILE_Q = TILE_K = 128

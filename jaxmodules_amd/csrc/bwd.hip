@@ -146,28 +146,23 @@ void bwd_pre(KArgs a) {
 //   S^T  = K Q^T         (A: K rows from LDS, B: Q^T in registers)
 //   dP^T = V dO^T        (A: V rows from LDS, B: dO^T in registers)
 //   dS^T = P^T * (dP^T - delta)    (each lane owns one query: lse, delta scalars)
-//   dQ^T += K^T dS^T     (A: K^T from a transposed LDS copy)
-// K, V and K^T are double-buffered in LDS.  K is loaded twice per sub-block:
-// row-major by a coalesced mapping, and four rows per thread for the
-// transposed copy.
+//   dQ^T += K^T dS^T     (A: K^T by transposed reads of the same K tile)
+// K and V are double-buffered, swizzled row-major tiles filled by direct
+// global->LDS loads.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bwd_dq_mfma(KArgs a) {
   using E = Elt<Tag>;
+  using TL = TileLoad<D>;
   constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BN = 64;
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
-  constexpr int CH = D / 8;
-  constexpr int KRP = 256 / CH;
-  constexpr int KPASS = BN / KRP;
-  constexpr int KG = BN * CH / 256;
-  constexpr int NKG = BN / KG;
-  constexpr int P = D + 8;
+  constexpr int NI = D / 32;       // load instructions per wave per tile
+  constexpr int BLK = 512;         // elements one load instruction fills
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * P];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * P];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[2][D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * D];
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0) return;
@@ -205,52 +200,44 @@ void bwd_dq_mfma(KArgs a) {
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  const int rc = tid % CH, rr0 = tid / CH;    // coalesced loader: chunk, first row
-  const int tg = tid % NKG, tc = tid / NKG;   // transposed loader: row group, chunk
-  uint32_t koff[KPASS], voff[KPASS], toff[KG];
+  uint32_t kld[NI], vld[NI];
 #pragma unroll
-  for (int i = 0; i < KPASS; ++i) {
-    koff[i] = (uint32_t)((rr0 + KRP * i) * a.ks[1] + 8 * rc);
-    voff[i] = (uint32_t)((rr0 + KRP * i) * a.vs[1] + 8 * rc);
+  for (int i = 0; i < NI; ++i) {
+    kld[i] = TL::src_off(NI * wave + i, lane, a.ks[1]);
+    vld[i] = TL::src_off(NI * wave + i, lane, a.vs[1]);
   }
+  int rro[NKD];               // row-read offsets (K and V tiles share the layout)
 #pragma unroll
-  for (int i = 0; i < KG; ++i) toff[i] = (uint32_t)((tg * KG + i) * a.ks[1] + 8 * tc);
+  for (int kd = 0; kd < NKD; ++kd) rro[kd] = sw_off<D>(l32, 2 * kd + hi);
+  int kto[NMD][2];            // K^T transposed-read offsets
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+    kto[mt][0] = tr_src<D>(lane, mt, 0);
+    kto[mt][1] = tr_src<D>(lane, mt, 1);
+  }
 
-  u32x4 kreg[KPASS], vreg[KPASS], treg[KG];
-  auto load = [&](int s) {
+  auto issue = [&](int s, int buf) {
     const int kt = a.row_ent[2 * (e0 + (s >> 1))];
     const int key0 = kt * TILE + (s & 1) * BN;
-    const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];
-    const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
+    uint16_t* kl = &Ks[buf][NI * wave * BLK];
+    uint16_t* vl = &Vs[buf][NI * wave * BLK];
     if (key0 + BN <= a.Lk) {
+      const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];
+      const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
 #pragma unroll
-      for (int i = 0; i < KPASS; ++i) {
-        kreg[i] = *(const u32x4*)(kp + koff[i]);
-        vreg[i] = *(const u32x4*)(vp + voff[i]);
+      for (int i = 0; i < NI; ++i) {
+        lds_load16(kp + kld[i], kl + i * BLK);
+        lds_load16(vp + vld[i], vl + i * BLK);
       }
-#pragma unroll
-      for (int i = 0; i < KG; ++i) treg[i] = *(const u32x4*)(kp + toff[i]);
     } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
 #pragma unroll
-      for (int i = 0; i < KPASS; ++i) {
-        const int key = min(key0 + rr0 + KRP * i, a.Lk - 1);
-        kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * rc);
-        vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * rc);
-      }
-#pragma unroll
-      for (int i = 0; i < KG; ++i) {
-        const int key = min(key0 + tg * KG + i, a.Lk - 1);
-        treg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * tc);
+      for (int i = 0; i < NI; ++i) {
+        const int key = min(key0 + TL::row_of(NI * wave + i, lane), a.Lk - 1);
+        const int c = TL::chunk_of(NI * wave + i, lane);
+        lds_load16(kb + (int64_t)key * a.ks[1] + 8 * c, kl + i * BLK);
+        lds_load16(vb + (int64_t)key * a.vs[1] + 8 * c, vl + i * BLK);
       }
     }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KPASS; ++i) {
-      *(u32x4*)&Ks[buf][rm_off<D>(rr0 + KRP * i, rc)] = kreg[i];
-      *(u32x4*)&Vs[buf][rm_off<D>(rr0 + KRP * i, rc)] = vreg[i];
-    }
-    tr_write<KG>(Kt[buf], treg, tg * KG, tc);
   };
 
   f32x16 acc[NMD];
@@ -264,8 +251,8 @@ void bwd_dq_mfma(KArgs a) {
       u32x4 ka[NKD], va[NKD];
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) {
-        ka[kd] = *(const u32x4*)&Ks[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
-        va[kd] = *(const u32x4*)&Vs[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+        ka[kd] = *(const u32x4*)&Ks[buf][rro[kd] + 32 * t * D];
+        va[kd] = *(const u32x4*)&Vs[buf][rro[kd] + 32 * t * D];
       }
       st[t] = f32x16{};
       dp[t] = f32x16{};
@@ -300,24 +287,27 @@ void bwd_dq_mfma(KArgs a) {
     }
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
-      const int d = 32 * mt + l32;
       u32x4 ta[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ta[ks] = *(const u32x4*)&Kt[buf][tchunk(d, ks, hi)];
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x2 lo = lds_read_tr(&Ks[buf][kto[mt][0] + 16 * ks * D]);
+        const u32x2 up = lds_read_tr(&Ks[buf][kto[mt][1] + 16 * ks * D]);
+        ta[ks] = u32x4{lo[0], lo[1], up[0], up[1]};
+      }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) acc[mt] = E::mfma(ta[ks], pk[ks], acc[mt]);
     }
   };
 
-  if (nsb > 0) load(0);
+  if (nsb > 0) issue(0, 0);
   for (int s = 0; s < nsb; ++s) {
     const int buf = s & 1;
-    store(buf);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
     uint64_t mw = 0;
     if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
-    if (s + 1 < nsb) load(s + 1);
+    if (s + 1 < nsb) issue(s + 1, buf ^ 1);
     step(buf, mask >= 0, mw);
   }
 
@@ -343,31 +333,28 @@ void bwd_dq_mfma(KArgs a) {
 //   S    = Q K^T          (A: Q rows from LDS, B: K^T in registers)
 //   dP   = dO V^T         (A: dO rows from LDS, B: V^T in registers)
 //   P    = exp2(scale_log2 S - lse),  dS = P * (dP - delta)
-//   dV^T += dO^T P        (A: dO^T from a transposed LDS copy; float16 MFMA)
-//   dK^T += Q^T dS        (A: Q^T from a transposed LDS copy)
-// Q, dO, Q^T, dO^T, lse and delta are double-buffered in LDS.  Q and dO are
-// loaded twice per sub-block: row-major by a coalesced mapping and four rows
-// per thread for the transposed copies.
+//   dV^T += dO^T P        (A: transposed reads of the float16 dO * s tile;
+//                          float16 MFMA)
+//   dK^T += Q^T dS        (A: transposed reads of the Q tile)
+// Q, dO (and, for bfloat16 inputs, the separate float16 dO * s tile), lse and
+// delta are double-buffered in LDS and filled by direct global->LDS loads.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void bwd_dkdv_mfma(KArgs a) {
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
+  using TL = TileLoad<D>;
   constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BM = 64;           // queries per sub-block
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
-  constexpr int CH = D / 8;
-  constexpr int RRP = 256 / CH;    // rows one coalesced pass loads
-  constexpr int RPASS = BM / RRP;
-  constexpr int QG = BM * CH / 256;  // consecutive rows per transposed-loader thread
-  constexpr int NQG = BM / QG;
-  constexpr int P = D + 8;
+  constexpr int NI = D / 32;
+  constexpr int BLK = 512;
+  constexpr int NH = IS_BF16 ? 2 : 1;  // float16 dO * s tile: separate (bf16) or the dO tile
 
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * P];
-  __shared__ __attribute__((aligned(16))) uint16_t Ds[2][BM * P];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[2][D * BM];
-  __shared__ __attribute__((aligned(16))) uint16_t Dt[2][D * BM];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Ds[2][BM * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Hs[NH == 2 ? 2 : 1][NH == 2 ? BM * D : 8];
   __shared__ __attribute__((aligned(16))) float Ls[2][BM];
   __shared__ __attribute__((aligned(16))) float Dl[2][BM];
 
@@ -410,76 +397,68 @@ void bwd_dkdv_mfma(KArgs a) {
     le = a.col_ptr[mc];
     lend = a.col_ptr[mc + 1];
   }
-  auto seek = [&]() {
+
+  const int64_t drow = (int64_t)a.Hq * D;   // row stride of the dense dO copies
+  uint32_t qld[NI], dld[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    qld[i] = TL::src_off(NI * wave + i, lane, a.qs[1]);
+    dld[i] = TL::src_off(NI * wave + i, lane, drow);
+  }
+  int rro[NKD];
+#pragma unroll
+  for (int kd = 0; kd < NKD; ++kd) rro[kd] = sw_off<D>(l32, 2 * kd + hi);
+  int tro[NMD][2];
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+    tro[mt][0] = tr_src<D>(lane, mt, 0);
+    tro[mt][1] = tr_src<D>(lane, mt, 1);
+  }
+  const float inv_s = a.dscale[1];
+  const float dps = IS_BF16 ? 1.f : inv_s;
+  int cmask_e = 0, chalf = 0;  // entry and half of the most recently issued sub-block
+
+  auto issue = [&](int buf) {  // global -> LDS loads of the sub-block at the cursor
     while (le >= lend) {
       ++lg;
       const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
       le = a.col_ptr[mc];
       lend = a.col_ptr[mc + 1];
     }
-  };
-
-  const int rc = tid % CH, rr0 = tid / CH;    // coalesced loader
-  const int tg = tid % NQG, tc = tid / NQG;   // transposed loader
-  const int64_t drow = (int64_t)a.Hq * D;     // row stride of the dense dO copies
-  uint32_t qoff[RPASS], doff[RPASS], tqoff[QG], tdoff[QG];
-#pragma unroll
-  for (int i = 0; i < RPASS; ++i) {
-    qoff[i] = (uint32_t)((rr0 + RRP * i) * a.qs[1] + 8 * rc);
-    doff[i] = (uint32_t)((rr0 + RRP * i) * drow + 8 * rc);
-  }
-#pragma unroll
-  for (int i = 0; i < QG; ++i) {
-    tqoff[i] = (uint32_t)((tg * QG + i) * a.qs[1] + 8 * tc);
-    tdoff[i] = (uint32_t)((tg * QG + i) * drow + 8 * tc);
-  }
-  // qreg/dreg: row-major Q and dO (bfloat16 copy, or dO * s for float16 inputs);
-  // tqreg/tdreg: Q and dO * s (float16) for the transposed copies
-  u32x4 qreg[RPASS], dreg[RPASS], tqreg[QG], tdreg[QG];
-  float lreg = 0.f;
-  const float inv_s = a.dscale[1];
-  const float dps = IS_BF16 ? 1.f : inv_s;
-  int cmask_e = 0, chalf = 0;  // entry and half of the sub-block being computed
-  auto load = [&]() {  // loads the sub-block at the cursor
-    seek();
     const int h = hk * a.G + lg;
     const int q0 = a.col_ent[2 * le] * TILE + lhalf * BM;
     const uint16_t* qb = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
     const int64_t dro = ((int64_t)b * a.Lq * a.Hq + h) * D;
     const uint16_t* db = (const uint16_t*)(IS_BF16 ? a.dO16 : a.dOh) + dro;
     const uint16_t* hb = (const uint16_t*)a.dOh + dro;
+    uint16_t* ql = &Qs[buf][NI * wave * BLK];
+    uint16_t* dl_ = &Ds[buf][NI * wave * BLK];
+    uint16_t* hl = &Hs[NH == 2 ? buf : 0][NH == 2 ? NI * wave * BLK : 0];
     if (q0 + BM <= a.Lq) {
       const uint16_t* qp = qb + (int64_t)q0 * a.qs[1];
       const uint16_t* dp = db + (int64_t)q0 * drow;
       const uint16_t* hp = hb + (int64_t)q0 * drow;
 #pragma unroll
-      for (int i = 0; i < RPASS; ++i) {
-        qreg[i] = *(const u32x4*)(qp + qoff[i]);
-        dreg[i] = *(const u32x4*)(dp + doff[i]);
-      }
-#pragma unroll
-      for (int i = 0; i < QG; ++i) {
-        tqreg[i] = *(const u32x4*)(qp + tqoff[i]);
-        tdreg[i] = *(const u32x4*)(hp + tdoff[i]);
+      for (int i = 0; i < NI; ++i) {
+        lds_load16(qp + qld[i], ql + i * BLK);
+        lds_load16(dp + dld[i], dl_ + i * BLK);
+        if constexpr (NH == 2) lds_load16(hp + dld[i], hl + i * BLK);
       }
     } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
 #pragma unroll
-      for (int i = 0; i < RPASS; ++i) {
-        const int qq = min(q0 + rr0 + RRP * i, a.Lq - 1);
-        qreg[i] = *(const u32x4*)(qb + (int64_t)qq * a.qs[1] + 8 * rc);
-        dreg[i] = *(const u32x4*)(db + (int64_t)qq * drow + 8 * rc);
-      }
-#pragma unroll
-      for (int i = 0; i < QG; ++i) {
-        const int qq = min(q0 + tg * QG + i, a.Lq - 1);
-        tqreg[i] = *(const u32x4*)(qb + (int64_t)qq * a.qs[1] + 8 * tc);
-        tdreg[i] = *(const u32x4*)(hb + (int64_t)qq * drow + 8 * tc);
+      for (int i = 0; i < NI; ++i) {
+        const int qq = min(q0 + TL::row_of(NI * wave + i, lane), a.Lq - 1);
+        const int c = TL::chunk_of(NI * wave + i, lane);
+        lds_load16(qb + (int64_t)qq * a.qs[1] + 8 * c, ql + i * BLK);
+        lds_load16(db + (int64_t)qq * drow + 8 * c, dl_ + i * BLK);
+        if constexpr (NH == 2) lds_load16(hb + (int64_t)qq * drow + 8 * c, hl + i * BLK);
       }
     }
-    if (tid < 2 * BM) {
-      const int qq = min(q0 + (tid & (BM - 1)), a.Lq - 1);
-      const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qq;
-      lreg = tid < BM ? a.lse[rs] : a.delta[rs];
+    if (wave < 2) {  // lse (wave 0) and delta (wave 1) of the 64 rows
+      const int qq = min(q0 + lane, a.Lq - 1);
+      const float* src = (wave == 0 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq + qq;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(wave == 0 ? Ls[buf] : Dl[buf]),
+                                       4, 0, 0);
     }
     cmask_e = le;
     chalf = lhalf;
@@ -490,31 +469,21 @@ void bwd_dkdv_mfma(KArgs a) {
       ++le;
     }
   };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < RPASS; ++i) {
-      *(u32x4*)&Qs[buf][rm_off<D>(rr0 + RRP * i, rc)] = qreg[i];
-      *(u32x4*)&Ds[buf][rm_off<D>(rr0 + RRP * i, rc)] = dreg[i];
-    }
-    tr_write<QG>(Qt[buf], tqreg, tg * QG, tc);
-    tr_write<QG>(Dt[buf], IS_BF16 ? tdreg : tdreg, tg * QG, tc);
-    if (tid < BM) Ls[buf][tid] = lreg;
-    else if (tid < 2 * BM) Dl[buf][tid - BM] = lreg;
-  };
 
   f32x16 dk[NMD], dv[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
 
   auto step = [&](int buf, bool masked, uint64_t mw) {
+    const uint16_t* ht = NH == 2 ? Hs[buf] : Ds[buf];  // float16 dO * s tile
     f32x16 st[2], dp[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       u32x4 qa[NKD], da[NKD];
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) {
-        qa[kd] = *(const u32x4*)&Qs[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
-        da[kd] = *(const u32x4*)&Ds[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+        qa[kd] = *(const u32x4*)&Qs[buf][rro[kd] + 32 * t * D];
+        da[kd] = *(const u32x4*)&Ds[buf][rro[kd] + 32 * t * D];
       }
       st[t] = f32x16{};
       dp[t] = f32x16{};
@@ -528,8 +497,7 @@ void bwd_dkdv_mfma(KArgs a) {
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r0 = 32 * t + 8 * j + 4 * hi;  // first of 4 query rows
-        const f32x4 lv = *(const f32x4*)&Ls[buf][r0];
+        const f32x4 lv = *(const f32x4*)&Ls[buf][32 * t + 8 * j + 4 * hi];
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[t][4 * j + i] = fast_exp2(fmaf(st[t][4 * j + i], c2, -lv[i]));
       }
@@ -563,12 +531,15 @@ void bwd_dkdv_mfma(KArgs a) {
     }
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
-      const int d = 32 * mt + l32;
       u32x4 ta[4], tb[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        ta[ks] = *(const u32x4*)&Dt[buf][tchunk(d, ks, hi)];
-        tb[ks] = *(const u32x4*)&Qt[buf][tchunk(d, ks, hi)];
+        const u32x2 h0 = lds_read_tr(&ht[tro[mt][0] + 16 * ks * D]);
+        const u32x2 h1 = lds_read_tr(&ht[tro[mt][1] + 16 * ks * D]);
+        const u32x2 q0 = lds_read_tr(&Qs[buf][tro[mt][0] + 16 * ks * D]);
+        const u32x2 q1 = lds_read_tr(&Qs[buf][tro[mt][1] + 16 * ks * D]);
+        ta[ks] = u32x4{h0[0], h0[1], h1[0], h1[1]};
+        tb[ks] = u32x4{q0[0], q0[1], q1[0], q1[1]};
       }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -578,15 +549,16 @@ void bwd_dkdv_mfma(KArgs a) {
     }
   };
 
-  if (tot > 0) load();
+  if (tot > 0) issue(0);
   for (int s = 0; s < tot; ++s) {
     const int buf = s & 1;
-    store(buf);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int mask = a.col_ent[2 * cmask_e + 1];
+    const int half = chalf;
     uint64_t mw = 0;
-    if (mask >= 0) mw = a.col_bits[((int64_t)mask * TILE + kloc) * 2 + chalf];
-    if (s + 1 < tot) load();
+    if (mask >= 0) mw = a.col_bits[((int64_t)mask * TILE + kloc) * 2 + half];
+    if (s + 1 < tot) issue(buf ^ 1);
     step(buf, mask >= 0, mw);
   }
 

@@ -122,14 +122,82 @@ __device__ __forceinline__ uint32_t elt16(const u32x4& x, int j) {
 // lanes per cycle, a ds_write_b64 32 lanes, so a 16-lane group must touch 16
 // distinct 16-byte bank groups.
 //
-// Row-major tile [rows][D] of 16-bit values with rows padded to D + 8
-// elements (a 16-byte shift per row): 16 lanes reading 16 consecutive rows at
-// one chunk hit 16 distinct bank groups, a coalesced writer (consecutive lanes
-// on consecutive chunks of a row) writes contiguous banks, and every operand
-// address is a per-lane base plus an immediate offset.
+// Row-major tile [rows][D] of 16-bit values, rows packed, filled by direct
+// global->LDS loads.  The 16-byte chunk c of row r is stored at chunk
+// c ^ swz<D>(r).  The swizzle makes both operand access patterns
+// conflict-free on the 64 banks:
+//   * ds_read_b128 row reads: 16 lanes read rows r0..r0+15 at one chunk;
+//   * ds_read_b64_tr_b16 reads: 32 lanes read rows r0..r0+3 (r0 % 4 == 0)
+//     at 4 consecutive chunks.
+// D = 128 (a row spans all banks): swz = 4 (r % 4) + (r / 4) % 4.
+// D = 64 (two rows per bank line, row parity picks the half):
+// swz = 4 ((r / 2) % 2) + (r / 4) % 4.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
+template <int D>
+__device__ __forceinline__ int sw_off(int r, int c) {  // element offset of chunk c of row r
+  return r * D + ((c ^ swz<D>(r)) << 3);
+}
+
+// Row-major tile [rows][D] with rows padded to D + 8 elements, written from
+// VGPRs by a coalesced loader: 16 lanes reading 16 consecutive rows at one
+// chunk hit 16 distinct bank groups.
 template <int D>
 __device__ __forceinline__ int rm_off(int r, int c) {
   return r * (D + 8) + (c << 3);
+}
+
+// Direct global->LDS tile loader: one global_load_lds_dwordx4 moves 1 KiB
+// (64 lanes x 16 bytes, lane L to LDS byte 16 L of the instruction's block).
+// Lane L of instruction block n covers row n * RPI + L / CPR of the tile and
+// physical chunk L % CPR, i.e. logical chunk (L % CPR) ^ swz(row).
+template <int D>
+struct TileLoad {
+  static constexpr int CPR = D / 8;          // chunks per row
+  static constexpr int RPI = 64 / CPR;       // rows per load instruction
+  // element offset (row-relative to the tile's first row, stride rs) of
+  // lane L's source in instruction block n
+  static __device__ __forceinline__ uint32_t src_off(int n, int lane, int64_t rs) {
+    const int r = n * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ swz<D>(r);
+    return (uint32_t)(r * rs + 8 * c);
+  }
+  static __device__ __forceinline__ int row_of(int n, int lane) { return n * RPI + lane / CPR; }
+  static __device__ __forceinline__ int chunk_of(int n, int lane) {
+    const int r = n * RPI + lane / CPR;
+    return (lane % CPR) ^ swz<D>(r);
+  }
+};
+
+__device__ __forceinline__ void lds_load16(const void* g, uint16_t* lds_block) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
+}
+
+// Transposed operand read (ds_read_b64_tr_b16): inside each 16-lane group, if
+// lane j addresses X[r + j/4][c + 4 (j % 4)], lane i receives
+// X[r + k][c + i] for k = 0..3.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// Element offset, within a swizzled [rows][D] tile, of the address lane
+// `lane` supplies to lds_read_tr so that it receives the A operand
+// A[i = 32 mt + lane % 32][k = rows 16 ks + 4 hi + 8 sec + 0..3] of a
+// 32x32x16 MFMA k-step (sec = 0: operand slots 0-3, sec = 1: slots 4-7),
+// i.e. X[16 ks + 8 sec + 4 hi + k][32 mt + lane % 32].  Returned for ks = 0;
+// k-step ks adds 16 * ks * D elements.
+template <int D>
+__device__ __forceinline__ int tr_src(int lane, int mt, int sec) {
+  const int i = lane & 15, g = lane >> 4, hi = lane >> 5;
+  const int r = 4 * hi + 8 * sec + (i >> 2);
+  const int c = 4 * mt + 2 * (g & 1) + ((i & 3) >> 1);
+  return r * D + ((c ^ swz<D>(r)) << 3) + 4 * (i & 1);
 }
 
 // Permuted position of row r (0..63) of a sub-block inside a transposed row:

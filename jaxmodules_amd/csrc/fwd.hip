@@ -9,7 +9,9 @@
 //                         cross-lane exchange and the row sum none)
 //     O^T += V^T P^T     (MFMA, V^T from a transposed LDS copy)
 // K and V^T are double-buffered in LDS; the next sub-block's global loads are
-// in flight while the current one is computed.
+// in flight while the current one is computed.  K and V tiles are moved by
+// direct global->LDS loads into swizzled row-major tiles; V^T operands are
+// read with the transposing LDS read.
 #include <type_traits>
 
 #include "common.hpp"
@@ -20,20 +22,18 @@ template <int D, class Tag, bool OUT_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
   using E = Elt<Tag>;
+  using TL = TileLoad<D>;
   constexpr int BN = 64;             // keys per sub-block
   constexpr int NKD = D / 16;        // k-steps of S^T over the head dimension
   constexpr int NMD = D / 32;        // M-tiles of O^T over the head dimension
-  constexpr int CH = D / 8;          // 16-byte chunks per row
-  constexpr int KRP = 256 / CH;      // K rows one pass of the workgroup loads
-  constexpr int KPASS = BN / KRP;    // K passes per sub-block
-  constexpr int KG = BN * CH / 256;  // consecutive V rows per thread (4 or 2)
-  constexpr int NKG = BN / KG;       // V row groups per sub-block
+  constexpr int NI = D / 32;         // load instructions per wave per tile
+  constexpr int BLK = 512;           // elements one load instruction fills
   // The running max is only raised when a row's max grows by more than 2^8
   // (base-2 units); until then P may reach 2^8, harmless in 16-bit and fp32.
   constexpr float RESCALE_SLACK = 8.f;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * D];
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0) return;
@@ -62,44 +62,44 @@ void fwd_mfma(KArgs a) {
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  const int kc = tid % CH, kr0 = tid / CH;       // K loader: chunk, first row (coalesced)
-  const int vg = tid % NKG, vc = tid / NKG;      // V loader: row group, chunk
-
-  // loop-invariant 32-bit element offsets of each thread's rows within a sub-block
-  uint32_t koff[KPASS], voff[KG];
+  uint32_t kld[NI], vld[NI];  // loop-invariant source offsets of this lane's load slots
 #pragma unroll
-  for (int i = 0; i < KPASS; ++i) koff[i] = (uint32_t)((kr0 + KRP * i) * a.ks[1] + 8 * kc);
+  for (int i = 0; i < NI; ++i) {
+    kld[i] = TL::src_off(NI * wave + i, lane, a.ks[1]);
+    vld[i] = TL::src_off(NI * wave + i, lane, a.vs[1]);
+  }
+  int kro[NKD];               // K row-read offsets (A operand of S^T), row tile 0
 #pragma unroll
-  for (int i = 0; i < KG; ++i) voff[i] = (uint32_t)((vg * KG + i) * a.vs[1] + 8 * vc);
+  for (int kd = 0; kd < NKD; ++kd) kro[kd] = sw_off<D>(l32, 2 * kd + hi);
+  int vto[NMD][2];            // V transposed-read offsets (A operand of O^T), k-step 0
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+    vto[mt][0] = tr_src<D>(lane, mt, 0);
+    vto[mt][1] = tr_src<D>(lane, mt, 1);
+  }
 
-  u32x4 kreg[KPASS], vreg[KG];
-  auto load = [&](int s) {
+  auto issue = [&](int s, int buf) {  // global -> LDS loads of sub-block s
     const int kt = a.row_ent[2 * (e0 + (s >> 1))];
     const int key0 = kt * TILE + (s & 1) * BN;
-    const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];   // wave-uniform bases
-    const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
+    uint16_t* kl = &Ks[buf][NI * wave * BLK];
+    uint16_t* vl = &Vs[buf][NI * wave * BLK];
     if (key0 + BN <= a.Lk) {
+      const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];
+      const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
 #pragma unroll
-      for (int i = 0; i < KPASS; ++i) kreg[i] = *(const u32x4*)(kp + koff[i]);
-#pragma unroll
-      for (int i = 0; i < KG; ++i) vreg[i] = *(const u32x4*)(vp + voff[i]);
+      for (int i = 0; i < NI; ++i) {
+        lds_load16(kp + kld[i], kl + i * BLK);
+        lds_load16(vp + vld[i], vl + i * BLK);
+      }
     } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
 #pragma unroll
-      for (int i = 0; i < KPASS; ++i) {
-        const int key = min(key0 + kr0 + KRP * i, a.Lk - 1);
-        kreg[i] = *(const u32x4*)(kb + (int64_t)key * a.ks[1] + 8 * kc);
-      }
-#pragma unroll
-      for (int i = 0; i < KG; ++i) {
-        const int key = min(key0 + vg * KG + i, a.Lk - 1);
-        vreg[i] = *(const u32x4*)(vb + (int64_t)key * a.vs[1] + 8 * vc);
+      for (int i = 0; i < NI; ++i) {
+        const int key = min(key0 + TL::row_of(NI * wave + i, lane), a.Lk - 1);
+        const int c = TL::chunk_of(NI * wave + i, lane);
+        lds_load16(kb + (int64_t)key * a.ks[1] + 8 * c, kl + i * BLK);
+        lds_load16(vb + (int64_t)key * a.vs[1] + 8 * c, vl + i * BLK);
       }
     }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KPASS; ++i) *(u32x4*)&Ks[buf][rm_off<D>(kr0 + KRP * i, kc)] = kreg[i];
-    tr_write<KG>(Vt[buf], vreg, vg * KG, vc);
   };
 
   f32x16 acc[NMD];
@@ -114,8 +114,7 @@ void fwd_mfma(KArgs a) {
     for (int t = 0; t < 2; ++t) {
       u32x4 ka[NKD];
 #pragma unroll
-      for (int kd = 0; kd < NKD; ++kd)
-        ka[kd] = *(const u32x4*)&Ks[buf][rm_off<D>(32 * t + l32, 2 * kd + hi)];
+      for (int kd = 0; kd < NKD; ++kd) ka[kd] = *(const u32x4*)&Ks[buf][kro[kd] + 32 * t * D];
       st[t] = f32x16{};
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(ka[kd], qf[kd], st[t]);
@@ -155,27 +154,30 @@ void fwd_mfma(KArgs a) {
         pk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(p0, p1);
       }
     }
-    // O^T += V^T P^T
+    // O^T += V^T P^T, V^T operands by transposed reads of the row-major V tile
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
-      const int d = 32 * mt + l32;
       u32x4 va[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) va[ks] = *(const u32x4*)&Vt[buf][tchunk(d, ks, hi)];
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x2 lo = lds_read_tr(&Vs[buf][vto[mt][0] + 16 * ks * D]);
+        const u32x2 up = lds_read_tr(&Vs[buf][vto[mt][1] + 16 * ks * D]);
+        va[ks] = u32x4{lo[0], lo[1], up[0], up[1]};
+      }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) acc[mt] = E::mfma(va[ks], pk[ks], acc[mt]);
     }
   };
 
-  if (nsb > 0) load(0);
+  if (nsb > 0) issue(0, 0);
   for (int s = 0; s < nsb; ++s) {
     const int buf = s & 1;
-    store(buf);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
+    __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
     uint64_t mw = 0;
     if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
-    if (s + 1 < nsb) load(s + 1);
+    if (s + 1 < nsb) issue(s + 1, buf ^ 1);
     step(buf, mask >= 0, mw);
   }
 
