@@ -58,28 +58,55 @@ __device__ __forceinline__ float block_max256(float x, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// NPART workgroups; grid-stride over (b, q, h) rows, 16 lanes per row.
+// NPART workgroups; grid-stride over (b, q, h) rows, 16 lanes per row, four
+// rows in flight per lane group.
 template <int D, class Tag, bool O_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
 void bwd_absmax(KArgs a) {
   constexpr int PER = D / 16;
+  constexpr int UNR = 4;
   __shared__ float red[4];
-  const int64_t nrows = (int64_t)a.B * a.Lq * a.Hq;
+  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
   const int sub = threadIdx.x & 15;
+  const uint32_t step = gridDim.x * 16;
   float mx = 0.f;
-  for (int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4); row < nrows;
-       row += (int64_t)gridDim.x * 16) {
-    const int h = (int)(row % a.Hq);
-    const int64_t bq = row / a.Hq;
-    const int q = (int)(bq % a.Lq), b = (int)(bq / a.Lq);
-    float g[PER];
-    load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
-                            sub, g);
+  for (uint32_t r0 = blockIdx.x * 16 + (threadIdx.x >> 4); r0 < nrows; r0 += UNR * step) {
+    float g[UNR][PER];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) mx = fmaxf(mx, fabsf(g[i]));
+    for (int u = 0; u < UNR; ++u) {
+      const uint32_t row = min(r0 + u * step, nrows - 1);  // a repeated row leaves the max unchanged
+      const int h = (int)(row % (uint32_t)a.Hq);
+      const uint32_t bq = row / (uint32_t)a.Hq;
+      const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
+      load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
+                              sub, g[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) mx = fmaxf(mx, fabsf(g[u][i]));
   }
   mx = block_max256(mx, red);
   if (threadIdx.x == 0) a.part[blockIdx.x] = mx;
+}
+
+// One workgroup: the power-of-two scale s with max |dO * s| < 2^14, and 1/s.
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
+void bwd_scale(KArgs a) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < NPART; i += 256) m = fmaxf(m, a.part[i]);
+  m = block_max256(m, red);
+  if (threadIdx.x == 0) {
+    float s = 1.f;
+    if (m > 0.f && m <= 3.4e38f) {
+      int e;
+      frexpf(m, &e);  // m < 2^e
+      s = ldexpf(1.f, min(126, max(-126, 14 - e)));
+    }
+    a.dscale[0] = s;
+    a.dscale[1] = 1.f / s;
+  }
 }
 
 // 16 lanes per (b, q, h) row, 16 rows per workgroup.  MODE 0: delta only
@@ -91,27 +118,14 @@ void bwd_pre(KArgs a) {
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
   constexpr int PER = D / 16;
-  __shared__ float red[4];
-  float s = 1.f;
-  if constexpr (MODE > 0) {
-    const float m = block_max256(fmaxf(a.part[threadIdx.x], a.part[threadIdx.x + 256]), red);
-    if (m > 0.f && m <= 3.4e38f) {
-      int e;
-      frexpf(m, &e);  // m < 2^e
-      s = ldexpf(1.f, min(126, max(-126, 14 - e)));
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-      a.dscale[0] = s;
-      a.dscale[1] = 1.f / s;
-    }
-  }
-  const int64_t nrows = (int64_t)a.B * a.Lq * a.Hq;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
+  const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
-  const int h = (int)(row % a.Hq);
-  const int64_t bq = row / a.Hq;
-  const int q = (int)(bq % a.Lq), b = (int)(bq / a.Lq);
+  const float s = MODE > 0 ? a.dscale[0] : 1.f;
+  const int h = (int)(row % (uint32_t)a.Hq);
+  const uint32_t bq = row / (uint32_t)a.Hq;
+  const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
   float x[PER], g[PER];
   load_row<D, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2], sub, x);
   load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
@@ -126,13 +140,13 @@ void bwd_pre(KArgs a) {
   if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
   if constexpr (MODE > 0) {
     // dense [B, Lq, Hq, D] copies
-    uint16_t* w = (uint16_t*)a.dOhw + row * D + sub * PER;
+    uint16_t* w = (uint16_t*)a.dOhw + (int64_t)row * D + sub * PER;
 #pragma unroll
     for (int i = 0; i < PER; i += 4)
       *(u32x2*)(w + i) = u32x2{H::pack2(g[i] * s, g[i + 1] * s), H::pack2(g[i + 2] * s, g[i + 3] * s)};
   }
   if constexpr (MODE == 2) {
-    uint16_t* w = (uint16_t*)a.dO16w + row * D + sub * PER;
+    uint16_t* w = (uint16_t*)a.dO16w + (int64_t)row * D + sub * PER;
 #pragma unroll
     for (int i = 0; i < PER; i += 4)
       *(u32x2*)(w + i) = u32x2{E::pack2(g[i], g[i + 1]), E::pack2(g[i + 2], g[i + 3])};
@@ -773,6 +787,7 @@ hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int s
 #define MATTN_PRE(DD, TAG, OF32, MODE)                                                           \
   do {                                                                                           \
     hipLaunchKernelGGL((bwd_absmax<DD, TAG, OF32>), dim3(NPART), dim3(256), 0, st, a);           \
+    hipLaunchKernelGGL(bwd_scale, dim3(1), dim3(256), 0, st, a);                                 \
     hipLaunchKernelGGL((bwd_pre<DD, TAG, OF32, MODE>), dim3(pre_grid), dim3(256), 0, st, a);     \
   } while (0)
 #define MATTN_BWD(DD, TAG, MODE)                                                                 \

@@ -120,7 +120,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
       !strides_ok(p->dv_stride, es) || !strides_ok(p->o_stride, eo) || !strides_ok(p->do_stride, eo))
     return MATTN_ERR_STRIDE;
   const int64_t nqt = cdiv(p->Lq, MATTN_TILE_Q), nkt = cdiv(p->Lk, MATTN_TILE_K);
-  if ((int64_t)p->B * p->Hq * nqt >= (1ll << 31) || (int64_t)p->B * p->Hkv * nkt >= (1ll << 31) ||
+  if ((int64_t)p->B * p->Hq * p->Lq >= (1ll << 31) || (int64_t)p->B * p->Hq * nqt >= (1ll << 31) || (int64_t)p->B * p->Hkv * nkt >= (1ll << 31) ||
       (int64_t)p->Lq + MATTN_TILE_Q >= (1ll << 31) || (int64_t)p->Lk + MATTN_TILE_K >= (1ll << 31))
     return MATTN_ERR_TOO_LARGE;
   // kernels address rows inside one (batch, head) slice with 32-bit element offsets

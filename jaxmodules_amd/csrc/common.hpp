@@ -37,7 +37,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int TILE = 128;  // map tile edge (MATTN_TILE_Q == MATTN_TILE_K)
-constexpr int NPART = 512;  // workgroups of the max |dO| pass
+constexpr int NPART = 1024;  // workgroups of the max |dO| pass
 constexpr float NEG_INF = -__builtin_inff();
 
 // Arguments of every kernel (passed by value in the kernarg segment).
