@@ -96,9 +96,9 @@ typedef struct mattn_blockmap {
   const int32_t* row_ent;    /* [2*nnz]: (key tile, mask id) per row entry   */
   const int32_t* col_ptr;    /* [map_b*map_h*nkt + 1]                        */
   const int32_t* col_ent;    /* [2*nnz]: (query tile, mask id) per column    */
-  /* row_bits[m][q][w]: bit j of word w = key 64*w + j of tile m allowed for
-   * query row q; col_bits[m][k][w]: bit j of word w = query 64*w + j allowed
-   * for key k.  [n_masks][128][2] uint64 each.                              */
+  /* row_bits[m][w][q]: bit j = key 64*w + j of tile m allowed for query row
+   * q; col_bits[m][w][k]: bit j = query 64*w + j allowed for key k.
+   * [n_masks][2][128] uint64 each.                                          */
   const uint64_t* row_bits;
   const uint64_t* col_bits;
   /* Launch order of the work items, one workgroup each, -1 = idle slot.

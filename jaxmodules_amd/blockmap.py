@@ -156,8 +156,8 @@ class TileMap:
     row_ent: np.ndarray     # int32 [nnz, 2] (key tile, mask id)
     col_ptr: np.ndarray     # int32 [map_b*map_h*nkt + 1]
     col_ent: np.ndarray     # int32 [nnz, 2] (query tile, mask id)
-    row_bits: np.ndarray    # uint64 [n_masks, 128, 2]
-    col_bits: np.ndarray    # uint64 [n_masks, 128, 2]
+    row_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, q] bit j = key 64w + j allowed
+    col_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, k] bit j = query 64w + j allowed
     q_order: np.ndarray     # int32 launch order of (b, h, query tile) items
     kv_order: np.ndarray    # int32 launch order of (b, kv head, key tile) items
     pairs: int              # allowed (b, h, q, k) positions over all B x Hq
@@ -189,11 +189,16 @@ class TileMap:
             if mid < 0:
                 out[r, :, kt * TILE:(kt + 1) * TILE] = True
             else:
-                bits = np.unpackbits(self.row_bits[mid].view(np.uint8).reshape(TILE, 16), axis=1,
-                                     bitorder="little").astype(bool)
+                bits = unpack_tile(self.row_bits[mid])
                 out[r, :, kt * TILE:(kt + 1) * TILE] = bits
         out = out.reshape(self.map_b, self.map_h, self.nqt * TILE, self.nkt * TILE)
         return out[:, :, :self.Lq, :self.Lk]
+
+
+def unpack_tile(words: np.ndarray) -> np.ndarray:
+    """bool [128, 128] of one tile mask stored as uint64 [2, 128] ([half][row])."""
+    w = np.ascontiguousarray(np.asarray(words, np.uint64).T)          # [row, half]
+    return np.unpackbits(w.view(np.uint8).reshape(TILE, 16), axis=1, bitorder="little").astype(bool)
 
 
 def _probe_dependence(mask4, B, Hq, N, L):
@@ -272,7 +277,11 @@ def trace(plan: Plan) -> TileMap:
             tiles = t[mb[part], mh[part], :, kt[part], :]          # [P, 128 q, 128 k]
             rb = np.ascontiguousarray(np.packbits(tiles, axis=2, bitorder="little")).view(np.uint64)
             cb = np.ascontiguousarray(np.packbits(tiles.transpose(0, 2, 1), axis=2,
-                                                  bitorder="little")).view(np.uint64)  # [P,128,2]
+                                                  bitorder="little")).view(np.uint64)
+            # [P, 128 rows, 2 words] -> [P, 2 words, 128 rows]: a wave's 32 rows of one
+            # 64-wide half are then one contiguous 256-byte block
+            rb = np.ascontiguousarray(rb.transpose(0, 2, 1))
+            cb = np.ascontiguousarray(cb.transpose(0, 2, 1))
             for i, p in enumerate(part):
                 key = rb[i].tobytes()
                 mid = masks.get(key)
@@ -322,8 +331,8 @@ def trace(plan: Plan) -> TileMap:
     kv_order = _lpt_xcd_order(kvw, kvgroups)
 
     pairs = pairs_map * (B // map_b) * (Hq // map_h)
-    rb = np.stack(row_bits) if row_bits else np.zeros((0, TILE, 2), np.uint64)
-    cb = np.stack(col_bits) if col_bits else np.zeros((0, TILE, 2), np.uint64)
+    rb = np.stack(row_bits) if row_bits else np.zeros((0, 2, TILE), np.uint64)
+    cb = np.stack(col_bits) if col_bits else np.zeros((0, 2, TILE), np.uint64)
     return TileMap(B, Hq, Hkv, N, L, map_b, map_h, nqt, nkt,
                    row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent,
                    np.ascontiguousarray(rb), np.ascontiguousarray(cb), q_order, kv_order, pairs,

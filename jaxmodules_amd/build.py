@@ -18,7 +18,11 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libmattn.so")
-SOURCES = ["fwd.hip", "bwd.hip", "capi.hip"]
+SOURCES = ["fwd.hip", "bwd_pre.hip", "bwd_dq.hip", "bwd_dkdv.hip", "capi.hip"]
+# machine-scheduler strategy per source: the ILP-oriented ones hoist LDS operand
+# reads ahead of the MFMA chains; each file uses the one measured fastest
+# without register spills for its kernels
+SCHED = {"fwd.hip": "iterative-ilp", "bwd_dq.hip": "iterative-ilp", "bwd_dkdv.hip": "iterative-ilp"}
 ARCH = "gfx950"
 
 
@@ -39,9 +43,6 @@ def common_flags(extra=()):
         "-I", CSRC,
         # packed fp32 VALU ops are kept out of the generated code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # the ILP-oriented machine scheduler hoists LDS operand reads ahead of
-        # the MFMA chains (measured faster on every MFMA kernel here)
-        "-mllvm", "-amdgpu-sched-strategy=iterative-ilp",
         "-Wno-unused-result",
         *extra,
     ]
@@ -57,26 +58,32 @@ def _run(cmd):
     return err
 
 
-def build(verbose: bool = False, extra_flags=()) -> str:
+def build(verbose: bool = False, extra_flags=(), sched_override=None, lib_path=None) -> str:
+    """sched_override: a scheduler strategy for every MFMA source ("" = LLVM's
+    default); lib_path: where to write the library (default: in-tree)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     cc = hipcc()
     flags = common_flags(extra_flags)
 
     def compile_one(src):
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-        err = _run([cc, *flags, "-c", os.path.join(CSRC, src), "-o", obj])
+        sched = ["-mllvm", f"-amdgpu-sched-strategy={SCHED[src]}"] if src in SCHED else []
+        if sched_override is not None and src in SCHED:
+            sched = ["-mllvm", f"-amdgpu-sched-strategy={sched_override}"] if sched_override else []
+        err = _run([cc, *flags, *sched, "-c", os.path.join(CSRC, src), "-o", obj])
         if verbose and err.strip():
             print(err, file=sys.stderr)
         return obj
 
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(compile_one, SOURCES))
-    tmp = LIB_PATH + ".tmp"
+    out = lib_path or LIB_PATH
+    tmp = out + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

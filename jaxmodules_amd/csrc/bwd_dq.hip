@@ -1,0 +1,214 @@
+// dQ kernel of the masked-attention backward (the custom_vjp bwd rule,
+// /root/reference/jaxmodules/attention.py:266-342): one workgroup per
+// 128-query map row, dQ accumulated in registers and written once.
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace mattn {
+
+// ---------------------------------------------------------------------------
+// dQ (MFMA)
+// ---------------------------------------------------------------------------
+// Each wave owns 32 queries; per 64-key sub-block:
+//   S^T  = K Q^T         (A: K rows from LDS, B: Q^T in registers)
+//   dP^T = V dO^T        (A: V rows from LDS, B: dO^T in registers)
+//   dS^T = P^T * (dP^T - delta)    (each lane owns one query: lse, delta scalars)
+//   dQ^T += K^T dS^T     (A: K^T by transposed reads of the same K tile)
+// K and V are double-buffered (one array per buffer, loop unrolled by two),
+// swizzled row-major tiles filled by direct global->LDS loads.
+template <int D, class Tag>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void bwd_dq_mfma(KArgs a) {
+  using E = Elt<Tag>;
+  using TL = TileLoad<D>;
+  constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
+  constexpr int BN = 64;
+  constexpr int NKD = D / 16;
+  constexpr int NMD = D / 32;
+  constexpr int NI = D / 32;       // load instructions per wave per tile
+  constexpr int BLK = 512;         // elements one load instruction fills
+
+  __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[BN * D], V1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];
+
+  const int item = a.q_order[blockIdx.x];
+  if (item < 0) return;
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int nsb = 2 * (e1 - e0);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int qloc = wave * 32 + l32;
+  const int q = qt * TILE + qloc;
+  const int qc = min(q, a.Lq - 1);
+  const float c2 = a.scale_log2;
+
+  u32x4 qf[NKD], df[NKD];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
+                         (int64_t)h * a.qs[2] + 8 * hi;
+    // bfloat16 inputs: dO rounded to bfloat16; float16 inputs: dO * s in float16
+    const void* dsrc = IS_BF16 ? a.dO16 : a.dOh;
+    const uint16_t* dp = (const uint16_t*)dsrc + (((int64_t)b * a.Lq + qc) * a.Hq + h) * D + 8 * hi;
+#pragma unroll
+    for (int kd = 0; kd < NKD; ++kd) {
+      qf[kd] = *(const u32x4*)(qp + 16 * kd);
+      df[kd] = *(const u32x4*)(dp + 16 * kd);
+    }
+  }
+  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
+  const float nlse = -a.lse[rs];
+  const float dl = a.delta[rs];
+  const float dps = IS_BF16 ? 1.f : a.dscale[1];  // undoes the dO scale of float16 inputs
+
+  const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
+  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
+  uint32_t kld[NI], vld[NI];  // source byte offsets of this lane's load slots
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
+    vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
+  }
+  int rro[NKD];               // row-read offsets (K and V tiles share the layout)
+#pragma unroll
+  for (int kd = 0; kd < NKD; ++kd) rro[kd] = sw_off<D>(l32, 2 * kd + hi);
+  int kto[NMD][2];            // K^T transposed-read offsets
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+    kto[mt][0] = tr_src<D>(lane, mt, 0);
+    kto[mt][1] = tr_src<D>(lane, mt, 1);
+  }
+  const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);
+  EntryCache ec;
+
+  auto issue = [&](int s, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    int kt, mask;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
+    const int key0 = kt * TILE + (s & 1) * BN;
+    uint16_t* kl = (BUF ? K1 : K0) + wofs;
+    uint16_t* vl = (BUF ? V1 : V0) + wofs;
+    if (mask >= 0) {
+      const uint32_t* src = (const uint32_t*)(a.row_bits + ((int64_t)mask * 2 + (s & 1)) * TILE + wave * 32);
+      __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
+                                       4, 0, 0);
+    }
+    if (key0 + BN <= a.Lk) {
+      const char* kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
+      const char* vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        lds_load16(kp + kld[i], kl + i * BLK);
+        lds_load16(vp + vld[i], vl + i * BLK);
+      }
+    } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int key = min(key0 + TL::row_of(NI * wave + i, lane), a.Lk - 1);
+        const int c = TL::chunk_of(NI * wave + i, lane);
+        lds_load16(kb + (int64_t)key * a.ks[1] + 8 * c, kl + i * BLK);
+        lds_load16(vb + (int64_t)key * a.vs[1] + 8 * c, vl + i * BLK);
+      }
+    }
+  };
+
+  f32x16 acc[NMD];
+#pragma unroll
+  for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
+
+  // Each 32-key half t of the sub-block is carried through S^T, dP^T, dS^T and
+  // its two dQ k-steps before the next half starts (halves the live state).
+  auto step = [&](auto bufc, bool masked) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* Kb = BUF ? K1 : K0;
+    const uint16_t* Vb = BUF ? V1 : V0;
+    const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x16 st = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int kd = 0; kd < NKD; ++kd) {
+        const u32x4 ka = *(const u32x4*)&Kb[rro[kd] + 32 * t * D];
+        const u32x4 va = *(const u32x4*)&Vb[rro[kd] + 32 * t * D];
+        st = E::mfma(ka, qf[kd], st);
+        dp = E::mfma(va, df[kd], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], c2, nlse));
+      if (masked) {
+        const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (!mask_bit(w32, r)) st[r] = 0.f;
+      }
+      u32x4 pk[2];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float d0 = st[r] * fmaf(dp[r], dps, -dl);
+        const float d1 = st[r + 1] * fmaf(dp[r + 1], dps, -dl);
+        pk[r >> 3][(r & 7) >> 1] = E::pack2(d0, d1);
+      }
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int ks = 2 * t + kk;
+          const u32x2 lo = lds_read_tr(&Kb[kto[mt][0] + 16 * ks * D]);
+          const u32x2 up = lds_read_tr(&Kb[kto[mt][1] + 16 * ks * D]);
+          acc[mt] = E::mfma(u32x4{lo[0], lo[1], up[0], up[1]}, pk[kk], acc[mt]);
+        }
+      }
+    }
+  };
+
+  auto iter = [&](int s, auto bufc) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int kt, mask;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
+    if (s + 1 < nsb) issue(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
+    step(bufc, mask >= 0);
+  };
+  if (nsb > 0) issue(0, std::integral_constant<int, 0>{});
+  for (int s = 0; s < nsb; s += 2) {
+    iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
+  }
+
+  if (q >= a.Lq) return;
+  char* op = (char*)a.dq;
+  const int64_t orow = (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2];
+#pragma unroll
+  for (int mt = 0; mt < NMD; ++mt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * mt + 8 * j + 4 * hi;
+      *(u32x2*)(op + 2 * (orow + d)) =
+          u32x2{E::pack2(acc[mt][4 * j] * a.scale, acc[mt][4 * j + 1] * a.scale),
+                E::pack2(acc[mt][4 * j + 2] * a.scale, acc[mt][4 * j + 3] * a.scale)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launcher
+// ---------------------------------------------------------------------------
+
+hipError_t launch_dq(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
+  if (dtype == MATTN_BF16) {
+    if (D == 64) hipLaunchKernelGGL((bwd_dq_mfma<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dq_mfma<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+  } else {
+    if (D == 64) hipLaunchKernelGGL((bwd_dq_mfma<64, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dq_mfma<128, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mattn

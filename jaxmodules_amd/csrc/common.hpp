@@ -251,9 +251,34 @@ __device__ __forceinline__ bool mask_bit(uint32_t w32, int r) {
   return (w32 >> (8 * (r >> 2) + (r & 3))) & 1u;
 }
 
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap: no LDS access, so
+// no wait on outstanding global->LDS loads)
 __device__ __forceinline__ float wave_max32(float x) {
-  return fmaxf(x, __shfl_xor(x, 32));
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float wave_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Tile-map entries of one map row/column, 64 at a time, one per lane: read
+// back with v_readlane at a wave-uniform index (no memory access inside the
+// loop, so no wait on the global->LDS loads in flight).  ent holds
+// (tile, mask id) pairs; [e0, e1) is the range this workgroup walks.
+struct EntryCache {
+  int tile = 0, mask = 0, base = -(1 << 30);
+  __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m) {
+    if (e - base >= 64 || e < base) {  // wave-uniform
+      base = e;
+      const int idx = min(e + lane, e1 - 1);
+      tile = ent[2 * idx];
+      mask = ent[2 * idx + 1];
+    }
+    t = __builtin_amdgcn_readlane(tile, e - base);
+    m = __builtin_amdgcn_readlane(mask, e - base);
+  }
+};
 
 __device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int t) {
   return ((a.map_b == 1 ? 0 : b) * a.map_h + (a.map_h == 1 ? 0 : h)) * n + t;

@@ -32,8 +32,11 @@ void fwd_mfma(KArgs a) {
   // (base-2 units); until then P may reach 2^8, harmless in 16-bit and fp32.
   constexpr float RESCALE_SLACK = 8.f;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * D];
+  // one array per buffer: the compiler then knows the loads landing in one
+  // buffer cannot alias the operand reads of the other (no vmcnt waits mid-step)
+  __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[BN * D], V1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0) return;
@@ -62,11 +65,11 @@ void fwd_mfma(KArgs a) {
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  uint32_t kld[NI], vld[NI];  // loop-invariant source offsets of this lane's load slots
+  uint32_t kld[NI], vld[NI];  // loop-invariant source byte offsets of this lane's load slots
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    kld[i] = TL::src_off(NI * wave + i, lane, a.ks[1]);
-    vld[i] = TL::src_off(NI * wave + i, lane, a.vs[1]);
+    kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
+    vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
   }
   int kro[NKD];               // K row-read offsets (A operand of S^T), row tile 0
 #pragma unroll
@@ -78,14 +81,23 @@ void fwd_mfma(KArgs a) {
     vto[mt][1] = tr_src<D>(lane, mt, 1);
   }
 
-  auto issue = [&](int s, int buf) {  // global -> LDS loads of sub-block s
-    const int kt = a.row_ent[2 * (e0 + (s >> 1))];
+  const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);  // this wave's load block
+  EntryCache ec;
+  auto issue = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
+    constexpr int BUF = decltype(bufc)::value;
+    int kt, mask;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
     const int key0 = kt * TILE + (s & 1) * BN;
-    uint16_t* kl = &Ks[buf][NI * wave * BLK];
-    uint16_t* vl = &Vs[buf][NI * wave * BLK];
+    uint16_t* kl = (BUF ? K1 : K0) + wofs;
+    uint16_t* vl = (BUF ? V1 : V0) + wofs;
+    if (mask >= 0) {  // this wave's 32 mask words (256 bytes), one dword per lane
+      const uint32_t* src = (const uint32_t*)(a.row_bits + ((int64_t)mask * 2 + (s & 1)) * TILE + wave * 32);
+      __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
+                                       4, 0, 0);
+    }
     if (key0 + BN <= a.Lk) {
-      const uint16_t* kp = kb + (int64_t)key0 * a.ks[1];
-      const uint16_t* vp = vb + (int64_t)key0 * a.vs[1];
+      const char* kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
+      const char* vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         lds_load16(kp + kld[i], kl + i * BLK);
@@ -107,19 +119,23 @@ void fwd_mfma(KArgs a) {
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
   float m2 = NEG_INF, l = 0.f;  // running max (base-2 units) and partial row sum
 
-  auto step = [&](int buf, bool masked, uint64_t mw) {
+  auto step = [&](auto bufc, bool masked) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* Kb = BUF ? K1 : K0;
+    const uint16_t* Vb = BUF ? V1 : V0;
     // S^T = K Q^T, one row tile's K operands staged ahead of its MFMA chain
     f32x16 st[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       u32x4 ka[NKD];
 #pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) ka[kd] = *(const u32x4*)&Ks[buf][kro[kd] + 32 * t * D];
+      for (int kd = 0; kd < NKD; ++kd) ka[kd] = *(const u32x4*)&Kb[kro[kd] + 32 * t * D];
       st[t] = f32x16{};
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(ka[kd], qf[kd], st[t]);
     }
     if (masked) {
+      const uint64_t mw = (BUF ? M1 : M0)[qloc];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
@@ -160,8 +176,8 @@ void fwd_mfma(KArgs a) {
       u32x4 va[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const u32x2 lo = lds_read_tr(&Vs[buf][vto[mt][0] + 16 * ks * D]);
-        const u32x2 up = lds_read_tr(&Vs[buf][vto[mt][1] + 16 * ks * D]);
+        const u32x2 lo = lds_read_tr(&Vb[vto[mt][0] + 16 * ks * D]);
+        const u32x2 up = lds_read_tr(&Vb[vto[mt][1] + 16 * ks * D]);
         va[ks] = u32x4{lo[0], lo[1], up[0], up[1]};
       }
 #pragma unroll
@@ -169,19 +185,23 @@ void fwd_mfma(KArgs a) {
     }
   };
 
-  if (nsb > 0) issue(0, 0);
-  for (int s = 0; s < nsb; ++s) {
-    const int buf = s & 1;
+  // sub-block s computes from buffer s % 2 while s + 1 loads into the other;
+  // the loop is unrolled by two so that every buffer index is static
+  auto iter = [&](int s, auto bufc) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
-    const int mask = a.row_ent[2 * (e0 + (s >> 1)) + 1];
-    uint64_t mw = 0;
-    if (mask >= 0) mw = a.row_bits[((int64_t)mask * TILE + qloc) * 2 + (s & 1)];
-    if (s + 1 < nsb) issue(s + 1, buf ^ 1);
-    step(buf, mask >= 0, mw);
+    int kt, mask;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
+    if (s + 1 < nsb) issue(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
+    step(bufc, mask >= 0);
+  };
+  if (nsb > 0) issue(0, std::integral_constant<int, 0>{});
+  for (int s = 0; s < nsb; s += 2) {
+    iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
   }
 
-  l += __shfl_xor(l, 32);
+  l = wave_sum32(l);
   if (q >= a.Lq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (hi == 0)
@@ -256,7 +276,7 @@ void fwd_simt(KArgs a) {
       __syncthreads();
       uint32_t bits = 0xffffffffu;
       if (mask >= 0)
-        bits = (uint32_t)(a.row_bits[((int64_t)mask * TILE + row) * 2 + (sb >> 1)] >> (32 * (sb & 1)));
+        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
       float sc[SB];
       float mx = NEG_INF;
 #pragma unroll

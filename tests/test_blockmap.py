@@ -59,8 +59,8 @@ def check_consistency(tm, plan):
     # masks are distinct and the column bits are the transposed row bits
     seen = set()
     for m in range(tm.n_masks):
-        rbits = np.unpackbits(tm.row_bits[m].view(np.uint8).reshape(128, 16), axis=1, bitorder="little")
-        cbits = np.unpackbits(tm.col_bits[m].view(np.uint8).reshape(128, 16), axis=1, bitorder="little")
+        rbits = bm.unpack_tile(tm.row_bits[m])
+        cbits = bm.unpack_tile(tm.col_bits[m])
         assert np.array_equal(rbits.T, cbits)
         assert 0 < rbits.sum() < 128 * 128
         assert rbits.tobytes() not in seen
