@@ -18,6 +18,11 @@ per-query-block recompute in the backward pass), timed on a bounded sample of
 query blocks of one (batch, head) slice and scaled by the exact block count.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|target|cfg3|cfg4|cfg5]
+                       [--no-target] [--no-cpu] [--copy-probe]
+
+roofline.traffic is read from profiles/traffic_<config>.md (rocprofv3
+FETCH_SIZE and WRITE_SIZE of the dominant kernel, calibrated on the 1 GiB copy
+that --copy-probe launches); null when that file is absent.
 """
 from __future__ import annotations
 
@@ -35,6 +40,26 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0
+COPY_PROBE_BYTES = 1 << 30  # --copy-probe: one int64 device copy of this size (PMC calibration)
+# kernel symbol of each timed stage (for the rocprofv3 counter summaries)
+SYMBOL = {"fwd": "fwd_mfma", "bwd_dkdv": "bwd_dkdv_mfma", "bwd_dq": "bwd_dq_mfma"}
+
+
+def measured_traffic(config, stage):
+    """HBM bytes per launch of ``stage`` from the committed rocprofv3 counter
+    summary of this workload (FETCH_SIZE + WRITE_SIZE, scaled by the copy-probe
+    calibration); None when there is none."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.md")
+    if not os.path.exists(path):
+        return None
+    pat = re.compile(r"^traffic\[(\w+)\]\s*=\s*(\d+)\s*$")
+    for line in open(path):
+        m = pat.match(line.strip())
+        if m and m.group(1) == SYMBOL.get(stage):
+            return int(m.group(2))
+    return None
 
 
 def _docs(L, seed, mean=2048, minlen=64):
@@ -210,6 +235,8 @@ def main():
     ap.add_argument("--no-target", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed region, copy 1 GiB once (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -223,6 +250,13 @@ def main():
     r = Runner(args.config)
     _PAIRS[args.config] = r.pairs
     ms, kern = r.measure(args.steps, args.warmup)
+    if args.copy_probe:
+        src = torch.ones(COPY_PROBE_BYTES // 8, dtype=torch.int64, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     total = r.fwd_flop + r.bwd_flop
     value = total / (ms * 1e-3) / 1e12
     # dominant kernel and its algorithmic FLOPs per launch
@@ -230,7 +264,8 @@ def main():
     dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern[n])
     ach = alg[dom] / (kern[dom] * 1e-3) / 1e12
     roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+            "traffic": measured_traffic(args.config, dom),
             "kernel_ms": round(kern[dom], 4),
             "flop_per_launch": alg[dom]}
     out = {

@@ -3,8 +3,10 @@
 ``masked_attention_via_map`` and the ``block_mask`` machinery, forward and
 backward, on hand-written HIP kernels behind the C ABI in ``include/mattn.h``.
 """
-from . import blockmap
+from . import block_mask, blockmap
 from .attention import default_kernel, masked_attention_via_map, threshold_kernel
+from .block_mask import BlockMask, create_block_mask
 
 __version__ = "0.1"
-__all__ = ["masked_attention_via_map", "default_kernel", "threshold_kernel", "blockmap"]
+__all__ = ["masked_attention_via_map", "default_kernel", "threshold_kernel", "blockmap",
+           "block_mask", "BlockMask", "create_block_mask"]

@@ -248,12 +248,20 @@ def _lpt_xcd_order(weights: np.ndarray, groups: np.ndarray) -> np.ndarray:
 
 def trace(plan: Plan) -> TileMap:
     """Traces the effective mask of ``plan`` into a TileMap."""
+    map_b, map_h = _probe_dependence(plan.mask4, plan.B, plan.Hq, plan.N, plan.L)
+    nkt = -(-plan.L // TILE)
+    return trace_strips(lambda q0: _strip_mask(plan, map_b, map_h, q0, nkt), plan.B, plan.Hq,
+                        plan.Hkv, plan.N, plan.L, map_b, map_h)
+
+
+def trace_strips(strip, B, Hq, Hkv, N, L, map_b, map_h) -> TileMap:
+    """TileMap of the mask whose query rows [q0, q0+128) ``strip(q0)`` returns as
+    bool [map_b, map_h, 128, nkt*128] (False beyond N and L); map_b / map_h are
+    1 where the mask is the same for every batch / head."""
     import time
 
     t0 = time.perf_counter()
-    B, Hq, Hkv, N, L = plan.B, plan.Hq, plan.Hkv, plan.N, plan.L
     nqt, nkt = -(-N // TILE), -(-L // TILE)
-    map_b, map_h = _probe_dependence(plan.mask4, B, Hq, N, L)
     nmap = map_b * map_h
 
     masks: dict = {}
@@ -262,7 +270,8 @@ def trace(plan: Plan) -> TileMap:
     pairs_map = 0
     n_full = n_partial = 0
     for qt in range(nqt):
-        m = _strip_mask(plan, map_b, map_h, qt * TILE, nkt)
+        m = strip(qt * TILE)
+        assert m.shape == (map_b, map_h, TILE, nkt * TILE), m.shape
         pairs_map += int(np.count_nonzero(m))
         t = m.reshape(map_b, map_h, TILE, nkt, TILE)
         anyb = t.any(axis=(2, 4))
