@@ -103,7 +103,10 @@ typedef struct mattn_blockmap {
   const uint64_t* col_bits;
   /* Launch order of the work items, one workgroup each, -1 = idle slot.
    * q item   = (b * Hq  + h ) * nqt + query tile   (forward and dQ)
-   * kv item  = (b * Hkv + hk) * nkt + key tile     (dK/dV)                  */
+   * kv item  = (b * Hkv + hk) * nkt + key tile     (dK/dV)
+   * Each item should appear once.  Entries outside [0, B*Hq*nqt) and
+   * [0, B*Hkv*nkt) are skipped by the kernels (their outputs are not
+   * written), since device arrays cannot be checked on the host.           */
   const int32_t* q_order;
   const int32_t* kv_order;
   int32_t n_q_order, n_kv_order;

@@ -8,7 +8,15 @@ Mirrors the public interface of ``/root/reference/jaxmodules/attention.py``:
   custom_vjp (attention.py:180,244-345) realised as a
   ``torch.autograd.Function`` whose forward calls ``mattn_fwd`` and whose
   backward calls ``mattn_bwd`` (the C ABI in ``include/mattn.h``);
-* ``default_kernel`` / ``threshold_kernel`` (attention.py:18-50).
+* ``default_kernel`` / ``threshold_kernel`` (attention.py:18-50);
+* ``flex_attention(query, key, value, score_mod, block_mask, scale,
+  enable_gqa, return_lse)`` (attention.py:456-692) on the same kernels, its
+  ``BlockMask`` handed over as a tile map (``BlockMask.tile_map``).
+
+The kernels are built for head dimensions 64 and 128; other head dimensions
+up to 128 are zero-padded on the GPU to the next of the two (zero columns of
+Q and K leave every score unchanged, zero columns of V give zero output
+columns, which are sliced off; the scale stays 1/sqrt(true d)).
 
 Arrays are torch tensors on the GPU (jax is not available in this image; the
 jax.ffi binding a jax user would register is described with the C ABI).  The
@@ -28,8 +36,8 @@ import torch
 from . import _lib
 from . import blockmap as bmap
 
-__all__ = ["masked_attention_via_map", "default_kernel", "threshold_kernel", "trace_call",
-           "clear_cache", "mattn_forward", "mattn_backward"]
+__all__ = ["masked_attention_via_map", "flex_attention", "flex_attention_slow", "default_kernel",
+           "threshold_kernel", "trace_call", "clear_cache", "mattn_forward", "mattn_backward"]
 
 
 # ---------------------------------------------------------------------------
@@ -82,6 +90,7 @@ _CACHE_SIZE = 32
 
 def clear_cache():
     _CACHE.clear()
+    _BM_CACHE.clear()
 
 
 def trace_call(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, block_size=None,
@@ -102,6 +111,16 @@ def trace_call(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, bloc
     else:
         _CACHE.move_to_end(key)
     return plan, tm
+
+
+def _check_map(tm: bmap.TileMap, q, k):
+    """The tile map must be traced for this problem's shape: its launch orders
+    enumerate (b, head, tile) items of exactly these sizes."""
+    B, N, Hq, _ = q.shape
+    got = (tm.B, tm.Lq, tm.Hq, tm.Lk, tm.Hkv)
+    want = (B, N, Hq, k.shape[1], k.shape[2])
+    if got != want:
+        raise ValueError(f"tile map traced for (B, Lq, Hq, Lk, Hkv) = {got}, called with {want}")
 
 
 def device_blockmap(tm: bmap.TileMap, device) -> _lib.MattnBlockmap:
@@ -168,12 +187,19 @@ def _stream(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float32):
-    """O [B, N, Hq, d] (out_dtype) and base-2 LSE [B, Hq, N] via mattn_fwd."""
+def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float32,
+                  heads_major: bool = False):
+    """O [B, N, Hq, d] (out_dtype) and base-2 LSE [B, Hq, N] via mattn_fwd.
+    ``heads_major`` lays O out in memory as [B, Hq, N, d] (the returned tensor
+    is the [B, N, Hq, d] view of it)."""
     lib = _lib.load()
     B, N, Hq, d = q.shape
-    o = torch.empty((B, N, Hq, d), dtype=out_dtype, device=q.device)
+    if heads_major:
+        o = torch.empty((B, Hq, N, d), dtype=out_dtype, device=q.device).transpose(1, 2)
+    else:
+        o = torch.empty((B, N, Hq, d), dtype=out_dtype, device=q.device)
     lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
+    _check_map(tm, q, k)
     p = _problem(q, k, v, o, scale)
     bm = device_blockmap(tm, q.device)
     _lib.check(lib.mattn_fwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
@@ -185,6 +211,7 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
 def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
     """(dQ, dK, dV) via mattn_bwd."""
     lib = _lib.load()
+    _check_map(tm, q, k)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
@@ -206,8 +233,8 @@ class _MaskedAttention(torch.autograd.Function):
     log-sum-exp rather than re-running the forward scan."""
 
     @staticmethod
-    def forward(ctx, q, k, v, tm, scale, out_dtype):
-        o, lse = mattn_forward(q, k, v, tm, scale, out_dtype)
+    def forward(ctx, q, k, v, tm, scale, out_dtype, heads_major=False):
+        o, lse = mattn_forward(q, k, v, tm, scale, out_dtype, heads_major)
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.tm, ctx.scale = tm, scale
         return o
@@ -217,7 +244,20 @@ class _MaskedAttention(torch.autograd.Function):
         q, k, v, o, lse = ctx.saved_tensors
         do = _ready(do.to(o.dtype))
         dq, dk, dv = mattn_backward(q, k, v, o, lse, do, ctx.tm, ctx.scale)
-        return dq, dk, dv, None, None, None
+        return dq, dk, dv, None, None, None, None
+
+
+def _kernel_dim(d: int) -> int:
+    """Head dimension the kernels run at: 64 or 128 (d zero-padded up to it)."""
+    if d <= 64:
+        return 64
+    if d <= 128:
+        return 128
+    raise NotImplementedError(f"head dimension {d} > 128 is not supported by the HIP kernels")
+
+
+def _pad_dim(x: torch.Tensor, D: int) -> torch.Tensor:
+    return x if x.shape[-1] == D else torch.nn.functional.pad(x, (0, D - x.shape[-1]))
 
 
 def masked_attention_via_map(
@@ -259,11 +299,126 @@ def masked_attention_via_map(
         raise TypeError(f"unsupported dtype {dt}")
     if plan.squeeze_batch:
         Q, K, V = Q[None], K[None], V[None]
-    q, k, v = (_ready(x.to(dt)) for x in (Q, K, V))
+    D = _kernel_dim(plan.d)
+    q, k, v = (_ready(_pad_dim(x.to(dt), D)) for x in (Q, K, V))
+    od = _out_dtype(dt, out_dtype)
+    out = _MaskedAttention.apply(q, k, v, tm, scale, od)
+    if D != plan.d:
+        out = out[..., :plan.d]
+    return out[0] if plan.squeeze_batch else out
+
+
+def _out_dtype(dt, out_dtype):
     od = torch.float32 if out_dtype is None else out_dtype
     if dt == torch.float32 and od != torch.float32:
         raise TypeError("float32 inputs produce a float32 output")
     if od not in (torch.float32, dt):
         raise TypeError(f"out_dtype must be float32 or {dt}")
-    out = _MaskedAttention.apply(q, k, v, tm, scale, od)
-    return out[0] if plan.squeeze_batch else out
+    return od
+
+
+# ---------------------------------------------------------------------------
+# flex_attention (attention.py:456-692)
+# ---------------------------------------------------------------------------
+
+_BM_CACHE: "OrderedDict[tuple, bmap.TileMap]" = OrderedDict()
+
+
+def _block_mask_tiles(block_mask, B, Hq, Hkv, L, S, element_head="kv") -> bmap.TileMap:
+    """Tile map of a BlockMask (or of the full mask when None), cached per mask
+    object and head layout."""
+    from .block_mask import BlockMask
+
+    # the launch orders of a tile map are laid out for (B, Hq, Hkv): part of the key
+    key = ("full", L, S, B, Hq, Hkv) if block_mask is None else (block_mask, B, Hq, Hkv, element_head)
+    tm = _BM_CACHE.get(key)
+    if tm is None:
+        if block_mask is None:
+            tm = BlockMask.full_mask(1, 1, L, S, (L, S)).tile_map(B, Hq, Hkv)
+        else:
+            tm = block_mask.tile_map(B, Hq, Hkv, element_head)
+        _BM_CACHE[key] = tm
+        if len(_BM_CACHE) > _CACHE_SIZE:
+            _BM_CACHE.popitem(last=False)
+    else:
+        _BM_CACHE.move_to_end(key)
+    return tm
+
+
+def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   score_mod: Optional[Callable] = None, block_mask=None, scale=None,
+                   enable_gqa: bool = False, return_lse: bool = False,
+                   out_dtype: Optional[torch.dtype] = None, *,
+                   _element_head: str = "kv") -> torch.Tensor:
+    """Block-sparse softmax attention over a ``BlockMask`` (attention.py:456-692).
+
+    query [B, Hq, L, E], key [B, Hkv, S, E], value [B, Hkv, S, E]; returns
+    [B, Hq, L, E] (float32 by default, like the reference's float32 running
+    accumulators; ``out_dtype`` = the input dtype for a 16-bit output),
+    differentiable w.r.t. query, key and value.  Query head hq reads KV head
+    hq // (Hq / Hkv).  The attention pattern is the block mask's: full tiles
+    whole, partial tiles where ``mask_mod`` holds (``BlockMask.tile_map`` gives
+    the element rule); no block mask means every key.  Rows with no allowed key
+    are zero (attention.py:598-617).
+
+    Same checks and exception types as the reference (AssertionError for shape
+    mismatches, NotImplementedError for ``return_lse``).  ``score_mod`` has no
+    kernel here and raises NotImplementedError, as does a value head dimension
+    different from the query's.
+    """
+    if return_lse:
+        raise NotImplementedError("return_lse is not supported yet")
+    B, Hq, L, E = query.shape
+    Bk, Hkv, S, Ek = key.shape
+    Bv, Hv, Sv, Ev = value.shape
+    assert E == Ek, "query and key must have the same embedding dimension"
+    assert B == Bk, "query and key must have the same batch dimension"
+    assert Sv == S, "value and key must have the same sequence length"
+    assert Bv == B, "value and query must have the same batch dimension"
+    assert Hv == Hkv, "value and key must have the same head count"
+    if block_mask is not None:
+        Qb, KVb = block_mask.Q_BLOCK_SIZE, block_mask.KV_BLOCK_SIZE
+        assert L == block_mask.Q_LEN, "query length must match block mask"
+        assert S == block_mask.KV_LEN, "key length must match block mask"
+        assert L % Qb == 0, "query length must be divisible by Q_BLOCK_SIZE"
+        assert S % KVb == 0, "key length must be divisible by KV_BLOCK_SIZE"
+    if not enable_gqa:
+        assert Hq == Hkv, "query and key must have the same head count, unless enable_gqa is True"
+    assert Hq % Hkv == 0, "kv head count must divide query head count"
+    if score_mod is not None:
+        raise NotImplementedError("score_mod is not supported by the HIP kernels")
+    if Ev != E:
+        raise NotImplementedError("value head dimension must equal the query/key head dimension")
+    if not (query.is_cuda and key.is_cuda and value.is_cuda):
+        raise RuntimeError("flex_attention runs on the GPU only (no CPU code path)")
+    dt = torch.promote_types(torch.promote_types(query.dtype, key.dtype), value.dtype)
+    if dt not in _DT:
+        raise TypeError(f"unsupported dtype {dt}")
+    s = 1.0 / math.sqrt(E) if scale is None else float(scale)
+    if not math.isfinite(s):
+        raise ValueError(f"scale must be finite, got {s}")
+    tm = _block_mask_tiles(block_mask, B, Hq, Hkv, L, S, _element_head)
+    D = _kernel_dim(E)
+    q = query.to(dt)
+    # softmax(s q.k) == softmax(|s| (-q).k); s == 0 gives uniform weights: q = 0, scale 1
+    if s < 0:
+        q, s = -q, -s
+    elif s == 0:
+        q, s = q * 0, 1.0
+    # [B, H, L, E] tensors are strided [B, L, H, E] views for the kernels
+    q, k, v = (_ready(_pad_dim(x, D).transpose(1, 2)) for x in (q, key.to(dt), value.to(dt)))
+    out = _MaskedAttention.apply(q, k, v, tm, s, _out_dtype(dt, out_dtype), True)
+    out = out.transpose(1, 2)
+    return out[..., :E] if D != E else out
+
+
+def flex_attention_slow(query, key, value, score_mod=None, block_mask=None, scale=None,
+                        enable_gqa=False, return_lse=False, out_dtype=None):
+    """The reference's materialised-mask variant (attention.py:695-820) on the
+    same kernels.  As there: Hq != Hkv is accepted without ``enable_gqa``,
+    ``return_lse`` is ignored, and partial-tile elements are evaluated with the
+    query head (``materialize_mask``).  A row with no allowed key is zero here;
+    the reference's softmax over an all -inf row gives NaN."""
+    return flex_attention(query, key, value, score_mod=score_mod, block_mask=block_mask,
+                          scale=scale, enable_gqa=True, out_dtype=out_dtype,
+                          _element_head="query")

@@ -296,7 +296,7 @@ class BlockMask:
 
     # -- hand-over to the kernels --------------------------------------------
 
-    def tile_map(self, B: int, Hq: int, Hkv: int) -> "_bm.TileMap":
+    def tile_map(self, B: int, Hq: int, Hkv: int, element_head: str = "kv") -> "_bm.TileMap":
         """The kernels' tile map of this mask applied to queries [B, Hq, Q_LEN]
         and keys [B, Hkv, KV_LEN], with the element rule of the reference's
         ``flex_attention`` (attention.py:579-676): the tiles of query head hq
@@ -304,6 +304,9 @@ class BlockMask:
         on); a full tile allows all its elements, a partial tile those where
         ``mask_mod(b', h', q, k)`` holds, b' / h' being 0 along a broadcast axis
         and h' otherwise the KV head hq // (Hq / Hkv) (attention.py:561-575).
+        ``element_head="query"`` evaluates with hq itself instead, which is what
+        ``materialize_mask`` and the reference's ``flex_attention_slow`` do
+        (attention.py:799-809); the two agree unless Hq > Hkv.
 
         Raises ValueError where the reference's result is not a mask: a tile
         listed twice in a row (the reference would sum it twice) or a listed
@@ -328,7 +331,12 @@ class BlockMask:
                 raise ValueError("block mask lists a tile more than once in a row")
             cls_[b, h, i, kv] = kind
         mask_mod = self.mask_mod
-        h_elem = np.arange(map_h) // G if map_h > 1 else np.zeros(1, np.int64)
+        if element_head not in ("kv", "query"):
+            raise ValueError(f"element_head must be 'kv' or 'query', got {element_head!r}")
+        if map_h == 1:
+            h_elem = np.zeros(1, np.int64)
+        else:
+            h_elem = np.arange(map_h) // (G if element_head == "kv" else 1)
         nkt = -(-self.KV_LEN // _bm.TILE)
 
         def strip(q0):

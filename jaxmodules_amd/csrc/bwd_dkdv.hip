@@ -42,7 +42,7 @@ void bwd_dkdv_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) float Dl[2][BM];
 
   const int item = a.kv_order[blockIdx.x];
-  if (item < 0) return;
+  if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
   const int kt = item % a.nkt;
   const int bh = item / a.nkt;
   const int hk = bh % a.Hkv, b = bh / a.Hkv;

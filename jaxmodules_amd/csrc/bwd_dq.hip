@@ -34,7 +34,7 @@ void bwd_dq_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];
 
   const int item = a.q_order[blockIdx.x];
-  if (item < 0) return;
+  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;

@@ -169,7 +169,7 @@ void bwd_dq_simt(KArgs a) {
   __shared__ __attribute__((aligned(16))) float Vs[SB * D];
 
   const int item = a.q_order[blockIdx.x];
-  if (item < 0) return;
+  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -245,7 +245,7 @@ void bwd_dkdv_simt(KArgs a) {
   __shared__ float Ls[SB], Dl[SB];
 
   const int item = a.kv_order[blockIdx.x];
-  if (item < 0) return;
+  if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
   const int kt = item % a.nkt;
   const int bh = item / a.nkt;
   const int hk = bh % a.Hkv, b = bh / a.Hkv;
