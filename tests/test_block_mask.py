@@ -278,3 +278,25 @@ def test_tile_map_rejects_unrepresentable_lists():
     with pytest.raises(ValueError):
         outside.tile_map(1, 1, 1)
     assert bm.tile_map(1, 1, 1).pairs == 36
+
+
+def test_matches_loop_oracle():
+    """The vectorised module against the loop-level restatement in
+    oracle/block_mask_oracle.py (itself pinned in test_oracle.py)."""
+    from oracle import block_mask_oracle as bo
+
+    rng = np.random.default_rng(11)
+    for bs, (B, H, Q, KV) in (((4, 4), (2, 3, 16, 24)), ((8, 2), (1, 2, 24, 16)), ((3, 5), (2, 1, 12, 20))):
+        tbl = rng.random((B, H, Q, KV)) < 0.6
+        fn = lambda b, h, q, k: tbl[b, h, q, k]
+        ours = create_block_mask(fn, B, H, Q, KV, bs)
+        ref = bo.create_block_mask(fn, B, H, Q, KV, bs)
+        for f in ("kv_num_blocks", "kv_indices", "q_num_blocks", "q_indices", "full_kv_num_blocks",
+                  "full_kv_indices", "full_q_num_blocks", "full_q_indices"):
+            assert np.array_equal(getattr(ours, f), ref[f]), f
+        assert (ours.Q_LEN, ours.KV_LEN) == (ref["Q_LEN"], ref["KV_LEN"])
+        assert np.array_equal(ours.materialize_mask(), bo.materialize(ref))
+    kv_num, kv_idx = np.array([[[1, 2, 1]]]), np.array([[[[0, 3], [1, 2], [3, 3]]]])
+    fkv_num, fkv_idx = np.array([[[1, 0, 1]]]), np.array([[[[2, 0], [0, 0], [1, 0]]]])
+    bm = BlockMask.from_kv_blocks(kv_num, kv_idx, fkv_num, fkv_idx, 2, lambda b, h, q, k: q >= k)
+    assert bm.KV_LEN == bo.infer_kv_len(kv_num, kv_idx, fkv_num, fkv_idx, 2)
