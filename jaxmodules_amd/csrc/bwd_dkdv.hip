@@ -12,34 +12,41 @@ namespace mattn {
 // ---------------------------------------------------------------------------
 // dK / dV (MFMA, no atomics)
 // ---------------------------------------------------------------------------
-// Each wave owns 32 keys; per 64-query sub-block:
-//   S    = Q K^T          (A: Q rows from LDS, B: K^T in registers)
-//   dP   = dO V^T         (A: dO rows from LDS, B: V^T in registers)
-//   P    = exp2(scale_log2 S - lse),  dS = P * (dP - delta)
-//   dV^T += dO^T P        (A: transposed reads of the float16 dO * s tile;
-//                          float16 MFMA)
+// 8 waves (2 per SIMD).  Wave w owns keys 32 (w % 4) .. +31 of the tile and
+// query half w / 4 of every 64-query sub-block:
+//   S    = Q K^T          (A: Q rows, B: K rows; both from LDS)
+//   dP   = dO_h V_h^T     (float16: dO * s and V * vs_k; B: V_h rows from LDS)
+//   P    = exp2(scale_log2 S - lse),  dS = P * (dP / (s vs_k) - delta)
+//   dV^T += dO_h^T P      (A: transposed reads of the dO_h tile, float16)
 //   dK^T += Q^T dS        (A: transposed reads of the Q tile)
-// Q, dO (and, for bfloat16 inputs, the separate float16 dO * s tile), lse and
-// delta are double-buffered in LDS and filled by direct global->LDS loads.
+// The K and V_h tiles of the workgroup's 128 keys stay in LDS for the whole
+// column; Q, dO_h, lse, delta and the partial-tile mask words are
+// double-buffered and filled by direct global->LDS loads.  The two query
+// halves' dK/dV partials of a key are summed through LDS at the end.
+// V_h is V itself for float16 inputs (vs_k = 1) and the scaled float16 copy
+// the preprocess writes for bfloat16 inputs.
 template <int D, class Tag>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
   constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
-  constexpr int BM = 64;           // queries per sub-block
+  constexpr int BM = 64;              // queries per sub-block
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
-  constexpr int NI = D / 32;
-  constexpr int BLK = 512;
-  constexpr int NH = IS_BF16 ? 2 : 1;  // float16 dO * s tile: separate (bf16) or the dO tile
+  constexpr int BLK = 512;            // elements one load instruction fills
+  constexpr int NS = BM * D / BLK / 8;  // load slots per wave for a 64-row tile
+  constexpr int NW = 8;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * D];
-  __shared__ __attribute__((aligned(16))) uint16_t Ds[2][BM * D];
-  __shared__ __attribute__((aligned(16))) uint16_t Hs[NH == 2 ? 2 : 1][NH == 2 ? BM * D : 8];
-  __shared__ __attribute__((aligned(16))) float Ls[2][BM];
-  __shared__ __attribute__((aligned(16))) float Dl[2][BM];
+  // one array per buffer: the compiler then knows the loads landing in one
+  // buffer cannot alias the operand reads of the other (no vmcnt waits mid-step)
+  __shared__ __attribute__((aligned(16))) float L0[BM], L1[BM];        // lse
+  __shared__ __attribute__((aligned(16))) float G0[BM], G1[BM];        // delta
+  __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
+  __shared__ __attribute__((aligned(16))) uint16_t Q0[BM * D], Q1[BM * D];
+  __shared__ __attribute__((aligned(16))) uint16_t H0[BM * D], H1[BM * D];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE * D], Vs[TILE * D];
 
   const int item = a.kv_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
@@ -49,23 +56,14 @@ void bwd_dkdv_mfma(KArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int kloc = wave * 32 + l32;
+  const int kg = wave & 3, qh = wave >> 2;
+  const int kloc = 32 * kg + l32;
   const int key = kt * TILE + kloc;
   const int kcl = min(key, a.Lk - 1);
   const float c2 = a.scale_log2;
-
-  u32x4 kf[NKD], vf[NKD];
-  {
-    const uint16_t* kp = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)kcl * a.ks[1] +
-                         (int64_t)hk * a.ks[2] + 8 * hi;
-    const uint16_t* vp = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)kcl * a.vs[1] +
-                         (int64_t)hk * a.vs[2] + 8 * hi;
-#pragma unroll
-    for (int kd = 0; kd < NKD; ++kd) {
-      kf[kd] = *(const u32x4*)(kp + 16 * kd);
-      vf[kd] = *(const u32x4*)(vp + 16 * kd);
-    }
-  }
+  const float inv_s = a.dscale[1];
+  // dP = (dO_h V_h^T) / (s vs_k): one factor per lane, since a lane owns one key
+  const float dsc = IS_BF16 ? inv_s * a.vinv[((int64_t)b * a.Hkv + hk) * a.Lk + kcl] : inv_s;
 
   // Flattened walk over (query head g of the group, column entry, half).
   int tot = 0;
@@ -81,70 +79,96 @@ void bwd_dkdv_mfma(KArgs a) {
     lend = a.col_ptr[mc + 1];
   }
 
-  const int64_t drow = (int64_t)a.Hq * D;   // row stride of the dense dO copies
-  uint32_t qld[NI], dld[NI];
+  // K and V_h tiles of the column: loaded once, by all 8 waves
+  {
+    const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
+    const uint16_t* vb;
+    int64_t vrs;
+    if constexpr (IS_BF16) {
+      vb = (const uint16_t*)a.vh + (int64_t)b * a.Lk * a.Hkv * D + (int64_t)hk * D;
+      vrs = (int64_t)a.Hkv * D;
+    } else {
+      vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
+      vrs = a.vs[1];
+    }
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    qld[i] = TL::src_off(NI * wave + i, lane, a.qs[1]);
-    dld[i] = TL::src_off(NI * wave + i, lane, drow);
+    for (int i = 0; i < 2 * NS; ++i) {
+      const int n = 2 * NS * wave + i;
+      const int kk = min(kt * TILE + TL::row_of(n, lane), a.Lk - 1);
+      const int c = TL::chunk_of(n, lane);
+      lds_load16(kb + (int64_t)kk * a.ks[1] + 8 * c, Ks + n * BLK);
+      lds_load16(vb + (int64_t)kk * vrs + 8 * c, Vs + n * BLK);
+    }
   }
-  int rro[NKD];
-#pragma unroll
-  for (int kd = 0; kd < NKD; ++kd) rro[kd] = sw_off<D>(l32, 2 * kd + hi);
-  int tro[NMD][2];
-#pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
-    tro[mt][0] = tr_src<D>(lane, mt, 0);
-    tro[mt][1] = tr_src<D>(lane, mt, 1);
-  }
-  const float inv_s = a.dscale[1];
-  const float dps = IS_BF16 ? 1.f : inv_s;
-  int cmask_e = 0, chalf = 0;  // entry and half of the most recently issued sub-block
 
-  auto issue = [&](int buf) {  // global -> LDS loads of the sub-block at the cursor
-    while (le >= lend) {
+  const int64_t drow = (int64_t)a.Hq * D;   // row stride of the dense dO_h copy
+  uint32_t qld[NS], dld[NS];  // loop-invariant source byte offsets of this lane's load slots
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    qld[i] = 2 * TL::src_off(NS * wave + i, lane, a.qs[1]);
+    dld[i] = 2 * TL::src_off(NS * wave + i, lane, drow);
+  }
+  // LDS operand addresses, formed per use from lane seeds (one v_xad_u32 each)
+  // rather than held in 24 registers across the loop (element offsets):
+  //   row read, chunk 2 kd + hi of row r:   r D + ((16 kd) ^ rx),  rx = 8 hi ^ 8 swz(r)
+  //   transposed read (mt, sec):            tb[sec] + ((32 mt) ^ tz)
+  // Rows 32 qh + l32 (queries) and 32 kg + l32 (keys) share swz(l32); only the
+  // swizzle's bits from 2 up meet mt in a transposed read, and they do not depend on sec.
+  const int rx = (8 * hi) ^ (swz<D>(l32) << 3);
+  const int qrow = (32 * qh + l32) * D, krow_l = kloc * D;
+  const int tz = 32 * (swz<D>(4 * hi + ((lane & 15) >> 2)) >> 2);
+  const int tb0 = tr_src<D>(lane, 0, 0) + 32 * qh * D - tz;
+  const int tb1 = tr_src<D>(lane, 0, 1) + 32 * qh * D - tz;
+  const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
+  EntryCache ec;
+  int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
+
+  auto issue = [&](auto bufc) {  // global -> LDS loads of the sub-block at the cursor
+    constexpr int BUF = decltype(bufc)::value;
+    while (le >= lend) {  // next query head of the group: another column list
       ++lg;
       const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
       le = a.col_ptr[mc];
       lend = a.col_ptr[mc + 1];
+      ec.reset();
     }
     const int h = hk * a.G + lg;
-    const int q0 = a.col_ent[2 * le] * TILE + lhalf * BM;
+    int qt, mid;
+    ec.get(a.col_ent, le, lend, lane, qt, mid);
+    (BUF ? mid1 : mid0) = mid;
+    const int q0 = qt * TILE + lhalf * BM;
+    if (mid >= 0 && wave < 4) {  // 32 keys' mask words per wave (256 bytes), one dword per lane
+      const uint32_t* src = (const uint32_t*)(a.col_bits + ((int64_t)mid * 2 + lhalf) * TILE + wave * 32);
+      __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
+                                       4, 0, 0);
+    }
     const uint16_t* qb = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
-    const int64_t dro = ((int64_t)b * a.Lq * a.Hq + h) * D;
-    const uint16_t* db = (const uint16_t*)(IS_BF16 ? a.dO16 : a.dOh) + dro;
-    const uint16_t* hb = (const uint16_t*)a.dOh + dro;
-    uint16_t* ql = &Qs[buf][NI * wave * BLK];
-    uint16_t* dl_ = &Ds[buf][NI * wave * BLK];
-    uint16_t* hl = &Hs[NH == 2 ? buf : 0][NH == 2 ? NI * wave * BLK : 0];
+    const uint16_t* hb = (const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D;
+    uint16_t* ql = (BUF ? Q1 : Q0) + wofs;
+    uint16_t* hl = (BUF ? H1 : H0) + wofs;
     if (q0 + BM <= a.Lq) {
-      const uint16_t* qp = qb + (int64_t)q0 * a.qs[1];
-      const uint16_t* dp = db + (int64_t)q0 * drow;
-      const uint16_t* hp = hb + (int64_t)q0 * drow;
+      const char* qp = (const char*)(qb + (int64_t)q0 * a.qs[1]);
+      const char* hp = (const char*)(hb + (int64_t)q0 * drow);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
+      for (int i = 0; i < NS; ++i) {
         lds_load16(qp + qld[i], ql + i * BLK);
-        lds_load16(dp + dld[i], dl_ + i * BLK);
-        if constexpr (NH == 2) lds_load16(hp + dld[i], hl + i * BLK);
+        lds_load16(hp + dld[i], hl + i * BLK);
       }
     } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int qq = min(q0 + TL::row_of(NI * wave + i, lane), a.Lq - 1);
-        const int c = TL::chunk_of(NI * wave + i, lane);
+      for (int i = 0; i < NS; ++i) {
+        const int qq = min(q0 + TL::row_of(NS * wave + i, lane), a.Lq - 1);
+        const int c = TL::chunk_of(NS * wave + i, lane);
         lds_load16(qb + (int64_t)qq * a.qs[1] + 8 * c, ql + i * BLK);
-        lds_load16(db + (int64_t)qq * drow + 8 * c, dl_ + i * BLK);
-        if constexpr (NH == 2) lds_load16(hb + (int64_t)qq * drow + 8 * c, hl + i * BLK);
+        lds_load16(hb + (int64_t)qq * drow + 8 * c, hl + i * BLK);
       }
     }
-    if (wave < 2) {  // lse (wave 0) and delta (wave 1) of the 64 rows
+    if (wave >= 6) {  // lse (wave 6) and delta (wave 7) of the 64 rows
       const int qq = min(q0 + lane, a.Lq - 1);
-      const float* src = (wave == 0 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq + qq;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(wave == 0 ? Ls[buf] : Dl[buf]),
-                                       4, 0, 0);
+      const float* src = (wave == 6 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq + qq;
+      float* dst = wave == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0);
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
     }
-    cmask_e = le;
-    chalf = lhalf;
     if (lhalf == 0) {
       lhalf = 1;
     } else {
@@ -157,95 +181,112 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
 
-  auto step = [&](int buf, bool masked, uint64_t mw) {
-    const uint16_t* ht = NH == 2 ? Hs[buf] : Ds[buf];  // float16 dO * s tile
-    f32x16 st[2], dp[2];
+  auto step = [&](auto bufc, bool masked) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* Qb = BUF ? Q1 : Q0;
+    const uint16_t* Hb = BUF ? H1 : H0;
+    const float* Lb = (BUF ? L1 : L0) + 32 * qh;
+    const float* Gb = (BUF ? G1 : G0) + 32 * qh;
+    // seeds re-defined here, so the addresses derived from them stay per use
+    const int rxo = opaque(rx), qro = opaque(qrow), kro = opaque(krow_l);
+    f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      u32x4 qa[NKD], da[NKD];
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) {
-        qa[kd] = *(const u32x4*)&Qs[buf][rro[kd] + 32 * t * D];
-        da[kd] = *(const u32x4*)&Ds[buf][rro[kd] + 32 * t * D];
-      }
-      st[t] = f32x16{};
-      dp[t] = f32x16{};
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) {
-        st[t] = E::mfma(qa[kd], kf[kd], st[t]);
-        dp[t] = E::mfma(da[kd], vf[kd], dp[t]);
-      }
+    for (int kd = 0; kd < NKD; ++kd) {
+      const int xo = (16 * kd) ^ rxo;
+      const u32x4 qa = *(const u32x4*)&Qb[qro + xo];
+      const u32x4 kb = *(const u32x4*)&Ks[kro + xo];
+      const u32x4 ha = *(const u32x4*)&Hb[qro + xo];
+      const u32x4 vb = *(const u32x4*)&Vs[kro + xo];
+      st = E::mfma(qa, kb, st);
+      dp = H::mfma(ha, vb, dp);
     }
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 lv = *(const f32x4*)&Ls[buf][32 * t + 8 * j + 4 * hi];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[t][4 * j + i] = fast_exp2(fmaf(st[t][4 * j + i], c2, -lv[i]));
-      }
+      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], c2, -lv[i]));
     }
     if (masked) {
+      const uint32_t w32 = (uint32_t)((BUF ? M1 : M0)[kloc] >> (32 * qh)) >> (4 * hi);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
+      for (int r = 0; r < 16; ++r)
+        if (!mask_bit(w32, r)) st[r] = 0.f;
+    }
+    u32x4 pk[2], sk[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (!mask_bit(w32, r)) st[t][r] = 0.f;
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 dv4 = *(const f32x4*)&Gb[8 * j + 4 * hi];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * j + i;
+        dp[r] = st[r] * fmaf(dp[r], dsc, -dv4[i]);
       }
     }
-    u32x4 pk[4], sk[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 dv4 = *(const f32x4*)&Dl[buf][32 * t + 8 * j + 4 * hi];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * j + i;
-          dp[t][r] = st[t][r] * fmaf(dp[t][r], dps, -dv4[i]);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        pk[2 * t + (r >> 3)][(r & 7) >> 1] = H::pack2(st[t][r], st[t][r + 1]);
-        sk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(dp[t][r], dp[t][r + 1]);
-      }
+    for (int r = 0; r < 16; r += 2) {
+      pk[r >> 3][(r & 7) >> 1] = H::pack2(st[r], st[r + 1]);
+      sk[r >> 3][(r & 7) >> 1] = E::pack2(dp[r], dp[r + 1]);
     }
+    const int tzo = opaque(tz), t0 = opaque(tb0), t1 = opaque(tb1);
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
-      u32x4 ta[4], tb[4];
+      const int xm = (32 * mt) ^ tzo;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x2 h0 = lds_read_tr(&ht[tro[mt][0] + 16 * ks * D]);
-        const u32x2 h1 = lds_read_tr(&ht[tro[mt][1] + 16 * ks * D]);
-        const u32x2 q0 = lds_read_tr(&Qs[buf][tro[mt][0] + 16 * ks * D]);
-        const u32x2 q1 = lds_read_tr(&Qs[buf][tro[mt][1] + 16 * ks * D]);
-        ta[ks] = u32x4{h0[0], h0[1], h1[0], h1[1]};
-        tb[ks] = u32x4{q0[0], q0[1], q1[0], q1[1]};
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        dv[mt] = H::mfma(ta[ks], pk[ks], dv[mt]);
-        dk[mt] = E::mfma(tb[ks], sk[ks], dk[mt]);
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x2 h0 = lds_read_tr(&Hb[t0 + xm + 16 * ks * D]);
+        const u32x2 h1 = lds_read_tr(&Hb[t1 + xm + 16 * ks * D]);
+        const u32x2 q0 = lds_read_tr(&Qb[t0 + xm + 16 * ks * D]);
+        const u32x2 q1 = lds_read_tr(&Qb[t1 + xm + 16 * ks * D]);
+        dv[mt] = H::mfma(u32x4{h0[0], h0[1], h1[0], h1[1]}, pk[ks], dv[mt]);
+        dk[mt] = E::mfma(u32x4{q0[0], q0[1], q1[0], q1[1]}, sk[ks], dk[mt]);
       }
     }
   };
 
-  if (tot > 0) issue(0);
-  for (int s = 0; s < tot; ++s) {
-    const int buf = s & 1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    const int mask = a.col_ent[2 * cmask_e + 1];
-    const int half = chalf;
-    uint64_t mw = 0;
-    if (mask >= 0) mw = a.col_bits[((int64_t)mask * 2 + half) * TILE + kloc];
-    if (s + 1 < tot) issue(buf ^ 1);
-    step(buf, mask >= 0, mw);
+  // sub-block s computes from buffer s % 2 while s + 1 loads into the other;
+  // the loop is unrolled by two so that every buffer index is static
+  auto iter = [&](int s, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
+    __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
+    const bool masked = (BUF ? mid1 : mid0) >= 0;
+    if (s + 1 < tot) issue(std::integral_constant<int, 1 - BUF>{});
+    step(bufc, masked);
+  };
+  if (tot > 0) issue(std::integral_constant<int, 0>{});
+  for (int s = 0; s < tot; s += 2) {
+    iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});
   }
 
-  if (key >= a.Lk) return;
+  // dK / dV: the second query half's partials join the first's through LDS
+  // (wave kg + 4 -> wave kg, one 16 KiB slab per key group, lane-major floats)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  float* red = (float*)(kg == 0 ? Q0 : kg == 1 ? Q1 : kg == 2 ? H0 : H1);
+  static_assert(NMD * 16 * 64 * 4 <= BM * D * 2, "reduction slab");
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    if (qh == 1) {
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(mt * 16 + r) * 64 + lane] = pass == 0 ? dk[mt][r] : dv[mt][r];
+    }
+    __syncthreads();
+    if (qh == 0) {
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float x = red[(mt * 16 + r) * 64 + lane];
+          if (pass == 0) dk[mt][r] += x; else dv[mt][r] += x;
+        }
+    }
+    __syncthreads();
+  }
+
+  if (qh != 0 || key >= a.Lk) return;
   char* kp = (char*)a.dk;
   char* vp = (char*)a.dv;
   const int64_t krow = (int64_t)b * a.dks[0] + (int64_t)key * a.dks[1] + (int64_t)hk * a.dks[2];
@@ -271,11 +312,11 @@ void bwd_dkdv_mfma(KArgs a) {
 
 hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
   if (dtype == MATTN_BF16) {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, bf16_tag>), dim3(grid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, bf16_tag>), dim3(grid), dim3(512), 0, st, a);
   } else {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, f16_tag>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, f16_tag>), dim3(grid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, f16_tag>), dim3(grid), dim3(512), 0, st, a);
   }
   return hipGetLastError();
 }

@@ -59,6 +59,10 @@ struct KArgs {
   void* dv;
   void* dO16w;       // writable aliases for the preprocess kernel
   void* dOhw;
+  const void* vh;    // bfloat16 inputs: V * vs_k in float16, dense [B, Lk, Hkv, D] (workspace)
+  const float* vinv; // bfloat16 inputs: 1 / vs_k per key row [B, Hkv, Lk] (workspace)
+  void* vhw;         // writable aliases of the two
+  float* vinvw;
   int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3];
   int B, Lq, Lk, Hq, Hkv, G;
   float scale;       // softmax scale
@@ -266,8 +270,12 @@ __device__ __forceinline__ float wave_sum32(float x) {
 // back with v_readlane at a wave-uniform index (no memory access inside the
 // loop, so no wait on the global->LDS loads in flight).  ent holds
 // (tile, mask id) pairs; [e0, e1) is the range this workgroup walks.
+// Tile entries of one CSR list [e, e1): lane l holds entry base + l (clamped to
+// e1 - 1), refilled when e leaves the window.  The clamp ties the window to one
+// list: call reset() before reading another list.
 struct EntryCache {
   int tile = 0, mask = 0, base = -(1 << 30);
+  __device__ __forceinline__ void reset() { base = -(1 << 30); }
   __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m) {
     if (e - base >= 64 || e < base) {  // wave-uniform
       base = e;
@@ -279,6 +287,13 @@ struct EntryCache {
     m = __builtin_amdgcn_readlane(mask, e - base);
   }
 };
+
+// x, re-defined by an empty asm: values computed from the result inside a loop
+// are not hoisted out of it (trades a few VALU ops for registers held across the loop)
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 __device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int t) {
   return ((a.map_b == 1 ? 0 : b) * a.map_h + (a.map_h == 1 ? 0 : h)) * n + t;
