@@ -22,7 +22,7 @@ SOURCES = ["fwd.hip", "bwd_pre.hip", "bwd_dq.hip", "bwd_dkdv.hip", "capi.hip"]
 # machine-scheduler strategy per source: the ILP-oriented ones hoist LDS operand
 # reads ahead of the MFMA chains; each file uses the one measured fastest
 # without register spills for its kernels
-SCHED = {"fwd.hip": "iterative-ilp", "bwd_dq.hip": "iterative-ilp", "bwd_dkdv.hip": "iterative-ilp"}
+SCHED = {"fwd.hip": "iterative-ilp", "bwd_dkdv.hip": "iterative-ilp"}
 ARCH = "gfx950"
 
 

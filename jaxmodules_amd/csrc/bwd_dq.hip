@@ -18,7 +18,7 @@ namespace mattn {
 // K and V are double-buffered (one array per buffer, loop unrolled by two),
 // swizzled row-major tiles filled by direct global->LDS loads.
 template <int D, class Tag>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {
   using E = Elt<Tag>;
   using TL = TileLoad<D>;
@@ -75,15 +75,15 @@ void bwd_dq_mfma(KArgs a) {
     kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
     vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
   }
-  int rro[NKD];               // row-read offsets (K and V tiles share the layout)
-#pragma unroll
-  for (int kd = 0; kd < NKD; ++kd) rro[kd] = sw_off<D>(l32, 2 * kd + hi);
-  int kto[NMD][2];            // K^T transposed-read offsets
-#pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
-    kto[mt][0] = tr_src<D>(lane, mt, 0);
-    kto[mt][1] = tr_src<D>(lane, mt, 1);
-  }
+  // LDS operand addresses, formed per use from lane seeds (one v_xad_u32 each)
+  // rather than held in 16 registers across the loop (element offsets):
+  //   row read, chunk 2 kd + hi of row l32 (+32 t):  l32 D + ((16 kd) ^ rx)
+  //   K^T transposed read (mt, sec):                 tb[sec] + ((32 mt) ^ tz)
+  const int rx = (8 * hi) ^ (swz<D>(l32) << 3);
+  const int rrow = l32 * D;
+  const int tz = 32 * (swz<D>(4 * hi + ((lane & 15) >> 2)) >> 2);
+  const int tb0 = tr_src<D>(lane, 0, 0) - tz;
+  const int tb1 = tr_src<D>(lane, 0, 1) - tz;
   const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);
   EntryCache ec;
 
@@ -129,13 +129,17 @@ void bwd_dq_mfma(KArgs a) {
     const uint16_t* Kb = BUF ? K1 : K0;
     const uint16_t* Vb = BUF ? V1 : V0;
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
+    // seeds re-defined here, so the addresses derived from them stay per use
+    const int rxo = opaque(rx), rro = opaque(rrow);
+    const int tzo = opaque(tz), t0 = opaque(tb0), t1 = opaque(tb1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int kd = 0; kd < NKD; ++kd) {
-        const u32x4 ka = *(const u32x4*)&Kb[rro[kd] + 32 * t * D];
-        const u32x4 va = *(const u32x4*)&Vb[rro[kd] + 32 * t * D];
+        const int xo = (16 * kd) ^ rxo;
+        const u32x4 ka = *(const u32x4*)&Kb[rro + xo + 32 * t * D];
+        const u32x4 va = *(const u32x4*)&Vb[rro + xo + 32 * t * D];
         st = E::mfma(ka, qf[kd], st);
         dp = E::mfma(va, df[kd], dp);
       }
@@ -156,11 +160,12 @@ void bwd_dq_mfma(KArgs a) {
       }
 #pragma unroll
       for (int mt = 0; mt < NMD; ++mt) {
+        const int xm = (32 * mt) ^ tzo;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const int ks = 2 * t + kk;
-          const u32x2 lo = lds_read_tr(&Kb[kto[mt][0] + 16 * ks * D]);
-          const u32x2 up = lds_read_tr(&Kb[kto[mt][1] + 16 * ks * D]);
+          const u32x2 lo = lds_read_tr(&Kb[t0 + xm + 16 * ks * D]);
+          const u32x2 up = lds_read_tr(&Kb[t1 + xm + 16 * ks * D]);
           acc[mt] = E::mfma(u32x4{lo[0], lo[1], up[0], up[1]}, pk[kk], acc[mt]);
         }
       }
