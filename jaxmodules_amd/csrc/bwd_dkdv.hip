@@ -122,6 +122,11 @@ void bwd_dkdv_mfma(KArgs a) {
   const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
   EntryCache ec;
   int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
+  // buffer resources of the current query head's Q and dO_h slices
+  const uint32_t qbytes = (uint32_t)(((int64_t)(a.Lq - 1) * a.qs[1] + D) * 2);
+  const uint32_t hbytes = (uint32_t)(((int64_t)(a.Lq - 1) * drow + D) * 2);
+  __amdgpu_buffer_rsrc_t rq, rh;
+  int rh_head = -1;
 
   auto issue = [&](auto bufc) {  // global -> LDS loads of the sub-block at the cursor
     constexpr int BUF = decltype(bufc)::value;
@@ -142,25 +147,27 @@ void bwd_dkdv_mfma(KArgs a) {
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
                                        4, 0, 0);
     }
-    const uint16_t* qb = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
-    const uint16_t* hb = (const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D;
+    if (h != rh_head) {
+      rh_head = h;
+      rq = make_rsrc((const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2], qbytes);
+      rh = make_rsrc((const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D, hbytes);
+    }
     uint16_t* ql = (BUF ? Q1 : Q0) + wofs;
     uint16_t* hl = (BUF ? H1 : H0) + wofs;
     if (q0 + BM <= a.Lq) {
-      const char* qp = (const char*)(qb + (int64_t)q0 * a.qs[1]);
-      const char* hp = (const char*)(hb + (int64_t)q0 * drow);
+      const uint32_t qso = (uint32_t)((int64_t)q0 * a.qs[1] * 2), hso = (uint32_t)((int64_t)q0 * drow * 2);
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
-        lds_load16(qp + qld[i], ql + i * BLK);
-        lds_load16(hp + dld[i], hl + i * BLK);
+        lds_load16_buf(rq, qld[i], qso, ql + i * BLK);
+        lds_load16_buf(rh, dld[i], hso, hl + i * BLK);
       }
     } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         const int qq = min(q0 + TL::row_of(NS * wave + i, lane), a.Lq - 1);
         const int c = TL::chunk_of(NS * wave + i, lane);
-        lds_load16(qb + (int64_t)qq * a.qs[1] + 8 * c, ql + i * BLK);
-        lds_load16(hb + (int64_t)qq * drow + 8 * c, hl + i * BLK);
+        lds_load16_buf(rq, (uint32_t)(qq * a.qs[1] + 8 * c) * 2, 0, ql + i * BLK);
+        lds_load16_buf(rh, (uint32_t)(qq * drow + 8 * c) * 2, 0, hl + i * BLK);
       }
     }
     if (wave >= 6) {  // lse (wave 6) and delta (wave 7) of the 64 rows

@@ -180,6 +180,22 @@ __device__ __forceinline__ void lds_load16(const void* g, uint16_t* lds_block) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
 }
 
+// Buffer resource of `bytes` bytes at `base` (raw, no stride; loads past the
+// end return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Direct global->LDS load of 16 bytes per lane through a buffer resource: lane L
+// reads rsrc + soff + voff and lands at lds_block + 16 L (as lds_load16).  The
+// address is formed by the load unit: a loop-invariant per-lane voff and a
+// uniform soff need no per-load VALU arithmetic.
+__device__ __forceinline__ void lds_load16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                               uint16_t* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_block, 16, (int)voff,
+                                          (int)soff, 0, 0);
+}
+
 // Transposed operand read (ds_read_b64_tr_b16): inside each 16-lane group, if
 // lane j addresses X[r + j/4][c + 4 (j % 4)], lane i receives
 // X[r + k][c + i] for k = 0..3.
