@@ -70,6 +70,36 @@ def _docs(L, seed, mean=2048, minlen=64):
     return np.repeat(np.arange(len(lens)), lens)[:L]
 
 
+def _cfg4_tiles():
+    """cfg4's per-head tile selection: Bernoulli(0.25) over the full 64x64 grid, diagonal on."""
+    nt, H = 8192 // 128, 32
+    rng = np.random.default_rng(4)
+    tbl = rng.random((H, nt, nt)) < 0.25
+    tbl[:, np.arange(nt), np.arange(nt)] = True
+    return tbl
+
+
+def _cfg5_docs():
+    return _docs(32768, 5)
+
+
+def closed_form_mask(name):
+    """The mask of configs 3-5 in closed form (jaxmodules_amd.masks), which the
+    GPU classifies; the same mask as workload(name)'s mask_fn."""
+    from jaxmodules_amd import masks
+
+    if name == "cfg3":
+        return masks.intersect(masks.causal(), masks.window(512, 0))
+    if name == "cfg4":
+        t = _cfg4_tiles().astype(np.uint8)                 # 1: every element
+        nt = t.shape[1]
+        t[:, np.arange(nt), np.arange(nt)] = 2             # diagonal: causal inside
+        return masks.intersect(masks.tile_table(t), masks.causal())
+    if name == "cfg5":
+        return masks.intersect(masks.documents(_cfg5_docs()), masks.causal())
+    raise SystemExit(f"no closed-form mask for {name}")
+
+
 def workload(name):
     """(B, L, H, d, kwargs, description) of a BASELINE configuration."""
     if name == "cfg2":
@@ -83,15 +113,12 @@ def workload(name):
                                        window_size=(512, 0), block_size=128), \
             "cfg3: sliding window (q>=k)&(q-k<=512), window (512,0), bf16 B=2 L=16384 H=16 d=128"
     if name == "cfg4":
-        nt, H = 8192 // 128, 32
-        rng = np.random.default_rng(4)
-        tbl = rng.random((H, nt, nt)) < 0.25
-        tbl[:, np.arange(nt), np.arange(nt)] = True
+        H, tbl = 32, _cfg4_tiles()
         mask = lambda b, h, q, k: tbl[h, q // 128, k // 128] & ((q // 128 != k // 128) | (q >= k))
         return 1, 8192, H, 64, dict(mask_fn=mask, block_size=128), \
             "cfg4: per-head random 128x128 tiles at 25% (full grid), diagonal causal, bf16 B=1 L=8192 H=32 d=64"
     if name == "cfg5":
-        doc = _docs(32768, 5)
+        doc = _cfg5_docs()
         mask = lambda b, h, q, k: (doc[q] == doc[k]) & (q >= k)
         return 1, 32768, 8, 128, dict(mask_fn=mask, block_size=128), \
             f"cfg5: packed documents ({doc.max() + 1} docs, geometric mean 2048, min 64) & causal, bf16 B=1 L=32768 H=8 d=128"
@@ -226,6 +253,42 @@ def _pairs_of(name):
     return _PAIRS[name]
 
 
+def tilemap_build_times(repeats=5):
+    """Seconds to build the tile map of configs 3-5: the host tracer on the
+    configs' mask_fn lambdas, and the GPU classifier on the same masks in
+    closed form (median of ``repeats`` builds, each ending with the map on the
+    host, after one untimed build).  The two maps are compared array for array."""
+    import torch
+
+    from jaxmodules_amd import blockmap as bmap
+
+    out = {"metric": "tile-map build seconds, host tracer vs GPU classifier", "unit": "s",
+           "higher_is_better": False, "configs": {}}
+    for name in ("cfg3", "cfg4", "cfg5"):
+        B, L, H, d, kw, desc = workload(name)
+        shape = (B, L, H, d)
+        t0 = time.perf_counter()
+        host = bmap.trace(bmap.make_plan(shape, shape, shape, **kw))
+        th = time.perf_counter() - t0
+        kw2 = dict(kw, mask_fn=closed_form_mask(name))
+        plan = bmap.make_plan(shape, shape, shape, **kw2)
+        bmap.device_trace(plan, "cuda:0")
+        ts = []
+        for _ in range(repeats):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dev = bmap.device_trace(plan, "cuda:0")
+            ts.append(time.perf_counter() - t0)
+        same = all(np.array_equal(getattr(host, f), getattr(dev, f))
+                   for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "row_bits", "col_bits",
+                             "q_order", "kv_order")) and host.pairs == dev.pairs
+        out["configs"][name] = {"workload": desc, "host_s": round(th, 4),
+                                "device_s": round(float(np.median(ts)), 5),
+                                "speedup": round(th / float(np.median(ts)), 1), "identical": same,
+                                "nnz": dev.nnz, "masks": dev.n_masks}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,6 +300,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed region, copy 1 GiB once (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--tilemap", action="store_true",
+                    help="instead: time the tile-map build of configs 3-5, host tracer vs GPU classifier")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -247,6 +312,9 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.tilemap:
+        print(json.dumps(tilemap_build_times()), flush=True)
+        return
     r = Runner(args.config)
     _PAIRS[args.config] = r.pairs
     ms, kern = r.measure(args.steps, args.warmup)

@@ -148,6 +148,60 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     const void* o, const void* do_, const float* lse,
                     void* workspace, void* dq, void* dk, void* dv, void* stream);
 
+/*
+ * Device tile-map classifier, for masks given in closed form.  It replaces the
+ * element-by-element evaluation of create_block_mask (block_mask.py:454-498,
+ * get_partial_block :381-408) and of the host tracer of mask_fn; the host
+ * assembles the mattn_blockmap lists from its per-tile output.
+ *
+ * The effective mask of map row (mb, mh) at query q, key k is the AND of
+ *   - the unpadded range q < Lq, k < Lk                       (attention.py:426-437)
+ *   - when blk_size > 0, the reference's visited key blocks: the block of k in
+ *     [s, s + blk_left + blk_right), s = min(max(q / blk_size - blk_left, 0),
+ *     blk_nk - blk_left - blk_right)                      (attention.py:161-167,199-204)
+ *   - when tab_b > 0, the table entry of the tile: 0 no element, 1 every
+ *     element, 2 the element predicates below
+ *   - the element predicates: k <= q when causal; q - k <= win_left and
+ *     k - q <= win_right where those are >= 0; doc_q[b][q] == doc_k[b][k]
+ *     when doc_b > 0 (b = 0 when doc_b == 1).
+ * Every pointer is device memory.
+ */
+typedef struct mattn_maskspec {
+  int32_t causal;                /* 0 or 1                                       */
+  int32_t win_left, win_right;   /* element window, -1 = unbounded               */
+  int32_t doc_b;                 /* 0: no document ids; 1: shared; map_b: per b  */
+  const int32_t* doc_q;          /* [doc_b][Lq] document id of each query        */
+  const int32_t* doc_k;          /* [doc_b][Lk] document id of each key          */
+  int32_t tab_b, tab_h;          /* 0: no table; else 1 or map_b, 1 or map_h     */
+  const uint8_t* tiles;          /* [tab_b][tab_h][nqt][nkt] table entries       */
+  int32_t blk_size;              /* 0: no visited-block window                   */
+  int32_t blk_left, blk_right;   /* blocks before / from the query's block        */
+  int32_t blk_nk;                /* key blocks of the padded key length          */
+} mattn_maskspec;
+
+/* Host-only check of a mask spec for a map_b x map_h map of Lq x Lk. */
+int mattn_maskspec_validate(const mattn_maskspec* ms, int32_t Lq, int32_t Lk,
+                            int32_t map_b, int32_t map_h);
+
+/* Classifies every tile t = ((mb * map_h + mh) * nqt + qt) * nkt + kt:
+ *   state[t]            int8: 0 absent, 1 full, 2 partial
+ *   count[t]            int32: allowed elements of the tile
+ *   hash[2t], hash[2t+1] 128-bit hash of a partial tile's row bits (else 0). */
+int mattn_tilemap_classify(const mattn_maskspec* ms, int32_t Lq, int32_t Lk,
+                           int32_t map_b, int32_t map_h,
+                           int8_t* state, int32_t* count, uint64_t* hash, void* stream);
+
+/* For n (tile index, mask id) pairs in list (int32 [2n]):
+ *   write != 0: writes row_bits[id] and col_bits[id] (mattn_blockmap layout,
+ *               [n_masks][2][128] each) from the tile's mask;
+ *   write == 0: compares the tile's mask with row_bits[id] and stores 1 into
+ *               *mismatch when they differ (the caller zeroes it first).
+ * Pairs with a tile index or mask id out of range are skipped. */
+int mattn_tilemap_bits(const mattn_maskspec* ms, int32_t Lq, int32_t Lk,
+                       int32_t map_b, int32_t map_h, const int32_t* list, int32_t n,
+                       int32_t n_masks, int32_t write, uint64_t* row_bits,
+                       uint64_t* col_bits, int32_t* mismatch, void* stream);
+
 /* Static text of a status code. */
 const char* mattn_strerror(int status);
 

@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
 
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 TILE_Q = TILE_K = 128
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 STATUS = {
     0: "MATTN_OK",
@@ -33,7 +33,8 @@ STATUS = {
 
 # every symbol include/mattn.h declares
 EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_fwd", "mattn_bwd",
-           "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version")
+           "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version", "mattn_maskspec_validate",
+           "mattn_tilemap_classify", "mattn_tilemap_bits")
 BWD_PRE, BWD_DKDV, BWD_DQ = 0, 1, 2
 
 _I64x3 = ctypes.c_int64 * 3
@@ -60,6 +61,16 @@ class MattnBlockmap(ctypes.Structure):
         ("row_bits", ctypes.c_void_p), ("col_bits", ctypes.c_void_p),
         ("q_order", ctypes.c_void_p), ("kv_order", ctypes.c_void_p),
         ("n_q_order", ctypes.c_int32), ("n_kv_order", ctypes.c_int32),
+    ]
+
+
+class MattnMaskspec(ctypes.Structure):
+    _fields_ = [
+        ("causal", ctypes.c_int32), ("win_left", ctypes.c_int32), ("win_right", ctypes.c_int32),
+        ("doc_b", ctypes.c_int32), ("doc_q", ctypes.c_void_p), ("doc_k", ctypes.c_void_p),
+        ("tab_b", ctypes.c_int32), ("tab_h", ctypes.c_int32), ("tiles", ctypes.c_void_p),
+        ("blk_size", ctypes.c_int32), ("blk_left", ctypes.c_int32), ("blk_right", ctypes.c_int32),
+        ("blk_nk", ctypes.c_int32),
     ]
 
 
@@ -102,6 +113,14 @@ def load():
         lib.mattn_bwd_stage.restype = ctypes.c_int
         lib.mattn_strerror.argtypes = [ctypes.c_int]
         lib.mattn_strerror.restype = ctypes.c_char_p
+        S = ctypes.POINTER(MattnMaskspec)
+        i32 = ctypes.c_int32
+        lib.mattn_maskspec_validate.argtypes = [S, i32, i32, i32, i32]
+        lib.mattn_maskspec_validate.restype = ctypes.c_int
+        lib.mattn_tilemap_classify.argtypes = [S, i32, i32, i32, i32, vp, vp, vp, vp]
+        lib.mattn_tilemap_classify.restype = ctypes.c_int
+        lib.mattn_tilemap_bits.argtypes = [S, i32, i32, i32, i32, vp, i32, i32, i32, vp, vp, vp, vp]
+        lib.mattn_tilemap_bits.restype = ctypes.c_int
         lib.mattn_abi_version.argtypes = []
         lib.mattn_abi_version.restype = ctypes.c_int
         if lib.mattn_abi_version() != ABI_VERSION:

@@ -94,9 +94,14 @@ def clear_cache():
 
 
 def trace_call(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, block_size=None,
-               window_size=None):
+               window_size=None, device=None):
     """(Plan, TileMap) of a call; tile maps are cached per mask function and shapes
-    (like the reference, which bakes mask_fn in at trace time under jax.jit)."""
+    (like the reference, which bakes mask_fn in at trace time under jax.jit).
+
+    With a GPU ``device``, masks in closed form (``jaxmodules_amd.masks``,
+    ``is_causal`` and no mask) are classified on that GPU
+    (``blockmap.device_trace``); other mask functions are traced on the host.
+    Both give the same map."""
     plan = bmap.make_plan(q_shape, k_shape, v_shape, is_causal=is_causal, mask_fn=mask_fn,
                           block_size=block_size, window_size=window_size)
     key = (bool(is_causal), mask_fn, block_size,
@@ -104,7 +109,11 @@ def trace_call(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, bloc
            plan.B, plan.N, plan.L, plan.Hq, plan.Hkv)
     tm = _CACHE.get(key)
     if tm is None:
-        tm = bmap.trace(plan)
+        on_gpu = device is not None and torch.device(device).type == "cuda"
+        if on_gpu and bmap.spec_of(plan.mask4) is not None:
+            tm = bmap.device_trace(plan, device)
+        else:
+            tm = bmap.trace(plan)
         _CACHE[key] = tm
         if len(_CACHE) > _CACHE_SIZE:
             _CACHE.popitem(last=False)
@@ -290,7 +299,8 @@ def masked_attention_via_map(
     Rows with no allowed key are zero (attention.py:91-100).
     """
     plan, tm = trace_call(tuple(Q.shape), tuple(K.shape), tuple(V.shape), is_causal=is_causal,
-                          mask_fn=mask_fn, block_size=block_size, window_size=window_size)
+                          mask_fn=mask_fn, block_size=block_size, window_size=window_size,
+                          device=Q.device if Q.is_cuda else None)
     scale = _kernel_scale(kernel_fn, plan.d)
     if not (Q.is_cuda and K.is_cuda and V.is_cuda):
         raise RuntimeError("masked_attention_via_map runs on the GPU only (no CPU code path)")

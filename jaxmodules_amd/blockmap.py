@@ -25,11 +25,14 @@ reference's ``create_block_mask``.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Optional, Tuple
 
 import numpy as np
+
+from .masks import MaskSpec, spec_of
 
 TILE = 128
 NUM_XCD = 8  # MI355X: 8 accelerator complex dies, workgroups dispatched round-robin
@@ -76,6 +79,10 @@ def _causal(b, h, q, k):
 
 def _everything(b, h, q, k):
     return True
+
+
+_causal._mattn_spec = MaskSpec(causal=True)
+_everything._mattn_spec = MaskSpec()
 
 
 def make_plan(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, block_size=None,
@@ -312,6 +319,20 @@ def trace_strips(strip, B, Hq, Hkv, N, L, map_b, map_h) -> TileMap:
         mid = np.concatenate(ent_mid)
     else:
         r = kt = mid = np.zeros(0, np.int64)
+    rb = np.stack(row_bits) if row_bits else np.zeros((0, 2, TILE), np.uint64)
+    cb = np.stack(col_bits) if col_bits else np.zeros((0, 2, TILE), np.uint64)
+    return _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_full,
+                     n_partial, t0)
+
+
+def _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_full, n_partial,
+              t0) -> TileMap:
+    """TileMap from its present tiles: map row r = (mb * map_h + mh) * nqt + qt,
+    key tile kt and mask id (-1 full) of each, and the distinct masks' bits."""
+    import time
+
+    nqt, nkt = -(-N // TILE), -(-L // TILE)
+    nmap = map_b * map_h
     o = np.lexsort((kt, r))                 # rows ascending, key tiles ascending
     r, kt, mid = r[o], kt[o], mid[o]
     row_ptr = np.zeros(nmap * nqt + 1, np.int64)
@@ -340,12 +361,114 @@ def trace_strips(strip, B, Hq, Hkv, N, L, map_b, map_h) -> TileMap:
     kv_order = _lpt_xcd_order(kvw, kvgroups)
 
     pairs = pairs_map * (B // map_b) * (Hq // map_h)
-    rb = np.stack(row_bits) if row_bits else np.zeros((0, 2, TILE), np.uint64)
-    cb = np.stack(col_bits) if col_bits else np.zeros((0, 2, TILE), np.uint64)
     return TileMap(B, Hq, Hkv, N, L, map_b, map_h, nqt, nkt,
                    row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent,
                    np.ascontiguousarray(rb), np.ascontiguousarray(cb), q_order, kv_order, pairs,
                    n_full=n_full, n_partial=n_partial, trace_seconds=time.perf_counter() - t0)
+
+
+def device_trace(plan: Plan, device) -> TileMap:
+    """The TileMap of ``trace(plan)``, built on the GPU for a mask in closed form
+    (``plan.mask4`` made by ``jaxmodules_amd.masks``, or causal / no mask).
+
+    ``mattn_tilemap_classify`` evaluates every tile on the device (one wave per
+    tile) and returns per tile its state, allowed-element count and a 128-bit
+    hash of a partial tile's bits.  The host numbers the distinct partial
+    masks in the order the host tracer meets them (query tile, map row, key
+    tile) -- de-duplicated by hash -- and assembles the lists with the same code
+    as ``trace``; ``mattn_tilemap_bits`` then writes the distinct masks and
+    checks every partial tile against the mask its hash picked (a collision
+    raises).  The result equals ``trace(plan)`` array for array."""
+    import time
+
+    import torch
+
+    from . import _lib
+
+    spec = spec_of(plan.mask4)
+    if spec is None:
+        raise ValueError("device_trace needs a mask made by jaxmodules_amd.masks (or causal / None)")
+    t0 = time.perf_counter()
+    B, Hq, N, L = plan.B, plan.Hq, plan.N, plan.L
+    spec.check(B, Hq, N, L)
+    map_b, map_h = spec.map_dims(B, Hq)
+    nqt, nkt = -(-N // TILE), -(-L // TILE)
+    nmap = map_b * map_h
+    lib = _lib.load()
+    dev = torch.device(device)
+    keep = []
+
+    def up(a):
+        t = torch.from_numpy(np.array(a, copy=True, order="C")).to(dev)
+        keep.append(t)
+        return t.data_ptr()
+
+    ms = _lib.MattnMaskspec(causal=int(spec.causal),
+                            win_left=-1 if spec.win_left is None else min(spec.win_left, 2**31 - 2),
+                            win_right=-1 if spec.win_right is None else min(spec.win_right, 2**31 - 2))
+    if spec.doc_q is not None:
+        ms.doc_b = spec.doc_q.shape[0] if map_b > 1 else 1
+        ms.doc_q = up(spec.doc_q[:ms.doc_b])
+        ms.doc_k = up(spec.doc_k[:ms.doc_b])
+    if spec.table is not None:
+        ms.tab_b, ms.tab_h = spec.table.shape[0], spec.table.shape[1]
+        ms.tiles = up(spec.table)
+    if plan.window is not None:
+        ms.blk_size, ms.blk_left, ms.blk_right = plan.bs, plan.window[0], plan.window[1]
+        ms.blk_nk = plan.Lpad // plan.bs
+    nt = nmap * nqt * nkt
+    state = torch.empty(nt, dtype=torch.int8, device=dev)
+    count = torch.empty(nt, dtype=torch.int32, device=dev)
+    hsh = torch.empty(2 * nt, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    args = (ctypes.byref(ms), N, L, map_b, map_h)
+    _lib.check(lib.mattn_tilemap_classify(*args, state.data_ptr(), count.data_ptr(), hsh.data_ptr(),
+                                          stream), "mattn_tilemap_classify")
+    st = state.cpu().numpy().reshape(nmap, nqt, nkt)
+    cnt = count.cpu().numpy()
+    hv = hsh.cpu().numpy().view(np.uint64).reshape(nmap, nqt, nkt, 2)
+
+    # partial tiles in the host tracer's order of discovery: query tile, map row, key tile
+    qp, mp, kp = np.nonzero(st.transpose(1, 0, 2) == 2)
+    tidx = (mp * nqt + qp) * nkt + kp
+    if len(tidx):
+        h = np.ascontiguousarray(hv[mp, qp, kp]).view(np.dtype((np.void, 16))).reshape(-1)
+        _, first, inv = np.unique(h, return_index=True, return_inverse=True)
+        rank = np.empty(len(first), np.int64)
+        rank[np.argsort(first)] = np.arange(len(first))
+        pmid = rank[inv.reshape(-1)]
+        n_masks = len(first)
+        reps = np.stack([tidx[np.sort(first)], np.arange(n_masks)], axis=1).astype(np.int32)
+        allp = np.stack([tidx, pmid], axis=1).astype(np.int32)
+        rbits = torch.empty(n_masks * 2 * TILE, dtype=torch.int64, device=dev)
+        cbits = torch.empty_like(rbits)
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+        for lst, write in ((reps, 1), (allp, 0)):
+            _lib.check(lib.mattn_tilemap_bits(*args, up(lst.reshape(-1)), len(lst), n_masks, write,
+                                              rbits.data_ptr(), cbits.data_ptr(), bad.data_ptr(),
+                                              stream), "mattn_tilemap_bits")
+        if int(bad.item()) != 0:
+            raise RuntimeError("tile-map hash collision: two different partial tiles hashed alike")
+        rb = rbits.cpu().numpy().view(np.uint64).reshape(n_masks, 2, TILE)
+        cb = cbits.cpu().numpy().view(np.uint64).reshape(n_masks, 2, TILE)
+    else:
+        pmid = np.zeros(0, np.int64)
+        rb = cb = np.zeros((0, 2, TILE), np.uint64)
+
+    # present tiles: map row, key tile, mask id
+    mm, qq, kk = np.nonzero(st)
+    mid = np.full(len(mm), -1, np.int64)
+    flat = (mm * nqt + qq) * nkt + kk
+    if len(tidx):
+        pos = np.searchsorted(flat, tidx)      # flat is ascending; every partial tile is in it
+        mid[pos] = pmid
+    r = mm * nqt + qq
+    n_partial = len(tidx)
+    n_full = len(mm) - n_partial
+    pairs_map = int(cnt.astype(np.int64).sum())
+    return _assemble(B, Hq, plan.Hkv, N, L, map_b, map_h, r.astype(np.int64), kk.astype(np.int64),
+                     mid, np.ascontiguousarray(rb), np.ascontiguousarray(cb), pairs_map, n_full,
+                     n_partial, t0)
 
 
 def flops(tm: TileMap, d: int):

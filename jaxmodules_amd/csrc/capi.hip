@@ -15,7 +15,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 

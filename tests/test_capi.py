@@ -46,7 +46,8 @@ def test_abi_version(lib):
 
 def test_struct_layout_matches_header(tmp_path):
     """Compile a probe against the header and compare sizeof/offsetof with ctypes."""
-    fields = {"mattn_problem": _lib.MattnProblem, "mattn_blockmap": _lib.MattnBlockmap}
+    fields = {"mattn_problem": _lib.MattnProblem, "mattn_blockmap": _lib.MattnBlockmap,
+              "mattn_maskspec": _lib.MattnMaskspec}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mattn.h"', "int main(void){"]
     for cname, cls in fields.items():
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')

@@ -1,0 +1,175 @@
+"""Closed-form masks (jaxmodules_amd.masks) on the CPU: each family evaluates
+like the plain mask function it stands for, both elementwise (scalars, the
+reference's calling convention) and through the host tracer, and bad
+arguments raise before anything reaches the GPU."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from jaxmodules_amd import _lib
+from jaxmodules_amd import blockmap as bmap
+from jaxmodules_amd import masks
+
+
+def assert_same_map(a, b):
+    for f in ("map_b", "map_h", "pairs", "n_full", "n_partial"):
+        assert getattr(a, f) == getattr(b, f), f
+    for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "row_bits", "col_bits", "q_order",
+              "kv_order"):
+        assert np.array_equal(getattr(a, f), getattr(b, f)), f
+
+
+def traced(shape_q, shape_k, **kw):
+    return bmap.trace(bmap.make_plan(shape_q, shape_k, shape_k, **kw))
+
+
+DOC = np.repeat(np.arange(7), [100, 37, 300, 5, 200, 158, 200])          # 1000 positions
+
+
+def test_scalar_calls_follow_the_definitions():
+    m = masks.intersect(masks.causal(), masks.window(3, 0), masks.documents(DOC))
+    for q, k in [(5, 5), (5, 2), (5, 1), (4, 6), (99, 99), (100, 99), (120, 118)]:
+        want = (q >= k) and (q - k <= 3) and DOC[q] == DOC[k]
+        assert bool(m(0, 0, q, k)) == want, (q, k)
+    w = masks.window(None, 2)
+    assert bool(w(0, 0, 0, 2)) and not bool(w(0, 0, 0, 3)) and bool(w(0, 0, 900, 0))
+
+
+@pytest.mark.parametrize("case", ["causal_window", "docs", "docs_batch", "table", "cross"])
+def test_host_trace_equals_lambda(case):
+    rng = np.random.default_rng(1)
+    if case == "causal_window":
+        sq = sk = (1, 1000, 2, 16)
+        mf = masks.intersect(masks.causal(), masks.window(130, 0))
+        lam = lambda b, h, q, k: (q >= k) & (q - k <= 130)                # noqa: E731
+        kw = dict(block_size=50)
+    elif case == "docs":
+        sq = sk = (2, 1000, 2, 16)
+        mf = masks.intersect(masks.documents(DOC), masks.causal())
+        lam = lambda b, h, q, k: (DOC[q] == DOC[k]) & (q >= k)            # noqa: E731
+        kw = dict(block_size=100)
+    elif case == "docs_batch":
+        sq = sk = (2, 1000, 2, 16)
+        d2 = np.stack([DOC, DOC[::-1].copy()])
+        mf = masks.documents(d2)
+        lam = lambda b, h, q, k: d2[b, q] == d2[b, k]                      # noqa: E731
+        kw = dict(block_size=100)
+    elif case == "table":
+        sq = sk = (1, 1000, 3, 16)
+        t = rng.integers(0, 3, size=(3, 8, 8)).astype(np.uint8)
+        mf = masks.intersect(masks.tile_table(t), masks.causal())
+        lam = lambda b, h, q, k: (t[h, q // 128, k // 128] == 1) | (       # noqa: E731
+            (t[h, q // 128, k // 128] == 2) & (q >= k))
+        kw = dict(block_size=100)
+    else:
+        sq, sk = (1, 300, 2, 16), (1, 700, 2, 16)
+        dq, dk = np.arange(300) // 30, np.arange(700) // 70
+        mf = masks.documents(dq, dk)
+        lam = lambda b, h, q, k: dq[q] == dk[k]                            # noqa: E731
+        kw = dict(block_size=100)
+    assert_same_map(traced(sq, sk, mask_fn=mf, **kw), traced(sq, sk, mask_fn=lam, **kw))
+
+
+def test_map_dims():
+    assert masks.spec_of(masks.causal()).map_dims(4, 8) == (1, 1)
+    assert masks.spec_of(masks.documents(np.zeros((4, 10), int))).map_dims(4, 8) == (4, 1)
+    assert masks.spec_of(masks.documents(np.zeros(10, int))).map_dims(4, 8) == (1, 1)
+    assert masks.spec_of(masks.tile_table(np.zeros((8, 1, 1), np.uint8))).map_dims(4, 8) == (1, 8)
+    assert masks.spec_of(masks.tile_table(np.zeros((4, 1, 1, 1), np.uint8))).map_dims(4, 8) == (4, 1)
+
+
+def test_intersect_rules():
+    s = masks.spec_of(masks.intersect(masks.window(10, 5), masks.window(20, 2), masks.causal()))
+    assert (s.win_left, s.win_right, s.causal) == (10, 2, True)
+    with pytest.raises(ValueError):
+        masks.intersect(masks.documents(DOC), masks.documents(DOC))
+    with pytest.raises(ValueError):
+        masks.intersect(masks.causal(), lambda b, h, q, k: q >= k)
+    with pytest.raises(ValueError):
+        masks.intersect()
+
+
+def test_argument_errors():
+    with pytest.raises(ValueError):
+        masks.window(-1, 0)
+    with pytest.raises(ValueError):
+        masks.documents(np.zeros((2, 3, 4), int))
+    with pytest.raises(ValueError):
+        masks.documents(np.zeros(10, np.float32))
+    with pytest.raises(ValueError):
+        masks.tile_table(np.full((2, 2), 3))
+    spec = masks.spec_of(masks.documents(np.zeros(100, int)))
+    with pytest.raises(ValueError):
+        spec.check(1, 1, 99, 100)                       # ids of the wrong length
+    spec = masks.spec_of(masks.tile_table(np.zeros((2, 2), np.uint8)))
+    with pytest.raises(ValueError):
+        spec.check(1, 1, 1000, 1000)                    # 8 x 8 tiles needed
+    spec.check(1, 1, 256, 129)
+    spec = masks.spec_of(masks.tile_table(np.zeros((3, 2, 2), np.uint8)))
+    with pytest.raises(ValueError):
+        spec.check(1, 4, 256, 256)                      # 3 head tables for 4 heads
+
+
+def test_arrays_are_copied_and_frozen():
+    d = DOC.copy()
+    m = masks.documents(d)
+    d[:] = 0
+    s = masks.spec_of(m)
+    assert s.doc_q.max() == 6
+    with pytest.raises(ValueError):
+        s.doc_q[0, 0] = 5
+
+
+def test_device_trace_needs_closed_form():
+    plan = bmap.make_plan((1, 64, 1, 16), (1, 64, 1, 16), (1, 64, 1, 16),
+                          mask_fn=lambda b, h, q, k: q >= k)
+    with pytest.raises(ValueError):
+        bmap.device_trace(plan, "cuda:0")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libmattn.so not built")
+    return _lib.load()
+
+
+def _spec(**kw):
+    s = _lib.MattnMaskspec(causal=1, win_left=-1, win_right=-1)
+    for k, v in kw.items():
+        setattr(s, k, v)
+    return s
+
+
+def test_maskspec_validate_codes(lib):
+    v = lambda s, Lq=1000, Lk=1000, mb=1, mh=1: lib.mattn_maskspec_validate(  # noqa: E731
+        ctypes.byref(s), Lq, Lk, mb, mh)
+    assert v(_spec()) == 0
+    assert lib.mattn_maskspec_validate(None, 10, 10, 1, 1) == -1
+    assert v(_spec(causal=2)) == -2
+    assert v(_spec(), Lq=0) == -2
+    assert v(_spec(win_left=-2)) == -2
+    assert v(_spec(doc_b=1)) == -1                                  # ids missing
+    assert v(_spec(doc_b=1, doc_q=8, doc_k=8)) == 0
+    assert v(_spec(doc_b=3, doc_q=8, doc_k=8), mb=2) == -2          # neither 1 nor map_b
+    assert v(_spec(doc_b=2, doc_q=8, doc_k=8), mb=2) == 0
+    assert v(_spec(tab_b=1, tab_h=1)) == -1                         # table missing
+    assert v(_spec(tab_b=1, tab_h=3, tiles=8), mh=4) == -2
+    assert v(_spec(tab_b=1, tab_h=4, tiles=8), mh=4) == 0
+    assert v(_spec(blk_size=128, blk_left=0, blk_right=0, blk_nk=8)) == -2
+    assert v(_spec(blk_size=128, blk_left=4, blk_right=1, blk_nk=4)) == -2
+    assert v(_spec(blk_size=128, blk_left=3, blk_right=1, blk_nk=4)) == 0
+    assert v(_spec(), Lq=2**30, Lk=2**30) == -8                     # tile index beyond int32
+
+
+def test_tilemap_entry_points_reject_before_launch(lib):
+    s = _spec()
+    assert lib.mattn_tilemap_classify(ctypes.byref(s), 100, 100, 1, 1, None, None, None, None) == -1
+    assert lib.mattn_tilemap_bits(ctypes.byref(s), 100, 100, 1, 1, None, 1, 1, 1, None, None, None,
+                                  None) == -1
+    assert lib.mattn_tilemap_bits(ctypes.byref(s), 100, 100, 1, 1, None, -1, 1, 1, None, None, None,
+                                  None) == -2
+    assert lib.mattn_tilemap_bits(ctypes.byref(s), 100, 100, 1, 1, None, 0, 0, 1, None, None, None,
+                                  None) == 0                          # nothing to do
