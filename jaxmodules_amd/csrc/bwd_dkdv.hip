@@ -38,6 +38,13 @@ void bwd_dkdv_mfma(KArgs a) {
   constexpr int BLK = 512;            // elements one load instruction fills
   constexpr int NS = BM * D / BLK / 8;  // load slots per wave for a 64-row tile
   constexpr int NW = 8;
+  // The Q / dO_h buffers lie above the K and V tiles, 64 KiB up at D = 128: a
+  // ds_read immediate (16 bits) cannot reach them from an LDS offset near 0, so
+  // their per-lane seeds carry +64 KiB (QB elements) and the operand reads use
+  // array bases lowered by as much -- the array address minus 64 KiB is then
+  // the immediate, and no add per read is needed (any placement stays correct;
+  // only this one is fast).
+  constexpr int QB = D == 128 ? 32768 : 0;
 
   // one array per buffer: the compiler then knows the loads landing in one
   // buffer cannot alias the operand reads of the other (no vmcnt waits mid-step)
@@ -190,12 +197,13 @@ void bwd_dkdv_mfma(KArgs a) {
 
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* Qb = BUF ? Q1 : Q0;
-    const uint16_t* Hb = BUF ? H1 : H0;
+    const uint16_t* Qb = (BUF ? Q1 : Q0) - QB;   // indexed with the biased seeds below
+    const uint16_t* Hb = (BUF ? H1 : H0) - QB;
     const float* Lb = (BUF ? L1 : L0) + 32 * qh;
     const float* Gb = (BUF ? G1 : G0) + 32 * qh;
-    // seeds re-defined here, so the addresses derived from them stay per use
-    const int rxo = opaque(rx), qro = opaque(qrow), kro = opaque(krow_l);
+    // seeds re-defined here, so the addresses derived from them stay per use;
+    // the Q / dO_h seeds carry a bias of QB elements (taken off the array bases)
+    const int rxo = opaque(rx), qro = opaque(qrow + QB), kro = opaque(krow_l);
     f32x16 st = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kd = 0; kd < NKD; ++kd) {
@@ -234,7 +242,7 @@ void bwd_dkdv_mfma(KArgs a) {
       pk[r >> 3][(r & 7) >> 1] = H::pack2(st[r], st[r + 1]);
       sk[r >> 3][(r & 7) >> 1] = E::pack2(dp[r], dp[r + 1]);
     }
-    const int tzo = opaque(tz), t0 = opaque(tb0), t1 = opaque(tb1);
+    const int tzo = opaque(tz), t0 = opaque(tb0 + QB), t1 = opaque(tb1 + QB);
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt) {
       const int xm = (32 * mt) ^ tzo;
