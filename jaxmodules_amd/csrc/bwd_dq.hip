@@ -29,8 +29,9 @@ void bwd_dq_mfma(KArgs a) {
   constexpr int NI = D / 32;       // load instructions per wave per tile
   constexpr int BLK = 512;         // elements one load instruction fills
 
-  __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t V0[BN * D], V1[BN * D];
+  // K and V tiles of one buffer in one array (V at + BN D): the V operand reads
+  // reuse the K address with a constant offset
+  __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];
 
   const int item = a.q_order[blockIdx.x];
@@ -92,8 +93,8 @@ void bwd_dq_mfma(KArgs a) {
     int kt, mask;
     ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
     const int key0 = kt * TILE + (s & 1) * BN;
-    uint16_t* kl = (BUF ? K1 : K0) + wofs;
-    uint16_t* vl = (BUF ? V1 : V0) + wofs;
+    uint16_t* kl = (BUF ? KV1 : KV0) + wofs;
+    uint16_t* vl = (BUF ? KV1 : KV0) + BN * D + wofs;
     if (mask >= 0) {
       const uint32_t* src = (const uint32_t*)(a.row_bits + ((int64_t)mask * 2 + (s & 1)) * TILE + wave * 32);
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
@@ -126,8 +127,8 @@ void bwd_dq_mfma(KArgs a) {
   // its two dQ k-steps before the next half starts (halves the live state).
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* Kb = BUF ? K1 : K0;
-    const uint16_t* Vb = BUF ? V1 : V0;
+    const uint16_t* Kb = BUF ? KV1 : KV0;
+    const uint16_t* Vb = Kb + BN * D;
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
     // seeds re-defined here, so the addresses derived from them stay per use
     const int rxo = opaque(rx), rro = opaque(rrow);
