@@ -23,8 +23,8 @@ namespace mattn {
 // column; Q, dO_h, lse, delta and the partial-tile mask words are
 // double-buffered and filled by direct global->LDS loads.  The two query
 // halves' dK/dV partials of a key are summed through LDS at the end.
-// V_h is V itself for float16 inputs (vs_k = 1) and the scaled float16 copy
-// the preprocess writes for bfloat16 inputs.
+// V_h is V itself for float16 inputs (vs_k = 1); for bfloat16 inputs the
+// prologue converts the column's V rows to float16, each scaled by vs_k.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
@@ -54,6 +54,7 @@ void bwd_dkdv_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Q0[BM * D], Q1[BM * D];
   __shared__ __attribute__((aligned(16))) uint16_t H0[BM * D], H1[BM * D];
   __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE * D], Vs[TILE * D];
+  __shared__ float VI[TILE];  // bfloat16 inputs: 1 / vs_k of the tile's keys
 
   const int item = a.kv_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
@@ -70,7 +71,8 @@ void bwd_dkdv_mfma(KArgs a) {
   const float c2 = a.scale_log2;
   const float inv_s = a.dscale[1];
   // dP = (dO_h V_h^T) / (s vs_k): one factor per lane, since a lane owns one key
-  const float dsc = IS_BF16 ? inv_s * a.vinv[((int64_t)b * a.Hkv + hk) * a.Lk + kcl] : inv_s;
+  // (set once the V tile is converted, below)
+  float dsc = inv_s;
 
   // Flattened walk over (query head g of the group, column entry, half).
   int tot = 0;
@@ -86,25 +88,17 @@ void bwd_dkdv_mfma(KArgs a) {
     lend = a.col_ptr[mc + 1];
   }
 
-  // K and V_h tiles of the column: loaded once, by all 8 waves
+  // K tile of the column (and V for float16 inputs): loaded once, by all 8 waves
+  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
   {
     const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-    const uint16_t* vb;
-    int64_t vrs;
-    if constexpr (IS_BF16) {
-      vb = (const uint16_t*)a.vh + (int64_t)b * a.Lk * a.Hkv * D + (int64_t)hk * D;
-      vrs = (int64_t)a.Hkv * D;
-    } else {
-      vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-      vrs = a.vs[1];
-    }
 #pragma unroll
     for (int i = 0; i < 2 * NS; ++i) {
       const int n = 2 * NS * wave + i;
       const int kk = min(kt * TILE + TL::row_of(n, lane), a.Lk - 1);
       const int c = TL::chunk_of(n, lane);
       lds_load16(kb + (int64_t)kk * a.ks[1] + 8 * c, Ks + n * BLK);
-      lds_load16(vb + (int64_t)kk * vrs + 8 * c, Vs + n * BLK);
+      if constexpr (!IS_BF16) lds_load16(vb + (int64_t)kk * a.vs[1] + 8 * c, Vs + n * BLK);
     }
   }
 
@@ -269,6 +263,43 @@ void bwd_dkdv_mfma(KArgs a) {
     step(bufc, masked);
   };
   if (tot > 0) issue(std::integral_constant<int, 0>{});
+  if constexpr (IS_BF16) {
+    // V tile in float16 for the dP product, each key row scaled by a power of
+    // two vs_k with max_d |V vs_k| in [2^13, 2^14): a bfloat16 value has 8
+    // significant bits, so V vs_k is exact in float16 down to 2^-16 (subnormals
+    // included), 2^29 below the row's largest element.  4 lanes per key row.
+    constexpr int CPL = D / 32;  // 16-byte chunks per lane
+    const int r = tid >> 2, part = tid & 3;
+    const int kk = min(kt * TILE + r, a.Lk - 1);
+    const uint16_t* vp = vb + (int64_t)kk * a.vs[1] + 8 * CPL * part;
+    u32x4 x[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = *(const u32x4*)(vp + 8 * j);
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(E::to_f32(elt16(x[j], e))));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    float vs = 1.f;
+    if (m > 0.f && m <= 3.4e38f) {
+      int e;
+      frexpf(m, &e);  // m < 2^e
+      vs = ldexpf(1.f, min(126, max(-126, 14 - e)));
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      u32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = H::pack2(E::to_f32(elt16(x[j], 2 * e)) * vs, E::to_f32(elt16(x[j], 2 * e + 1)) * vs);
+      *(u32x4*)&Vs[sw_off<D>(r, CPL * part + j)] = y;
+    }
+    if (part == 0) VI[r] = 1.f / vs;
+    __syncthreads();
+    dsc = inv_s * VI[kloc];
+  }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});

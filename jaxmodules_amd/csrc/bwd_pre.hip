@@ -156,49 +156,6 @@ void bwd_pre(KArgs a) {
   }
 }
 
-// bfloat16 inputs: V in float16 for the dP = dO V^T product of the dK/dV
-// kernel, each key row scaled by a power of two vs_k with max_d |V * vs_k| in
-// [2^13, 2^14).  A bfloat16 value has 8 significant bits, so V * vs_k is exact
-// in float16 down to 2^-16 (subnormals included), 2^29 below the row's largest
-// element.  Writes vh [B, Lk, Hkv, D] densely and vinv = 1 / vs_k [B, Hkv, Lk].
-// 16 lanes per (b, k, hk) row, 16 rows per workgroup.
-template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
-void bwd_vconv(KArgs a) {
-  using E = Elt<bf16_tag>;
-  using H = Elt<f16_tag>;
-  constexpr int PER = D / 16;
-  const uint32_t nrows = (uint32_t)a.B * a.Lk * a.Hkv;  // < 2^31 (checked by the C ABI)
-  const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
-  const int hk = (int)(row % (uint32_t)a.Hkv);
-  const uint32_t bk = row / (uint32_t)a.Hkv;
-  const int k = (int)(bk % (uint32_t)a.Lk), b = (int)(bk / (uint32_t)a.Lk);
-  float x[PER];
-  load_row<D, bf16_tag, false>(a.v, (int64_t)b * a.vs[0] + (int64_t)k * a.vs[1] + (int64_t)hk * a.vs[2],
-                               sub, x);
-  float m = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) m = fmaxf(m, fabsf(x[i]));
-  m = fmaxf(m, __shfl_xor(m, 1, 16));
-  m = fmaxf(m, __shfl_xor(m, 2, 16));
-  m = fmaxf(m, __shfl_xor(m, 4, 16));
-  m = fmaxf(m, __shfl_xor(m, 8, 16));
-  float s = 1.f;
-  if (m > 0.f && m <= 3.4e38f) {
-    int e;
-    frexpf(m, &e);  // m < 2^e
-    s = ldexpf(1.f, min(126, max(-126, 14 - e)));
-  }
-  uint16_t* w = (uint16_t*)a.vhw + (int64_t)row * D + sub * PER;
-#pragma unroll
-  for (int i = 0; i < PER; i += 4)
-    *(u32x2*)(w + i) = u32x2{H::pack2(x[i] * s, x[i + 1] * s), H::pack2(x[i + 2] * s, x[i + 3] * s)};
-  if (sub == 0) a.vinvw[((int64_t)b * a.Hkv + hk) * a.Lk + k] = 1.f / s;
-  (void)sizeof(E);
-}
-
 // ---------------------------------------------------------------------------
 // float32 SIMT backward
 // ---------------------------------------------------------------------------
@@ -401,10 +358,6 @@ hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int s
   if (dtype == MATTN_BF16) {
     if (D == 64) { if (of32) MATTN_PRE(64, bf16_tag, true, 2); else MATTN_PRE(64, bf16_tag, false, 2); }
     else { if (of32) MATTN_PRE(128, bf16_tag, true, 2); else MATTN_PRE(128, bf16_tag, false, 2); }
-    const int64_t krows = (int64_t)a.B * a.Lk * a.Hkv;
-    const int vgrid = (int)((krows + 15) / 16);
-    if (D == 64) hipLaunchKernelGGL((bwd_vconv<64>), dim3(vgrid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((bwd_vconv<128>), dim3(vgrid), dim3(256), 0, st, a);
   } else {
     if (D == 64) { if (of32) MATTN_PRE(64, f16_tag, true, 1); else MATTN_PRE(64, f16_tag, false, 1); }
     else { if (of32) MATTN_PRE(128, f16_tag, true, 1); else MATTN_PRE(128, f16_tag, false, 1); }

@@ -33,9 +33,9 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Backward workspace: delta (f32 per query row), the partial maxima of |dO|
 // and the scale pair, dO * s in float16, and for bfloat16 inputs dO in
-// bfloat16, V in float16 scaled per key row and the inverse row scales.
+// bfloat16.
 struct WsLayout {
-  size_t delta, part, scale, doh, do16, vh, vinv, total;
+  size_t delta, part, scale, doh, do16, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
@@ -46,10 +46,7 @@ WsLayout ws_layout(const mattn_problem* p) {
   w.scale = w.part + align256(NPART * sizeof(float));
   w.doh = w.scale + 256;
   w.do16 = w.doh + (p->dtype == MATTN_F32 ? 0 : align256(rows * p->D * 2));
-  w.vh = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
-  const size_t krows = (size_t)p->B * p->Hkv * p->Lk;
-  w.vinv = w.vh + (p->dtype == MATTN_BF16 ? align256(krows * p->D * 2) : 0);
-  w.total = w.vinv + (p->dtype == MATTN_BF16 ? align256(krows * sizeof(float)) : 0);
+  w.total = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
   return w;
 }
 
@@ -199,10 +196,6 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   a.dOh = a.dOhw;
   a.dO16w = ws + w.do16;
   a.dO16 = a.dO16w;
-  a.vhw = ws + w.vh;
-  a.vh = a.vhw;
-  a.vinvw = (float*)(ws + w.vinv);
-  a.vinv = a.vinvw;
   hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
                                   bm->n_kv_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;

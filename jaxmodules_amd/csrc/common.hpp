@@ -59,10 +59,6 @@ struct KArgs {
   void* dv;
   void* dO16w;       // writable aliases for the preprocess kernel
   void* dOhw;
-  const void* vh;    // bfloat16 inputs: V * vs_k in float16, dense [B, Lk, Hkv, D] (workspace)
-  const float* vinv; // bfloat16 inputs: 1 / vs_k per key row [B, Hkv, Lk] (workspace)
-  void* vhw;         // writable aliases of the two
-  float* vinvw;
   int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3];
   int B, Lq, Lk, Hq, Hkv, G;
   float scale;       // softmax scale

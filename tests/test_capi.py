@@ -126,15 +126,12 @@ def test_validate_blockmap(lib):
 def test_workspace_bytes(lib):
     p = _problem()
     rows = 2 * 8 * 300
-    krows = 2 * 2 * 300
     align = lambda x: (x + 255) // 256 * 256
     n = lib.mattn_workspace_bytes(ctypes.byref(p))
     # delta + partial maxima + scale + two 16-bit copies of dO (float16 scaled, bfloat16)
-    # + (bfloat16 inputs) V in float16 and its per-key-row scales
-    assert n >= rows * 4 + 2 * rows * 128 * 2 + krows * 128 * 2 + krows * 4
+    assert n >= rows * 4 + 2 * rows * 128 * 2
     p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
-    assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == \
-        n - align(rows * 128 * 2) - align(krows * 128 * 2) - align(krows * 4)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == n - align(rows * 128 * 2)
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
 
 
