@@ -65,7 +65,7 @@ void bwd_dq_mfma(KArgs a) {
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
   const float nlse = -a.lse[rs];
-  const float dl = a.delta[rs];
+  const float dl = IS_BF16 ? a.delta16[rs] : a.delta[rs];  // delta of the dO copy dP uses
   const float dps = IS_BF16 ? 1.f : a.dscale[1];  // undoes the dO scale of float16 inputs
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];

@@ -133,26 +133,53 @@ void bwd_pre(KArgs a) {
   load_row<D, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2], sub, x);
   load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
                           sub, g);
-  float acc = 0.f;
+  // delta = rowsum(dO * O) with dO as rounded in the copy whose dP it meets:
+  // dS = P (dP - delta) then cancels exactly where it should (a row with one
+  // allowed key has dS = 0), and its error scales with V - O rather than V.
+  // MODE 0: float32 dO; MODE 1, 2: the float16 dO * s copy (divided by s),
+  // and MODE 2 also delta16 from the bfloat16 copy (the dQ kernel's dP).
+  uint32_t hp[PER / 2], bp[PER / 2];
+  float acc = 0.f, acc16 = 0.f;
+  if constexpr (MODE == 0) {
 #pragma unroll
-  for (int i = 0; i < PER; ++i) acc = fmaf(x[i], g[i], acc);
-  acc += __shfl_xor(acc, 1, 16);
-  acc += __shfl_xor(acc, 2, 16);
-  acc += __shfl_xor(acc, 4, 16);
-  acc += __shfl_xor(acc, 8, 16);
-  if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
+    for (int i = 0; i < PER; ++i) acc = fmaf(x[i], g[i], acc);
+  } else {
+    const float inv = a.dscale[1];
+#pragma unroll
+    for (int i = 0; i < PER; i += 2) {
+      hp[i / 2] = H::pack2(g[i] * s, g[i + 1] * s);
+      acc = fmaf(x[i], H::to_f32(hp[i / 2] & 0xffffu) * inv, acc);
+      acc = fmaf(x[i + 1], H::to_f32(hp[i / 2] >> 16) * inv, acc);
+    }
+  }
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int i = 0; i < PER; i += 2) {
+      bp[i / 2] = E::pack2(g[i], g[i + 1]);
+      acc16 = fmaf(x[i], E::to_f32(bp[i / 2] & 0xffffu), acc16);
+      acc16 = fmaf(x[i + 1], E::to_f32(bp[i / 2] >> 16), acc16);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    acc += __shfl_xor(acc, o, 16);
+    if constexpr (MODE == 2) acc16 += __shfl_xor(acc16, o, 16);
+  }
+  const int64_t rr = ((int64_t)b * a.Hq + h) * a.Lq + q;
+  if (sub == 0) {
+    a.delta[rr] = acc;
+    if constexpr (MODE == 2) a.delta16[rr] = acc16;
+  }
   if constexpr (MODE > 0) {
     // dense [B, Lq, Hq, D] copies
     uint16_t* w = (uint16_t*)a.dOhw + (int64_t)row * D + sub * PER;
 #pragma unroll
-    for (int i = 0; i < PER; i += 4)
-      *(u32x2*)(w + i) = u32x2{H::pack2(g[i] * s, g[i + 1] * s), H::pack2(g[i + 2] * s, g[i + 3] * s)};
+    for (int i = 0; i < PER; i += 4) *(u32x2*)(w + i) = u32x2{hp[i / 2], hp[i / 2 + 1]};
   }
   if constexpr (MODE == 2) {
     uint16_t* w = (uint16_t*)a.dO16w + (int64_t)row * D + sub * PER;
 #pragma unroll
-    for (int i = 0; i < PER; i += 4)
-      *(u32x2*)(w + i) = u32x2{E::pack2(g[i], g[i + 1]), E::pack2(g[i + 2], g[i + 3])};
+    for (int i = 0; i < PER; i += 4) *(u32x2*)(w + i) = u32x2{bp[i / 2], bp[i / 2 + 1]};
   }
 }
 

@@ -33,9 +33,9 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Backward workspace: delta (f32 per query row), the partial maxima of |dO|
 // and the scale pair, dO * s in float16, and for bfloat16 inputs dO in
-// bfloat16.
+// bfloat16 with its own delta.
 struct WsLayout {
-  size_t delta, part, scale, doh, do16, total;
+  size_t delta, part, scale, doh, do16, delta16, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
@@ -46,7 +46,8 @@ WsLayout ws_layout(const mattn_problem* p) {
   w.scale = w.part + align256(NPART * sizeof(float));
   w.doh = w.scale + 256;
   w.do16 = w.doh + (p->dtype == MATTN_F32 ? 0 : align256(rows * p->D * 2));
-  w.total = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
+  w.delta16 = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
+  w.total = w.delta16 + (p->dtype == MATTN_BF16 ? align256(rows * sizeof(float)) : 0);
   return w;
 }
 
@@ -190,6 +191,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
+  a.delta16 = (float*)(ws + w.delta16);
   a.part = (float*)(ws + w.part);
   a.dscale = (float*)(ws + w.scale);
   a.dOhw = ws + w.doh;

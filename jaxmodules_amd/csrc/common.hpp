@@ -53,7 +53,8 @@ struct KArgs {
   float* part;       // [NPART] partial max |dO| (workspace)
   void* out;         // forward output O
   float* lse;        // [B, Hq, Lq] base-2 log-sum-exp
-  float* delta;      // [B, Hq, Lq] rowsum(dO * O) (workspace)
+  float* delta;      // [B, Hq, Lq] rowsum(dO * O), dO as in dOh (workspace)
+  float* delta16;    // [B, Hq, Lq] rowsum(dO * O), dO as in dO16 (workspace; bf16 inputs only)
   void* dq;
   void* dk;
   void* dv;

@@ -45,12 +45,19 @@ def seeded_inputs(B, N, L, Hq, Hkv, d, seed, scaled=True):
 
 
 def oracle(Q, K, V, dO, kw, grads=True):
-    """fp64 closed-form O, base-2 LSE and gradients on exactly the given values."""
+    """fp64 closed-form O, base-2 LSE and gradients on exactly the given values.
+    A ``kernel_fn`` in kw selects the softmax scale: the reference's
+    threshold_kernel (attention.py:18-36) is exp(q.k - t / sqrt(d)), whose
+    constant factor cancels in the normalisation -- scale 1; the default
+    kernel's is 1/sqrt(d)."""
+    kw = dict(kw)
+    kfn = kw.pop("kernel_fn", None)
+    scale = None if kfn is None or getattr(kfn, "_mattn_scale", None) is None else float(kfn._mattn_scale)
     plan = ao.canonical_plan(Q.shape, K.shape, V.shape, **kw)
     Qb, Kb, Vb, dOb = (x if x is None or not plan.squeeze_batch else x[None] for x in (Q, K, V, dO))
     allowed = ao.effective_mask(plan)
-    O, lse = ao.dense_forward(Qb, Kb, Vb, allowed)
-    g = ao.dense_backward(Qb, Kb, Vb, allowed, dOb) if grads else None
+    O, lse = ao.dense_forward(Qb, Kb, Vb, allowed, scale=scale)
+    g = ao.dense_backward(Qb, Kb, Vb, allowed, dOb, scale=scale) if grads else None
     if plan.squeeze_batch:
         O = O[0]
         g = tuple(x[0] for x in g) if g is not None else None

@@ -35,6 +35,9 @@ def config(name):
     if name == "cfg2":
         kw = dict(is_causal=True, block_size=128)
         return 4, 4096, 32, 128, kw, lambda h, q, k: q >= k
+    if name == "target":   # the north star's shape
+        kw = dict(is_causal=True, block_size=128)
+        return 1, 8192, 32, 128, kw, lambda h, q, k: q >= k
     if name == "cfg3":
         m = lambda b, h, q, k: (q >= k) & (q - k <= 512)
         kw = dict(mask_fn=m, window_size=(512, 0), block_size=128)
@@ -85,7 +88,7 @@ def reference_head(q, k, v, do, allowed_fn, h, chunk):
     return O, dQ, dK, dV
 
 
-@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg5"])
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg5", "target"])
 def test_baseline_config_full_size(name):
     import jaxmodules_amd as jm
 

@@ -387,3 +387,30 @@ def test_oracle_rounding_floor():
     assert half_ulp(np.array([1.0, 3.0, 0.3]), "bfloat16").tolist() == [2 ** -8, 2 ** -7, 2 ** -10]
     assert half_ulp(np.array([1.0, 3.0]), "float16").tolist() == [2 ** -11, 2 ** -10]
     assert half_ulp(np.array([5.0]), "float32").tolist() == [0.0]
+
+
+def test_threshold_kernel_is_scale_one_softmax():
+    """attention.py:18-36: threshold_kernel(t) scores exp(q.k - t / sqrt(d)) and
+    the running mean normalises by their sum (attention.py:83-100), so the
+    constant factor exp(-t / sqrt(d)) cancels: the result is softmax with scale
+    1.  Checked by evaluating the kernel's scores literally (vectorised over the
+    tile) against the oracle's dense path at scale=1, for several thresholds."""
+    from jaxmodules_amd.attention import threshold_kernel
+
+    rng = np.random.default_rng(7)
+    B, N, H, d = 1, 24, 2, 16
+    Q = rng.standard_normal((B, N, H, d)) * 0.3
+    K = rng.standard_normal((B, N, H, d)) * 0.3
+    V = rng.standard_normal((B, N, H, d))
+    allowed = np.broadcast_to(np.tril(np.ones((N, N), bool))[None, None], (B, H, N, N))
+    O1, _ = ao.dense_forward(Q, K, V, allowed, scale=1.0)
+    for t in (None, 0.0, 3.0, -2.5):
+        kfn = threshold_kernel(t)
+        assert kfn._mattn_scale == 1.0
+        sc = np.zeros((B, H, N, N))
+        for h in range(H):
+            for i in range(N):
+                for j in range(N):
+                    sc[0, h, i, j] = kfn(Q[0, i, h], K[0, j, h]) if allowed[0, h, i, j] else 0.0
+        O = np.einsum("bhqk,bkhd->bqhd", sc, V) / sc.sum(-1)[..., None].transpose(0, 2, 1, 3)
+        np.testing.assert_allclose(O, O1, rtol=1e-12, atol=1e-12)
