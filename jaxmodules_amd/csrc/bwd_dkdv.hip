@@ -74,20 +74,6 @@ void bwd_dkdv_mfma(KArgs a) {
   // (set once the V tile is converted, below)
   float dsc = inv_s;
 
-  // Flattened walk over (query head g of the group, column entry, half).
-  int tot = 0;
-  for (int g = 0; g < a.G; ++g) {
-    const int mc = map_row(a, b, hk * a.G + g, a.nkt, kt);
-    tot += 2 * (a.col_ptr[mc + 1] - a.col_ptr[mc]);
-  }
-  // cursor of the next sub-block to load
-  int lg = 0, le = 0, lend = 0, lhalf = 0;
-  {
-    const int mc = map_row(a, b, hk * a.G, a.nkt, kt);
-    le = a.col_ptr[mc];
-    lend = a.col_ptr[mc + 1];
-  }
-
   // K tile of the column (and V for float16 inputs): loaded once, by all 8 waves
   const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
   {
@@ -100,6 +86,31 @@ void bwd_dkdv_mfma(KArgs a) {
       lds_load16(kb + (int64_t)kk * a.ks[1] + 8 * c, Ks + n * BLK);
       if constexpr (!IS_BF16) lds_load16(vb + (int64_t)kk * a.vs[1] + 8 * c, Vs + n * BLK);
     }
+  }
+
+  // bfloat16 inputs: this thread's share of the V tile (4 threads per key row),
+  // loaded now so that the column-list reads below overlap its latency
+  constexpr int CPL = D / 32;  // 16-byte chunks per thread
+  u32x4 vx[CPL];
+  if constexpr (IS_BF16) {
+    const int kk = min(kt * TILE + (tid >> 2), a.Lk - 1);
+    const uint16_t* vp = vb + (int64_t)kk * a.vs[1] + 8 * CPL * (tid & 3);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) vx[j] = *(const u32x4*)(vp + 8 * j);
+  }
+
+  // Flattened walk over (query head g of the group, column entry, half).
+  int tot = 0;
+  for (int g = 0; g < a.G; ++g) {
+    const int mc = map_row(a, b, hk * a.G + g, a.nkt, kt);
+    tot += 2 * (a.col_ptr[mc + 1] - a.col_ptr[mc]);
+  }
+  // cursor of the next sub-block to load
+  int lg = 0, le = 0, lend = 0, lhalf = 0;
+  {
+    const int mc = map_row(a, b, hk * a.G, a.nkt, kt);
+    le = a.col_ptr[mc];
+    lend = a.col_ptr[mc + 1];
   }
 
   const int64_t drow = (int64_t)a.Hq * D;   // row stride of the dense dO_h copy
@@ -268,13 +279,8 @@ void bwd_dkdv_mfma(KArgs a) {
     // two vs_k with max_d |V vs_k| in [2^13, 2^14): a bfloat16 value has 8
     // significant bits, so V vs_k is exact in float16 down to 2^-16 (subnormals
     // included), 2^29 below the row's largest element.  4 lanes per key row.
-    constexpr int CPL = D / 32;  // 16-byte chunks per lane
     const int r = tid >> 2, part = tid & 3;
-    const int kk = min(kt * TILE + r, a.Lk - 1);
-    const uint16_t* vp = vb + (int64_t)kk * a.vs[1] + 8 * CPL * part;
-    u32x4 x[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) x[j] = *(const u32x4*)(vp + 8 * j);
+    const u32x4* x = vx;
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
@@ -306,48 +312,64 @@ void bwd_dkdv_mfma(KArgs a) {
   }
 
   // dK / dV: the second query half's partials join the first's through LDS
-  // (wave kg + 4 -> wave kg, one 16 KiB slab per key group, lane-major floats)
+  // (wave kg + 4 -> wave kg; per key group a dK slab in the K / V tiles and a
+  // dV slab in a Q / dO_h buffer, all free now; lane-major floats).  Wave kg
+  // then writes the finished rows of its 32 keys, scaled and rounded, over its
+  // own slabs as [32 keys][D + 8] tiles, and all 8 waves store the 128 x D
+  // tiles with 16-byte accesses along the rows.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  float* red = (float*)(kg == 0 ? Q0 : kg == 1 ? Q1 : kg == 2 ? H0 : H1);
-  static_assert(NMD * 16 * 64 * 4 <= BM * D * 2, "reduction slab");
+  constexpr int SLAB = NMD * 16 * 64;  // floats
+  constexpr int OR = D + 8;            // staged row (elements): 16-byte aligned, spreads banks
+  static_assert(2 * SLAB * 4 <= TILE * D * 2 && SLAB * 4 <= BM * D * 2 && 32 * OR * 2 <= SLAB * 4,
+                "reduction slabs");
+  float* redk = (float*)(kg < 2 ? Ks : Vs) + (kg & 1) * SLAB;
+  float* redv = (float*)(kg == 0 ? Q0 : kg == 1 ? Q1 : kg == 2 ? H0 : H1);
+  if (qh == 1) {
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    if (qh == 1) {
+    for (int mt = 0; mt < NMD; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < NMD; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) red[(mt * 16 + r) * 64 + lane] = pass == 0 ? dk[mt][r] : dv[mt][r];
-    }
-    __syncthreads();
-    if (qh == 0) {
-#pragma unroll
-      for (int mt = 0; mt < NMD; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = red[(mt * 16 + r) * 64 + lane];
-          if (pass == 0) dk[mt][r] += x; else dv[mt][r] += x;
-        }
-    }
-    __syncthreads();
+      for (int r = 0; r < 16; ++r) {
+        redk[(mt * 16 + r) * 64 + lane] = dk[mt][r];
+        redv[(mt * 16 + r) * 64 + lane] = dv[mt][r];
+      }
   }
-
-  if (qh != 0 || key >= a.Lk) return;
-  char* kp = (char*)a.dk;
-  char* vp = (char*)a.dv;
-  const int64_t krow = (int64_t)b * a.dks[0] + (int64_t)key * a.dks[1] + (int64_t)hk * a.dks[2];
-  const int64_t vrow = (int64_t)b * a.dvs[0] + (int64_t)key * a.dvs[1] + (int64_t)hk * a.dvs[2];
+  __syncthreads();
+  if (qh == 0) {
+    // the slabs are this wave's alone: the rows overwrite them after the reads
+    auto finish = [&](f32x16 (&acc)[NMD], float* red, float sc) {
 #pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
+      for (int mt = 0; mt < NMD; ++mt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * mt + 8 * j + 4 * hi;
-      *(u32x2*)(kp + 2 * (krow + d)) =
-          u32x2{E::pack2(dk[mt][4 * j] * a.scale, dk[mt][4 * j + 1] * a.scale),
-                E::pack2(dk[mt][4 * j + 2] * a.scale, dk[mt][4 * j + 3] * a.scale)};
-      *(u32x2*)(vp + 2 * (vrow + d)) =
-          u32x2{E::pack2(dv[mt][4 * j] * inv_s, dv[mt][4 * j + 1] * inv_s),
-                E::pack2(dv[mt][4 * j + 2] * inv_s, dv[mt][4 * j + 3] * inv_s)};
+        for (int r = 0; r < 16; ++r) acc[mt][r] += red[(mt * 16 + r) * 64 + lane];
+      uint16_t* o = (uint16_t*)red + l32 * OR;
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *(u32x2*)(o + 32 * mt + 8 * j + 4 * hi) =
+              u32x2{E::pack2(acc[mt][4 * j] * sc, acc[mt][4 * j + 1] * sc),
+                    E::pack2(acc[mt][4 * j + 2] * sc, acc[mt][4 * j + 3] * sc)};
+      }
+    };
+    finish(dk, redk, a.scale);
+    finish(dv, redv, inv_s);
+  }
+  __syncthreads();
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+#pragma unroll
+  for (int i = 0; i < TILE * CPR / 512; ++i) {
+    const int n = tid + 512 * i;
+    const int kl = n / CPR, c = n % CPR;  // key within the tile, chunk
+    const int key_n = kt * TILE + kl;
+    const int g = kl >> 5, off = (kl & 31) * OR + 8 * c;
+    const float* sk = (const float*)(g < 2 ? Ks : Vs) + (g & 1) * SLAB;
+    const float* sv = (const float*)(g == 0 ? Q0 : g == 1 ? Q1 : g == 2 ? H0 : H1);
+    const u32x4 xk = *(const u32x4*)((const uint16_t*)sk + off);
+    const u32x4 xv = *(const u32x4*)((const uint16_t*)sv + off);
+    if (key_n < a.Lk) {
+      *(u32x4*)((char*)a.dk + 2 * ((int64_t)b * a.dks[0] + (int64_t)key_n * a.dks[1] + (int64_t)hk * a.dks[2] + 8 * c)) = xk;
+      *(u32x4*)((char*)a.dv + 2 * ((int64_t)b * a.dvs[0] + (int64_t)key_n * a.dvs[1] + (int64_t)hk * a.dvs[2] + 8 * c)) = xv;
     }
   }
 }
