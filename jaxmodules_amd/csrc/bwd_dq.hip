@@ -43,7 +43,8 @@ void bwd_dq_mfma(KArgs a) {
   const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
   const int nsb = 2 * (e1 - e0);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int qloc = wave * 32 + l32;
   const int q = qt * TILE + qloc;
@@ -187,19 +188,15 @@ void bwd_dq_mfma(KArgs a) {
     if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
   }
 
-  if (q >= a.Lq) return;
-  char* op = (char*)a.dq;
-  const int64_t orow = (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2];
-#pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * mt + 8 * j + 4 * hi;
-      *(u32x2*)(op + 2 * (orow + d)) =
-          u32x2{E::pack2(acc[mt][4 * j] * a.scale, acc[mt][4 * j + 1] * a.scale),
-                E::pack2(acc[mt][4 * j + 2] * a.scale, acc[mt][4 * j + 3] * a.scale)};
-    }
-  }
+  // dQ through LDS (an eighth of the K / V buffers per wave, free once every wave is done)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * 32 * D;
+  static_assert(2 * 32 * D <= 2 * BN * D, "output staging");
+  const int r0 = qt * TILE + 32 * wave;
+  store_rows<D, 2>(acc, a.scale, stage, a.dq,
+                   (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2], a.dqs[1],
+                   min(32, a.Lq - r0), lane, E::pack2);
 }
 
 // ---------------------------------------------------------------------------

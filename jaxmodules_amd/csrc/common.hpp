@@ -301,6 +301,44 @@ struct EntryCache {
   }
 };
 
+// Output rows of one wave from the MFMA C layout to global memory along the
+// rows.  The wave holds 32 rows x D columns as acc[mt][4 j + i] = column
+// 32 mt + 8 j + 4 hi + i of row l32 (scaled by sc on the way out); they are
+// staged in `lds` (32 * D * ES bytes, this wave's alone) as rows of 16-byte
+// chunks, chunk c of row r at c ^ (r % chunks-per-row), then read back so that
+// each global store instruction writes whole rows, 16 bytes per lane.  Row r
+// goes to out + ES * (row0 + r * rstride) when r < nrows.  ES = 4 stores
+// float32, ES = 2 the 16-bit values pack2 makes.
+template <int D, int ES, class Pack>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc, void* lds, void* out,
+                                           int64_t row0, int64_t rstride, int nrows, int lane, Pack pack2) {
+  constexpr int RB = D * ES;     // bytes per row
+  constexpr int CPR = RB / 16;   // 16-byte chunks per row
+  const int r = lane & 31, hi = lane >> 5;
+  char* L = (char*)lds;
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * mt + 8 * j + 4 * hi;
+      const float o0 = acc[mt][4 * j] * sc, o1 = acc[mt][4 * j + 1] * sc;
+      const float o2 = acc[mt][4 * j + 2] * sc, o3 = acc[mt][4 * j + 3] * sc;
+      if constexpr (ES == 4) {
+        *(f32x4*)(L + r * RB + (((d >> 2) ^ (r & (CPR - 1))) << 4)) = f32x4{o0, o1, o2, o3};
+      } else {
+        *(u32x2*)(L + r * RB + (((d >> 3) ^ (r & (CPR - 1))) << 4) + 8 * hi) = u32x2{pack2(o0, o1), pack2(o2, o3)};
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 32 * CPR / 64; ++i) {
+    const int n = 64 * i + lane;
+    const int row = n / CPR, c = n % CPR;
+    const u32x4 v = *(const u32x4*)(L + row * RB + ((c ^ (row & (CPR - 1))) << 4));
+    if (row < nrows) *(u32x4*)((char*)out + (int64_t)ES * (row0 + (int64_t)row * rstride) + 16 * c) = v;
+  }
+}
+
 // x, re-defined by an empty asm: values computed from the result inside a loop
 // are not hoisted out of it (trades a few VALU ops for registers held across the loop)
 __device__ __forceinline__ int opaque(int x) {

@@ -47,7 +47,8 @@ void fwd_mfma(KArgs a) {
   const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
   const int nsb = 2 * (e1 - e0);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int qloc = wave * 32 + l32;
   const int q = qt * TILE + qloc;
@@ -202,26 +203,18 @@ void fwd_mfma(KArgs a) {
   }
 
   l = wave_sum32(l);
-  if (q >= a.Lq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (hi == 0)
+  if (hi == 0 && q < a.Lq)
     a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
-  char* op = (char*)a.out;
-  const int64_t orow = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2];
-#pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * mt + 8 * j + 4 * hi;
-      const float o0 = acc[mt][4 * j] * inv, o1 = acc[mt][4 * j + 1] * inv;
-      const float o2 = acc[mt][4 * j + 2] * inv, o3 = acc[mt][4 * j + 3] * inv;
-      if constexpr (OUT_F32) {
-        *(f32x4*)(op + 4 * (orow + d)) = f32x4{o0, o1, o2, o3};
-      } else {
-        *(u32x2*)(op + 2 * (orow + d)) = u32x2{E::pack2(o0, o1), E::pack2(o2, o3)};
-      }
-    }
-  }
+  // O through LDS (one K / V buffer per wave, free once every wave is done)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint16_t* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+  static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
+  const int r0 = qt * TILE + 32 * wave;
+  store_rows<D, OUT_F32 ? 4 : 2>(acc, inv, stage, a.out,
+                                 (int64_t)b * a.os[0] + (int64_t)r0 * a.os[1] + (int64_t)h * a.os[2], a.os[1],
+                                 min(32, a.Lq - r0), lane, E::pack2);
 }
 
 // float32 forward (SIMT, no MFMA): 512 threads own the 128 queries of a map
