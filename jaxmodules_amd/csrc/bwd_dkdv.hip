@@ -51,9 +51,15 @@ void bwd_dkdv_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) float L0[BM], L1[BM];        // lse
   __shared__ __attribute__((aligned(16))) float G0[BM], G1[BM];        // delta
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
-  __shared__ __attribute__((aligned(16))) uint16_t Q0[BM * D], Q1[BM * D];
-  __shared__ __attribute__((aligned(16))) uint16_t H0[BM * D], H1[BM * D];
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE * D], Vs[TILE * D];
+  // per buffer: Q rows, then dO_h rows (BM * D elements each); K tile, then V_h tile
+  __shared__ __attribute__((aligned(16))) uint16_t QH0[2 * BM * D], QH1[2 * BM * D];
+  __shared__ __attribute__((aligned(16))) uint16_t KV[2 * TILE * D];
+  uint16_t* const Q0 = QH0;
+  uint16_t* const H0 = QH0 + BM * D;
+  uint16_t* const Q1 = QH1;
+  uint16_t* const H1 = QH1 + BM * D;
+  uint16_t* const Ks = KV;
+  uint16_t* const Vs = KV + TILE * D;
   __shared__ float VI[TILE];  // bfloat16 inputs: 1 / vs_k of the tile's keys
 
   const int item = a.kv_order[blockIdx.x];
@@ -210,15 +216,32 @@ void bwd_dkdv_mfma(KArgs a) {
     // the Q / dO_h seeds carry a bias of QB elements (taken off the array bases)
     const int rxo = opaque(rx), qro = opaque(qrow + QB), kro = opaque(krow_l);
     f32x16 st = f32x16{}, dp = f32x16{};
-#pragma unroll
-    for (int kd = 0; kd < NKD; ++kd) {
-      const int xo = (16 * kd) ^ rxo;
-      const u32x4 qa = *(const u32x4*)&Qb[qro + xo];
-      const u32x4 kb = *(const u32x4*)&Ks[kro + xo];
-      const u32x4 ha = *(const u32x4*)&Hb[qro + xo];
-      const u32x4 vb = *(const u32x4*)&Vs[kro + xo];
-      st = E::mfma(qa, kb, st);
-      dp = H::mfma(ha, vb, dp);
+    {
+      // S / dP pipelined by hand: the four operand reads of k-step kd + PD are
+      // issued before the MFMAs of k-step kd (dO_h sits BM * D elements after Q,
+      // V_h TILE * D after K: immediate offsets)
+      constexpr int PD = 1;
+      const uint32_t qa0 = lds_addr(BUF ? Q1 : Q0) + 2 * (uint32_t)qrow;
+      const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
+      u32x4 oq[PD + 1], ok[PD + 1], oh[PD + 1], ov[PD + 1];
+      auto rd = [&](auto kdc) {
+        constexpr int kd = decltype(kdc)::value, sl = kd % (PD + 1);
+        const uint32_t x = 2 * (uint32_t)((16 * kd) ^ rxo);
+        oq[sl] = ds_read128<0>(qa0 + x);
+        oh[sl] = ds_read128<2 * BM * D>(qa0 + x);
+        ok[sl] = ds_read128<0>(ka0 + x);
+        ov[sl] = ds_read128<2 * TILE * D>(ka0 + x);
+      };
+      static_for<PD>([&](auto i) { rd(i); });
+      static_for<NKD>([&](auto kdc) {
+        constexpr int kd = decltype(kdc)::value, sl = kd % (PD + 1);
+        if constexpr (kd + PD < NKD) rd(std::integral_constant<int, kd + PD>{});
+        constexpr int ahead = (kd + PD < NKD ? PD : NKD - 1 - kd) * 4;
+        lgkm_wait4<ahead>(oq[sl], ok[sl], oh[sl], ov[sl]);
+        st = E::mfma(oq[sl], ok[sl], st);
+        dp = H::mfma(oh[sl], ov[sl], dp);
+        asm volatile("" : "+v"(st), "+v"(dp));  // the MFMAs stay ahead of the next reads
+      });
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -247,19 +270,30 @@ void bwd_dkdv_mfma(KArgs a) {
       pk[r >> 3][(r & 7) >> 1] = H::pack2(st[r], st[r + 1]);
       sk[r >> 3][(r & 7) >> 1] = E::pack2(dp[r], dp[r + 1]);
     }
-    const int tzo = opaque(tz), t0 = opaque(tb0 + QB), t1 = opaque(tb1 + QB);
-#pragma unroll
-    for (int mt = 0; mt < NMD; ++mt) {
-      const int xm = (32 * mt) ^ tzo;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const u32x2 h0 = lds_read_tr(&Hb[t0 + xm + 16 * ks * D]);
-        const u32x2 h1 = lds_read_tr(&Hb[t1 + xm + 16 * ks * D]);
-        const u32x2 q0 = lds_read_tr(&Qb[t0 + xm + 16 * ks * D]);
-        const u32x2 q1 = lds_read_tr(&Qb[t1 + xm + 16 * ks * D]);
-        dv[mt] = H::mfma(u32x4{h0[0], h0[1], h1[0], h1[1]}, pk[ks], dv[mt]);
-        dk[mt] = E::mfma(u32x4{q0[0], q0[1], q1[0], q1[1]}, sk[ks], dk[mt]);
-      }
+    {
+      // dV^T / dK^T pipelined by hand like S / dP: step (mt, ks) reads four
+      // transposed 8-byte operands; those of the next step are issued first
+      const uint32_t qb0 = lds_addr(BUF ? Q1 : Q0);  // dO_h rows at +2 BM D bytes
+      const int tzo = opaque(tz);
+      const uint32_t a0 = qb0 + 2 * (uint32_t)tb0, a1 = qb0 + 2 * (uint32_t)tb1;
+      u32x2 rh0[2], rh1[2], rq0[2], rq1[2];
+      auto rd = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, mt = i / 2, ks = i % 2, sl = i % 2;
+        const uint32_t xm = 2 * (uint32_t)((32 * mt) ^ tzo);
+        rh0[sl] = ds_read_tr8<2 * BM * D + 32 * ks * D>(a0 + xm);
+        rh1[sl] = ds_read_tr8<2 * BM * D + 32 * ks * D>(a1 + xm);
+        rq0[sl] = ds_read_tr8<32 * ks * D>(a0 + xm);
+        rq1[sl] = ds_read_tr8<32 * ks * D>(a1 + xm);
+      };
+      rd(std::integral_constant<int, 0>{});
+      static_for<2 * NMD>([&](auto ic) {
+        constexpr int i = decltype(ic)::value, mt = i / 2, ks = i % 2, sl = i % 2;
+        if constexpr (i + 1 < 2 * NMD) rd(std::integral_constant<int, i + 1>{});
+        lgkm_wait4<i + 1 < 2 * NMD ? 4 : 0>(rh0[sl], rh1[sl], rq0[sl], rq1[sl]);
+        dv[mt] = H::mfma(u32x4{rh0[sl][0], rh0[sl][1], rh1[sl][0], rh1[sl][1]}, pk[ks], dv[mt]);
+        dk[mt] = E::mfma(u32x4{rq0[sl][0], rq0[sl][1], rq1[sl][0], rq1[sl][1]}, sk[ks], dk[mt]);
+        asm volatile("" : "+v"(dv[mt]), "+v"(dk[mt]));
+      });
     }
   };
 

@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <utility>
 
 #include "mattn.h"
 
@@ -337,6 +338,51 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc
     const u32x4 v = *(const u32x4*)(L + row * RB + ((c ^ (row & (CPR - 1))) << 4));
     if (row < nrows) *(u32x4*)((char*)out + (int64_t)ES * (row0 + (int64_t)row * rstride) + 16 * c) = v;
   }
+}
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16-byte LDS read issued where it stands (asm volatile keeps its order
+// against the other asm statements): hand-pipelined operand reads.  The
+// compiler does not count it in its own lgkmcnt waits (those stay correct: LDS
+// returns in order, so extra outstanding reads only lengthen them); the value
+// may be used only after lgkm_wait4 has covered it.
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16, lane mapping as lds_read_tr)
+// issued where it stands, like ds_read128.
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+// s_waitcnt lgkmcnt(N) that the four values pass through, so that nothing
+// using them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait4(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 
 // x, re-defined by an empty asm: values computed from the result inside a loop
