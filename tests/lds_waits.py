@@ -1,0 +1,77 @@
+"""Static check of compiled kernel assembly (gfx950): no instruction reads or
+overwrites the destination VGPRs of an LDS read before an ``s_waitcnt lgkmcnt``
+has covered that read.
+
+The dK/dV kernel issues its MFMA operand reads as inline-asm ``ds_read``
+instructions with hand-counted waits (the compiler does not track them), so
+the waits are checked on the code the compiler actually emitted.  LDS reads
+complete in order, so ``lgkmcnt(N)`` retires every LDS operation older than
+the N most recent ones.  The walk is linear within each basic block, every
+block must end with no LDS read outstanding, and an ``lgkmcnt(N > 0)`` wait
+while a scalar-memory load is outstanding (those complete out of order) is
+reported as well.
+"""
+from __future__ import annotations
+
+import re
+
+_REG = re.compile(r"v(\d+)$|v\[(\d+):(\d+)\]$")
+
+
+def _regs(tok: str) -> set:
+    m = _REG.fullmatch(tok)
+    if not m:
+        return set()
+    if m.group(1) is not None:
+        return {int(m.group(1))}
+    return set(range(int(m.group(2)), int(m.group(3)) + 1))
+
+
+def kernel_body(asm: str, name: str) -> list:
+    i = asm.index(name + ":")
+    j = asm.index(".Lfunc_end", i)
+    return asm[i:j].split("\n")
+
+
+def check(lines: list) -> tuple:
+    """(number of LDS reads seen, list of problem descriptions)."""
+    problems, reads = [], 0
+    pend = []  # outstanding lgkm operations, oldest first: (kind, dst regs, line)
+    for n, raw in enumerate(lines):
+        t = raw.split(";")[0].strip()
+        if not t:
+            continue
+        if t.endswith(":"):
+            if any(k == "lds" and d for k, d, _ in pend):
+                problems.append(f"LDS read outstanding at the end of the block before {t}")
+            pend = []
+            continue
+        if t.startswith("."):
+            continue
+        op = t.split()[0]
+        args = [a.strip().split()[0] for a in t[len(op):].split(",") if a.strip()]
+        if op == "s_waitcnt":
+            m = re.search(r"lgkmcnt\((\d+)\)", t)
+            if m or re.fullmatch(r"s_waitcnt\s+0", t):
+                lim = int(m.group(1)) if m else 0
+                if lim > 0 and any(k == "smem" for k, _, _ in pend):
+                    problems.append(f"line {n}: lgkmcnt({lim}) with a scalar load outstanding")
+                while len(pend) > lim:
+                    pend.pop(0)
+            continue
+        store = op.startswith(("ds_write", "global_store", "buffer_store", "scratch_store"))
+        has_dst = (op.startswith(("v_", "ds_read", "ds_bpermute", "global_load", "buffer_load", "scratch_load"))
+                   and not store and not op.startswith("v_cmp"))
+        dst = _regs(args[0]) if has_dst and args else set()
+        srcs = set()
+        for a in (args[1:] if has_dst else args):
+            srcs |= _regs(a)
+        for kind, d, ln in pend:
+            if kind == "lds" and d and (d & srcs or d & dst):
+                problems.append(f"line {n}: '{t}' touches the registers of the LDS read at line {ln}")
+        if op.startswith("ds_"):
+            pend.append(("lds", dst if (op.startswith("ds_read") or op.startswith("ds_bpermute")) else set(), n))
+            reads += op.startswith("ds_read")
+        elif op.startswith(("s_load", "s_buffer_load", "s_memtime", "s_memrealtime")):
+            pend.append(("smem", set(), n))
+    return reads, problems
