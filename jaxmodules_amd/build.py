@@ -23,7 +23,7 @@ SOURCES = ["fwd.hip", "bwd_pre.hip", "bwd_dq.hip", "bwd_dkdv.hip", "tilemap.hip"
 # reads ahead of the MFMA chains; each file uses the one measured fastest
 # without register spills for its kernels (bwd_dkdv.hip orders its operand reads
 # by hand and takes LLVM's default)
-SCHED = {"fwd.hip": "iterative-ilp"}
+SCHED = {"fwd.hip": "iterative-ilp", "bwd_dq.hip": "iterative-ilp"}
 ARCH = "gfx950"
 
 

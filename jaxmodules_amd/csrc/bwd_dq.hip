@@ -128,23 +128,39 @@ void bwd_dq_mfma(KArgs a) {
   // its two dQ k-steps before the next half starts (halves the live state).
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* Kb = BUF ? KV1 : KV0;
-    const uint16_t* Vb = Kb + BN * D;
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
-    // seeds re-defined here, so the addresses derived from them stay per use
-    const int rxo = opaque(rx), rro = opaque(rrow);
-    const int tzo = opaque(tz), t0 = opaque(tb0), t1 = opaque(tb1);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    // operand reads pipelined by hand (asm LDS reads issued PS / PQ k-steps
+    // ahead of their MFMAs, counted lgkmcnt waits); the V tile sits BN * D
+    // elements after K and key half t 32 t D elements in: immediate offsets
+    constexpr int PS = 1, PQ = 2;
+    const uint32_t kb = lds_addr(BUF ? KV1 : KV0);
+    const int rxo = opaque(rx), tzo = opaque(tz);
+    const uint32_t ra = kb + 2 * (uint32_t)opaque(rrow);
+    const uint32_t a0 = kb + 2 * (uint32_t)opaque(tb0), a1 = kb + 2 * (uint32_t)opaque(tb1);
+    // Each 32-key half t of the sub-block is carried through S^T, dP^T, dS^T and
+    // its two dQ k-steps before the next half starts (halves the live state).
+    static_for<2>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
       f32x16 st = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) {
-        const int xo = (16 * kd) ^ rxo;
-        const u32x4 ka = *(const u32x4*)&Kb[rro + xo + 32 * t * D];
-        const u32x4 va = *(const u32x4*)&Vb[rro + xo + 32 * t * D];
-        st = E::mfma(ka, qf[kd], st);
-        dp = E::mfma(va, df[kd], dp);
-      }
+      u32x4 ka[PS + 1], va[PS + 1];
+      auto rd = [&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PS + 1);
+        const uint32_t x = ra + 2 * (uint32_t)((16 * kd) ^ rxo);
+        ka[sl] = ds_read128<64 * t * D>(x);
+        va[sl] = ds_read128<2 * BN * D + 64 * t * D>(x);
+      };
+      static_for<PS>(rd);
+      static_for<NKD>([&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PS + 1);
+        if constexpr (kd + PS < NKD) rd(std::integral_constant<int, kd + PS>{});
+        lgkm_wait<2 * (kd + PS < NKD ? PS : NKD - 1 - kd)>();
+        hold(ka[sl]);
+        hold(va[sl]);
+        st = E::mfma(ka[sl], qf[kd], st);
+        dp = E::mfma(va[sl], df[kd], dp);
+        hold(st);
+        hold(dp);
+      });
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], c2, nlse));
       if (masked) {
@@ -160,19 +176,27 @@ void bwd_dq_mfma(KArgs a) {
         const float d1 = st[r + 1] * fmaf(dp[r + 1], dps, -dl);
         pk[r >> 3][(r & 7) >> 1] = E::pack2(d0, d1);
       }
-#pragma unroll
-      for (int mt = 0; mt < NMD; ++mt) {
-        const int xm = (32 * mt) ^ tzo;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int ks = 2 * t + kk;
-          const u32x2 lo = lds_read_tr(&Kb[t0 + xm + 16 * ks * D]);
-          const u32x2 up = lds_read_tr(&Kb[t1 + xm + 16 * ks * D]);
-          acc[mt] = E::mfma(u32x4{lo[0], lo[1], up[0], up[1]}, pk[kk], acc[mt]);
-        }
-      }
-    }
+      // dQ^T += K^T dS^T over the half's two k-steps, K^T by transposed reads
+      u32x2 lo[PQ + 1], up[PQ + 1];
+      auto rq = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, mt = i / 2, ks = 2 * t + i % 2, sl = i % (PQ + 1);
+        const uint32_t xm = 2 * (uint32_t)((32 * mt) ^ tzo);
+        lo[sl] = ds_read_tr8<32 * ks * D>(a0 + xm);
+        up[sl] = ds_read_tr8<32 * ks * D>(a1 + xm);
+      };
+      static_for<PQ>(rq);
+      static_for<2 * NMD>([&](auto ic) {
+        constexpr int i = decltype(ic)::value, mt = i / 2, kk = i % 2, sl = i % (PQ + 1);
+        if constexpr (i + PQ < 2 * NMD) rq(std::integral_constant<int, i + PQ>{});
+        lgkm_wait<2 * (i + PQ < 2 * NMD ? PQ : 2 * NMD - 1 - i)>();
+        hold(lo[sl]);
+        hold(up[sl]);
+        acc[mt] = E::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[kk], acc[mt]);
+        hold(acc[mt]);
+      });
+    });
   };
+
 
   auto iter = [&](int s, auto bufc) {
     __builtin_amdgcn_s_waitcnt(0);

@@ -378,6 +378,18 @@ template <int N>
 __device__ __forceinline__ void lgkm_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
+// s_waitcnt lgkmcnt(N) in the asm order; values read by ds_read128 /
+// ds_read_tr8 before it are passed through hold() after it, so that nothing
+// using them is scheduled ahead of the wait.  hold() also pins an MFMA result
+// between two asm statements (the MFMA is then issued where it stands).
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+template <class T>
+__device__ __forceinline__ void hold(T& x) {
+  asm volatile("" : "+v"(x));
+}
 // s_waitcnt lgkmcnt(N) that the four values pass through, so that nothing
 // using them is scheduled before it.
 template <int N>

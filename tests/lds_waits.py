@@ -2,14 +2,16 @@
 overwrites the destination VGPRs of an LDS read before an ``s_waitcnt lgkmcnt``
 has covered that read.
 
-The dK/dV kernel issues its MFMA operand reads as inline-asm ``ds_read``
-instructions with hand-counted waits (the compiler does not track them), so
+The dK/dV and dQ kernels issue their MFMA operand reads as inline-asm
+``ds_read`` instructions with hand-counted waits (the compiler does not track them), so
 the waits are checked on the code the compiler actually emitted.  LDS reads
 complete in order, so ``lgkmcnt(N)`` retires every LDS operation older than
-the N most recent ones.  The walk is linear within each basic block, every
-block must end with no LDS read outstanding, and an ``lgkmcnt(N > 0)`` wait
-while a scalar-memory load is outstanding (those complete out of order) is
-reported as well.
+the N most recent ones.  The walk is linear within each basic block; no read
+issued from inline asm may be outstanding at the end of a block (the
+compiler's own reads are tracked by the compiler across blocks; forgetting
+them at a label only makes this check stricter, since older operations
+retire first).  An ``lgkmcnt(N > 0)`` wait while a scalar-memory load is
+outstanding (those complete out of order) is reported as well.
 """
 from __future__ import annotations
 
@@ -37,13 +39,18 @@ def check(lines: list) -> tuple:
     """(number of LDS reads seen, list of problem descriptions)."""
     problems, reads = [], 0
     pend = []  # outstanding lgkm operations, oldest first: (kind, dst regs, line)
+    in_asm = False
     for n, raw in enumerate(lines):
+        if ";;#ASMSTART" in raw:
+            in_asm = True
+        elif ";;#ASMEND" in raw:
+            in_asm = False
         t = raw.split(";")[0].strip()
         if not t:
             continue
         if t.endswith(":"):
-            if any(k == "lds" and d for k, d, _ in pend):
-                problems.append(f"LDS read outstanding at the end of the block before {t}")
+            if any(k == "asm" for k, _, _ in pend):
+                problems.append(f"asm LDS read outstanding at the end of the block before {t}")
             pend = []
             continue
         if t.startswith("."):
@@ -67,10 +74,11 @@ def check(lines: list) -> tuple:
         for a in (args[1:] if has_dst else args):
             srcs |= _regs(a)
         for kind, d, ln in pend:
-            if kind == "lds" and d and (d & srcs or d & dst):
+            if kind in ("lds", "asm") and d and (d & srcs or d & dst):
                 problems.append(f"line {n}: '{t}' touches the registers of the LDS read at line {ln}")
         if op.startswith("ds_"):
-            pend.append(("lds", dst if (op.startswith("ds_read") or op.startswith("ds_bpermute")) else set(), n))
+            kind = "asm" if in_asm else "lds"
+            pend.append((kind, dst if (op.startswith("ds_read") or op.startswith("ds_bpermute")) else set(), n))
             reads += op.startswith("ds_read")
         elif op.startswith(("s_load", "s_buffer_load", "s_memtime", "s_memrealtime")):
             pend.append(("smem", set(), n))

@@ -1,5 +1,5 @@
-"""The hand-counted LDS waits of the dK/dV kernel, checked on its compiled
-gfx950 assembly (no GPU needed: hipcc cross-compiles here)."""
+"""The hand-counted LDS waits of the dK/dV and dQ kernels, checked on their
+compiled gfx950 assembly (no GPU needed: hipcc cross-compiles here)."""
 import os
 import re
 import shutil
@@ -14,26 +14,38 @@ pytestmark = pytest.mark.skipif(not (shutil.which("hipcc") or os.path.exists("/o
                                 reason="hipcc not available")
 
 
-@pytest.fixture(scope="module")
-def dkdv_asm(tmp_path_factory):
-    src = os.path.join(B.CSRC, "bwd_dkdv.hip")
-    out = str(tmp_path_factory.mktemp("asm") / "bwd_dkdv.s")
-    sched = B.SCHED.get("bwd_dkdv.hip")
+def _asm(src_name, tmp_path_factory):
+    """The source compiled to gfx950 assembly with the library's own flags."""
+    src = os.path.join(B.CSRC, src_name)
+    out = str(tmp_path_factory.mktemp("asm") / (src_name + ".s"))
+    sched = B.SCHED.get(src_name)
     flags = B.common_flags() + (["-mllvm", f"-amdgpu-sched-strategy={sched}"] if sched else [])
     B._run([B.hipcc(), *flags, "--cuda-device-only", "-S", src, "-o", out])
     return open(out).read()
 
 
-def _kernels(asm):
-    return sorted(set(re.findall(r"^(_ZN5mattn13bwd_dkdv_mfma\w+):", asm, re.M)))
+@pytest.fixture(scope="module")
+def dkdv_asm(tmp_path_factory):
+    return _asm("bwd_dkdv.hip", tmp_path_factory)
 
 
-def test_every_dkdv_instantiation_waits_before_use(dkdv_asm):
-    names = _kernels(dkdv_asm)
+@pytest.fixture(scope="module")
+def dq_asm(tmp_path_factory):
+    return _asm("bwd_dq.hip", tmp_path_factory)
+
+
+def _kernels(asm, stem="13bwd_dkdv_mfma"):
+    return sorted(set(re.findall(rf"^(_ZN5mattn{stem}\w+):", asm, re.M)))
+
+
+@pytest.mark.parametrize("which", ["dkdv", "dq"])
+def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm):
+    asm, stem, least = (dkdv_asm, "13bwd_dkdv_mfma", 100) if which == "dkdv" else (dq_asm, "11bwd_dq_mfma", 60)
+    names = _kernels(asm, stem)
     assert len(names) == 4, names          # D = 64 / 128 x bfloat16 / float16
     for name in names:
-        reads, problems = lds_waits.check(lds_waits.kernel_body(dkdv_asm, name))
-        assert reads > 100, (name, reads)
+        reads, problems = lds_waits.check(lds_waits.kernel_body(asm, name))
+        assert reads > least, (name, reads)
         assert not problems, (name, problems[:5])
 
 
