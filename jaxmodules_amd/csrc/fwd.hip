@@ -32,10 +32,9 @@ void fwd_mfma(KArgs a) {
   // (base-2 units); until then P may reach 2^8, harmless in 16-bit and fp32.
   constexpr float RESCALE_SLACK = 8.f;
 
-  // one array per buffer: the compiler then knows the loads landing in one
-  // buffer cannot alias the operand reads of the other (no vmcnt waits mid-step)
-  __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t V0[BN * D], V1[BN * D];
+  // one array per buffer (K rows, then V rows): the compiler then knows the
+  // loads landing in one buffer cannot alias the reads of the other
+  __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
 
   const int item = a.q_order[blockIdx.x];
@@ -72,15 +71,13 @@ void fwd_mfma(KArgs a) {
     kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
     vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
   }
-  int kro[NKD];               // K row-read offsets (A operand of S^T), row tile 0
-#pragma unroll
-  for (int kd = 0; kd < NKD; ++kd) kro[kd] = sw_off<D>(l32, 2 * kd + hi);
-  int vto[NMD][2];            // V transposed-read offsets (A operand of O^T), k-step 0
-#pragma unroll
-  for (int mt = 0; mt < NMD; ++mt) {
-    vto[mt][0] = tr_src<D>(lane, mt, 0);
-    vto[mt][1] = tr_src<D>(lane, mt, 1);
-  }
+  // LDS operand addresses, formed per use from lane seeds (element offsets):
+  //   K row read, chunk 2 kd + hi of row r:  r D + ((16 kd) ^ rx),  rx = 8 hi ^ 8 swz(r)
+  //   V transposed read (mt, sec):           tb[sec] + ((32 mt) ^ tz)
+  const int rx = (8 * hi) ^ (swz<D>(l32) << 3);
+  const int tz = 32 * (swz<D>(4 * hi + ((lane & 15) >> 2)) >> 2);
+  const int tb0 = tr_src<D>(lane, 0, 0) - tz;
+  const int tb1 = tr_src<D>(lane, 0, 1) - tz;
 
   const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);  // this wave's load block
   EntryCache ec;
@@ -89,8 +86,8 @@ void fwd_mfma(KArgs a) {
     int kt, mask;
     ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
     const int key0 = kt * TILE + (s & 1) * BN;
-    uint16_t* kl = (BUF ? K1 : K0) + wofs;
-    uint16_t* vl = (BUF ? V1 : V0) + wofs;
+    uint16_t* kl = (BUF ? KV1 : KV0) + wofs;
+    uint16_t* vl = (BUF ? KV1 : KV0) + BN * D + wofs;
     if (mask >= 0) {  // this wave's 32 mask words (256 bytes), one dword per lane
       const uint32_t* src = (const uint32_t*)(a.row_bits + ((int64_t)mask * 2 + (s & 1)) * TILE + wave * 32);
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
@@ -122,18 +119,34 @@ void fwd_mfma(KArgs a) {
 
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* Kb = BUF ? K1 : K0;
-    const uint16_t* Vb = BUF ? V1 : V0;
-    // S^T = K Q^T, one row tile's K operands staged ahead of its MFMA chain
-    f32x16 st[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      u32x4 ka[NKD];
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) ka[kd] = *(const u32x4*)&Kb[kro[kd] + 32 * t * D];
-      st[t] = f32x16{};
-#pragma unroll
-      for (int kd = 0; kd < NKD; ++kd) st[t] = E::mfma(ka[kd], qf[kd], st[t]);
+    // operand reads pipelined by hand (asm LDS reads issued PS / PV steps ahead
+    // of their MFMAs, counted lgkmcnt waits); V sits BN * D elements after K
+    constexpr int PS = 3, PV = 4;
+    const uint32_t kvb = lds_addr(BUF ? KV1 : KV0);
+    const int rxo = opaque(rx), tzo = opaque(tz);
+    const uint32_t ra = kvb + 2 * (uint32_t)opaque(l32 * D);
+    // S^T = K Q^T: k-step kd reads the K rows of both 32-key halves
+    f32x16 st[2] = {f32x16{}, f32x16{}};
+    {
+      u32x4 k0[PS + 1], k1[PS + 1];
+      auto rd = [&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PS + 1);
+        const uint32_t x = ra + 2 * (uint32_t)((16 * kd) ^ rxo);
+        k0[sl] = ds_read128<0>(x);
+        k1[sl] = ds_read128<64 * D>(x);
+      };
+      static_for<PS>(rd);
+      static_for<NKD>([&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PS + 1);
+        if constexpr (kd + PS < NKD) rd(std::integral_constant<int, kd + PS>{});
+        lgkm_wait<2 * (kd + PS < NKD ? PS : NKD - 1 - kd)>();
+        hold(k0[sl]);
+        hold(k1[sl]);
+        st[0] = E::mfma(k0[sl], qf[kd], st[0]);
+        st[1] = E::mfma(k1[sl], qf[kd], st[1]);
+        hold(st[0]);
+        hold(st[1]);
+      });
     }
     if (masked) {
       const uint64_t mw = (BUF ? M1 : M0)[qloc];
@@ -171,18 +184,27 @@ void fwd_mfma(KArgs a) {
         pk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(p0, p1);
       }
     }
-    // O^T += V^T P^T, V^T operands by transposed reads of the row-major V tile
-#pragma unroll
-    for (int mt = 0; mt < NMD; ++mt) {
-      u32x4 va[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x2 lo = lds_read_tr(&Vb[vto[mt][0] + 16 * ks * D]);
-        const u32x2 up = lds_read_tr(&Vb[vto[mt][1] + 16 * ks * D]);
-        va[ks] = u32x4{lo[0], lo[1], up[0], up[1]};
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc[mt] = E::mfma(va[ks], pk[ks], acc[mt]);
+    // O^T += V^T P^T, V^T operands by transposed reads of the row-major V tile;
+    // step (ks, mt) feeds accumulator mt, four independent chains
+    {
+      const uint32_t a0 = kvb + 2 * (uint32_t)opaque(tb0), a1 = kvb + 2 * (uint32_t)opaque(tb1);
+      u32x2 lo[PV + 1], up[PV + 1];
+      auto rv = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PV + 1);
+        const uint32_t xm = 2 * (uint32_t)((32 * mt) ^ tzo);
+        lo[sl] = ds_read_tr8<2 * BN * D + 32 * ks * D>(a0 + xm);
+        up[sl] = ds_read_tr8<2 * BN * D + 32 * ks * D>(a1 + xm);
+      };
+      static_for<PV>(rv);
+      static_for<4 * NMD>([&](auto ic) {
+        constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PV + 1);
+        if constexpr (i + PV < 4 * NMD) rv(std::integral_constant<int, i + PV>{});
+        lgkm_wait<2 * (i + PV < 4 * NMD ? PV : 4 * NMD - 1 - i)>();
+        hold(lo[sl]);
+        hold(up[sl]);
+        acc[mt] = E::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[ks], acc[mt]);
+        hold(acc[mt]);
+      });
     }
   };
 
@@ -209,7 +231,7 @@ void fwd_mfma(KArgs a) {
   // O through LDS (one K / V buffer per wave, free once every wave is done)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  uint16_t* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+  uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * BN * D;
   static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
   const int r0 = qt * TILE + 32 * wave;
   store_rows<D, OUT_F32 ? 4 : 2>(acc, inv, stage, a.out,

@@ -2,8 +2,8 @@
 overwrites the destination VGPRs of an LDS read before an ``s_waitcnt lgkmcnt``
 has covered that read.
 
-The dK/dV and dQ kernels issue their MFMA operand reads as inline-asm
-``ds_read`` instructions with hand-counted waits (the compiler does not track them), so
+The forward, dK/dV and dQ kernels issue their MFMA operand reads as
+inline-asm ``ds_read`` instructions with hand-counted waits (the compiler does not track them), so
 the waits are checked on the code the compiler actually emitted.  LDS reads
 complete in order, so ``lgkmcnt(N)`` retires every LDS operation older than
 the N most recent ones.  The walk is linear within each basic block; no read

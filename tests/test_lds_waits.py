@@ -1,5 +1,5 @@
-"""The hand-counted LDS waits of the dK/dV and dQ kernels, checked on their
-compiled gfx950 assembly (no GPU needed: hipcc cross-compiles here)."""
+"""The hand-counted LDS waits of the forward, dK/dV and dQ kernels, checked on
+their compiled gfx950 assembly (no GPU needed: hipcc cross-compiles here)."""
 import os
 import re
 import shutil
@@ -34,15 +34,24 @@ def dq_asm(tmp_path_factory):
     return _asm("bwd_dq.hip", tmp_path_factory)
 
 
+@pytest.fixture(scope="module")
+def fwd_asm(tmp_path_factory):
+    return _asm("fwd.hip", tmp_path_factory)
+
+
 def _kernels(asm, stem="13bwd_dkdv_mfma"):
     return sorted(set(re.findall(rf"^(_ZN5mattn{stem}\w+):", asm, re.M)))
 
 
-@pytest.mark.parametrize("which", ["dkdv", "dq"])
-def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm):
-    asm, stem, least = (dkdv_asm, "13bwd_dkdv_mfma", 100) if which == "dkdv" else (dq_asm, "11bwd_dq_mfma", 60)
+@pytest.mark.parametrize("which", ["dkdv", "dq", "fwd"])
+def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm, fwd_asm):
+    asm, stem, least, count = {
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 100, 4),   # D = 64 / 128 x bfloat16 / float16
+        "dq": (dq_asm, "11bwd_dq_mfma", 60, 4),
+        "fwd": (fwd_asm, "8fwd_mfma", 50, 8),            # ... x float32 / 16-bit output
+    }[which]
     names = _kernels(asm, stem)
-    assert len(names) == 4, names          # D = 64 / 128 x bfloat16 / float16
+    assert len(names) == count, names
     for name in names:
         reads, problems = lds_waits.check(lds_waits.kernel_body(asm, name))
         assert reads > least, (name, reads)
