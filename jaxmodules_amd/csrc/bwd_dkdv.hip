@@ -21,8 +21,11 @@ namespace mattn {
 //   dK^T += Q^T dS        (A: transposed reads of the Q tile)
 // The K and V_h tiles of the workgroup's 128 keys stay in LDS for the whole
 // column; Q, dO_h, lse, delta and the partial-tile mask words are
-// double-buffered and filled by direct global->LDS loads.  The two query
-// halves' dK/dV partials of a key are summed through LDS at the end.
+// double-buffered and filled by direct global->LDS loads.  The MFMA operand
+// reads are pipelined by hand: asm LDS reads issued one k-step ahead of their
+// MFMAs, with counted lgkmcnt waits.  The two query halves' dK/dV partials of
+// a key are summed through LDS at the end, and the rows leave through an
+// LDS-staged tile, 16 bytes per lane along each row.
 // V_h is V itself for float16 inputs (vs_k = 1); for bfloat16 inputs the
 // prologue converts the column's V rows to float16, each scaled by vs_k.
 template <int D, class Tag>
@@ -37,14 +40,6 @@ void bwd_dkdv_mfma(KArgs a) {
   constexpr int NMD = D / 32;
   constexpr int BLK = 512;            // elements one load instruction fills
   constexpr int NS = BM * D / BLK / 8;  // load slots per wave for a 64-row tile
-  constexpr int NW = 8;
-  // The Q / dO_h buffers lie above the K and V tiles, 64 KiB up at D = 128: a
-  // ds_read immediate (16 bits) cannot reach them from an LDS offset near 0, so
-  // their per-lane seeds carry +64 KiB (QB elements) and the operand reads use
-  // array bases lowered by as much -- the array address minus 64 KiB is then
-  // the immediate, and no add per read is needed (any placement stays correct;
-  // only this one is fast).
-  constexpr int QB = D == 128 ? 32768 : 0;
 
   // one array per buffer: the compiler then knows the loads landing in one
   // buffer cannot alias the operand reads of the other (no vmcnt waits mid-step)
@@ -72,8 +67,6 @@ void bwd_dkdv_mfma(KArgs a) {
   const int l32 = lane & 31, hi = lane >> 5;
   const int kg = wave & 3, qh = wave >> 2;
   const int kloc = 32 * kg + l32;
-  const int key = kt * TILE + kloc;
-  const int kcl = min(key, a.Lk - 1);
   const float c2 = a.scale_log2;
   const float inv_s = a.dscale[1];
   // dP = (dO_h V_h^T) / (s vs_k): one factor per lane, since a lane owns one key
@@ -208,13 +201,10 @@ void bwd_dkdv_mfma(KArgs a) {
 
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* Qb = (BUF ? Q1 : Q0) - QB;   // indexed with the biased seeds below
-    const uint16_t* Hb = (BUF ? H1 : H0) - QB;
     const float* Lb = (BUF ? L1 : L0) + 32 * qh;
     const float* Gb = (BUF ? G1 : G0) + 32 * qh;
     // seeds re-defined here, so the addresses derived from them stay per use;
-    // the Q / dO_h seeds carry a bias of QB elements (taken off the array bases)
-    const int rxo = opaque(rx), qro = opaque(qrow + QB), kro = opaque(krow_l);
+    const int rxo = opaque(rx);
     f32x16 st = f32x16{}, dp = f32x16{};
     {
       // S / dP pipelined by hand: the four operand reads of k-step kd + PD are
