@@ -337,7 +337,7 @@ void bwd_dkdv_mfma(KArgs a) {
 
   // dK / dV: the second query half's partials join the first's through LDS
   // (wave kg + 4 -> wave kg; per key group a dK slab in the K / V tiles and a
-  // dV slab in a Q / dO_h buffer, all free now; lane-major floats).  Wave kg
+  // dV slab in a Q / dO_h buffer, all free now; lane-major 16-byte chunks).  Wave kg
   // then writes the finished rows of its 32 keys, scaled and rounded, over its
   // own slabs as [32 keys][D + 8] tiles, and all 8 waves store the 128 x D
   // tiles with 16-byte accesses along the rows.
@@ -349,13 +349,14 @@ void bwd_dkdv_mfma(KArgs a) {
                 "reduction slabs");
   float* redk = (float*)(kg < 2 ? Ks : Vs) + (kg & 1) * SLAB;
   float* redv = (float*)(kg == 0 ? Q0 : kg == 1 ? Q1 : kg == 2 ? H0 : H1);
+  // slab layout: float j of lane-chunk (mt, c) at ((mt * 4 + c) * 64 + lane) * 4 + j
   if (qh == 1) {
 #pragma unroll
     for (int mt = 0; mt < NMD; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        redk[(mt * 16 + r) * 64 + lane] = dk[mt][r];
-        redv[(mt * 16 + r) * 64 + lane] = dv[mt][r];
+      for (int c = 0; c < 4; ++c) {
+        ((f32x4*)redk)[(mt * 4 + c) * 64 + lane] = f32x4{dk[mt][4 * c], dk[mt][4 * c + 1], dk[mt][4 * c + 2], dk[mt][4 * c + 3]};
+        ((f32x4*)redv)[(mt * 4 + c) * 64 + lane] = f32x4{dv[mt][4 * c], dv[mt][4 * c + 1], dv[mt][4 * c + 2], dv[mt][4 * c + 3]};
       }
   }
   __syncthreads();
@@ -365,7 +366,11 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
       for (int mt = 0; mt < NMD; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mt][r] += red[(mt * 16 + r) * 64 + lane];
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 x = ((const f32x4*)red)[(mt * 4 + c) * 64 + lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[mt][4 * c + j] += x[j];
+        }
       uint16_t* o = (uint16_t*)red + l32 * OR;
 #pragma unroll
       for (int mt = 0; mt < NMD; ++mt) {
