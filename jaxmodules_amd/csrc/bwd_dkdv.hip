@@ -22,8 +22,9 @@ namespace mattn {
 // The K and V_h tiles of the workgroup's 128 keys stay in LDS for the whole
 // column; Q, dO_h, lse, delta and the partial-tile mask words are
 // double-buffered and filled by direct global->LDS loads.  The MFMA operand
-// reads are pipelined by hand: asm LDS reads issued one k-step ahead of their
-// MFMAs, with counted lgkmcnt waits.  The two query halves' dK/dV partials of
+// reads are pipelined by hand: asm LDS reads issued two k-steps ahead of their
+// MFMAs, with counted lgkmcnt waits; bfloat16 and float16 MFMAs are grouped
+// by type.  The two query halves' dK/dV partials of
 // a key are summed through LDS at the end, and the rows leave through an
 // LDS-staged tile, 16 bytes per lane along each row.
 // V_h is V itself for float16 inputs (vs_k = 1); for bfloat16 inputs the
@@ -207,30 +208,34 @@ void bwd_dkdv_mfma(KArgs a) {
     const int rxo = opaque(rx);
     f32x16 st = f32x16{}, dp = f32x16{};
     {
-      // S / dP pipelined by hand: the four operand reads of k-step kd + PD are
-      // issued before the MFMAs of k-step kd (dO_h sits BM * D elements after Q,
-      // V_h TILE * D after K: immediate offsets)
-      constexpr int PD = 1;
+      // S / dP pipelined by hand: the eight bfloat16 S MFMAs, then the eight
+      // float16 dP MFMAs (one switch of MFMA type, which costs issue cycles);
+      // step i reads its two 16-byte operands PS steps ahead (dO_h sits BM * D
+      // elements after Q, V_h TILE * D after K: immediate offsets)
+      constexpr int PS = 2;
       const uint32_t qa0 = lds_addr(BUF ? Q1 : Q0) + 2 * (uint32_t)qrow;
       const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
-      u32x4 oq[PD + 1], ok[PD + 1], oh[PD + 1], ov[PD + 1];
-      auto rd = [&](auto kdc) {
-        constexpr int kd = decltype(kdc)::value, sl = kd % (PD + 1);
+      u32x4 oa[PS + 1], ob[PS + 1];
+      auto rd = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, kd = i % NKD, isdp = i / NKD, sl = i % (PS + 1);
         const uint32_t x = 2 * (uint32_t)((16 * kd) ^ rxo);
-        oq[sl] = ds_read128<0>(qa0 + x);
-        oh[sl] = ds_read128<2 * BM * D>(qa0 + x);
-        ok[sl] = ds_read128<0>(ka0 + x);
-        ov[sl] = ds_read128<2 * TILE * D>(ka0 + x);
+        oa[sl] = ds_read128<isdp ? 2 * BM * D : 0>(qa0 + x);
+        ob[sl] = ds_read128<isdp ? 2 * TILE * D : 0>(ka0 + x);
       };
-      static_for<PD>([&](auto i) { rd(i); });
-      static_for<NKD>([&](auto kdc) {
-        constexpr int kd = decltype(kdc)::value, sl = kd % (PD + 1);
-        if constexpr (kd + PD < NKD) rd(std::integral_constant<int, kd + PD>{});
-        constexpr int ahead = (kd + PD < NKD ? PD : NKD - 1 - kd) * 4;
-        lgkm_wait4<ahead>(oq[sl], ok[sl], oh[sl], ov[sl]);
-        st = E::mfma(oq[sl], ok[sl], st);
-        dp = H::mfma(oh[sl], ov[sl], dp);
-        asm volatile("" : "+v"(st), "+v"(dp));  // the MFMAs stay ahead of the next reads
+      static_for<PS>(rd);
+      static_for<2 * NKD>([&](auto ic) {
+        constexpr int i = decltype(ic)::value, isdp = i / NKD, sl = i % (PS + 1);
+        if constexpr (i + PS < 2 * NKD) rd(std::integral_constant<int, i + PS>{});
+        lgkm_wait<2 * (i + PS < 2 * NKD ? PS : 2 * NKD - 1 - i)>();
+        hold(oa[sl]);
+        hold(ob[sl]);
+        if constexpr (isdp) {
+          dp = H::mfma(oa[sl], ob[sl], dp);
+          hold(dp);
+        } else {
+          st = E::mfma(oa[sl], ob[sl], st);
+          hold(st);
+        }
       });
     }
 #pragma unroll
@@ -261,28 +266,47 @@ void bwd_dkdv_mfma(KArgs a) {
       sk[r >> 3][(r & 7) >> 1] = E::pack2(dp[r], dp[r + 1]);
     }
     {
-      // dV^T / dK^T pipelined by hand like S / dP: step (mt, ks) reads four
-      // transposed 8-byte operands; those of the next step are issued first
+      // dV^T / dK^T pipelined by hand like S / dP.  Per 16-query k-step ks, the
+      // four float16 dV MFMAs (one per 32-row d tile mt), then the four bfloat16
+      // dK MFMAs: switching between the two MFMA types costs issue cycles, so
+      // each type runs four at a time (and an accumulator recurs 8 MFMAs later).
+      // Step i reads the two transposed 8-byte halves of its A operand, issued
+      // PT steps ahead.
+      constexpr int PT = 2;
       const uint32_t qb0 = lds_addr(BUF ? Q1 : Q0);  // dO_h rows at +2 BM D bytes
       const int tzo = opaque(tz);
-      const uint32_t a0 = qb0 + 2 * (uint32_t)tb0, a1 = qb0 + 2 * (uint32_t)tb1;
-      u32x2 rh0[2], rh1[2], rq0[2], rq1[2];
-      auto rd = [&](auto ic) {
-        constexpr int i = decltype(ic)::value, mt = i / 2, ks = i % 2, sl = i % 2;
+      uint32_t am0[NMD], am1[NMD];
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt) {
         const uint32_t xm = 2 * (uint32_t)((32 * mt) ^ tzo);
-        rh0[sl] = ds_read_tr8<2 * BM * D + 32 * ks * D>(a0 + xm);
-        rh1[sl] = ds_read_tr8<2 * BM * D + 32 * ks * D>(a1 + xm);
-        rq0[sl] = ds_read_tr8<32 * ks * D>(a0 + xm);
-        rq1[sl] = ds_read_tr8<32 * ks * D>(a1 + xm);
+        am0[mt] = qb0 + 2 * (uint32_t)tb0 + xm;
+        am1[mt] = qb0 + 2 * (uint32_t)tb1 + xm;
+      }
+      constexpr int NSTEP = 4 * NMD;  // (ks, product, mt)
+      u32x2 lo[PT + 1], up[PT + 1];
+      auto rd = [&](auto ic) {
+        constexpr int i = decltype(ic)::value, ks = i / (2 * NMD), isdv = (i / NMD) % 2 == 0, mt = i % NMD;
+        constexpr int sl = i % (PT + 1);
+        constexpr int off = (isdv ? 2 * BM * D : 0) + 32 * ks * D;
+        lo[sl] = ds_read_tr8<off>(am0[mt]);
+        up[sl] = ds_read_tr8<off>(am1[mt]);
       };
-      rd(std::integral_constant<int, 0>{});
-      static_for<2 * NMD>([&](auto ic) {
-        constexpr int i = decltype(ic)::value, mt = i / 2, ks = i % 2, sl = i % 2;
-        if constexpr (i + 1 < 2 * NMD) rd(std::integral_constant<int, i + 1>{});
-        lgkm_wait4<i + 1 < 2 * NMD ? 4 : 0>(rh0[sl], rh1[sl], rq0[sl], rq1[sl]);
-        dv[mt] = H::mfma(u32x4{rh0[sl][0], rh0[sl][1], rh1[sl][0], rh1[sl][1]}, pk[ks], dv[mt]);
-        dk[mt] = E::mfma(u32x4{rq0[sl][0], rq0[sl][1], rq1[sl][0], rq1[sl][1]}, sk[ks], dk[mt]);
-        asm volatile("" : "+v"(dv[mt]), "+v"(dk[mt]));
+      static_for<PT>(rd);
+      static_for<NSTEP>([&](auto ic) {
+        constexpr int i = decltype(ic)::value, ks = i / (2 * NMD), isdv = (i / NMD) % 2 == 0, mt = i % NMD;
+        constexpr int sl = i % (PT + 1);
+        if constexpr (i + PT < NSTEP) rd(std::integral_constant<int, i + PT>{});
+        lgkm_wait<2 * (i + PT < NSTEP ? PT : NSTEP - 1 - i)>();
+        hold(lo[sl]);
+        hold(up[sl]);
+        const u32x4 aop = u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]};
+        if constexpr (isdv) {
+          dv[mt] = H::mfma(aop, pk[ks], dv[mt]);
+          hold(dv[mt]);
+        } else {
+          dk[mt] = E::mfma(aop, sk[ks], dk[mt]);
+          hold(dk[mt]);
+        }
       });
     }
   };

@@ -359,7 +359,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // against the other asm statements): hand-pipelined operand reads.  The
 // compiler does not count it in its own lgkmcnt waits (those stay correct: LDS
 // returns in order, so extra outstanding reads only lengthen them); the value
-// may be used only after lgkm_wait4 has covered it.
+// may be used only after an lgkm_wait that covers it, passed through hold().
 template <int OFF>
 __device__ __forceinline__ u32x4 ds_read128(uint32_t addr) {
   u32x4 v;
@@ -374,10 +374,6 @@ __device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return v;
 }
-template <int N>
-__device__ __forceinline__ void lgkm_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
-}
 // s_waitcnt lgkmcnt(N) in the asm order; values read by ds_read128 /
 // ds_read_tr8 before it are passed through hold() after it, so that nothing
 // using them is scheduled ahead of the wait.  hold() also pins an MFMA result
@@ -389,12 +385,6 @@ __device__ __forceinline__ void lgkm_wait() {
 template <class T>
 __device__ __forceinline__ void hold(T& x) {
   asm volatile("" : "+v"(x));
-}
-// s_waitcnt lgkmcnt(N) that the four values pass through, so that nothing
-// using them is scheduled before it.
-template <int N>
-__device__ __forceinline__ void lgkm_wait4(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
 }
 
 // x, re-defined by an empty asm: values computed from the result inside a loop
