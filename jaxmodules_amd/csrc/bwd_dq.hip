@@ -16,7 +16,10 @@ namespace mattn {
 //   dS^T = P^T * (dP^T - delta)    (each lane owns one query: lse, delta scalars)
 //   dQ^T += K^T dS^T     (A: K^T by transposed reads of the same K tile)
 // K and V are double-buffered (one array per buffer, loop unrolled by two),
-// swizzled row-major tiles filled by direct global->LDS loads.
+// swizzled row-major tiles filled by direct global->LDS loads.  The operand
+// reads are pipelined by hand (asm LDS reads one or two k-steps ahead of their
+// MFMAs, counted lgkmcnt waits), and the dQ rows leave through an LDS-staged
+// tile, 16 bytes per lane along each row.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {

@@ -7,11 +7,14 @@
 //     S^T = K Q^T        (MFMA, K from LDS, Q^T kept in registers)
 //     online softmax     (each lane owns one query, so the row max needs one
 //                         cross-lane exchange and the row sum none)
-//     O^T += V^T P^T     (MFMA, V^T from a transposed LDS copy)
-// K and V^T are double-buffered in LDS; the next sub-block's global loads are
+//     O^T += V^T P^T     (MFMA, V^T by transposed reads of the V tile)
+// K and V are double-buffered in LDS; the next sub-block's global loads are
 // in flight while the current one is computed.  K and V tiles are moved by
 // direct global->LDS loads into swizzled row-major tiles; V^T operands are
-// read with the transposing LDS read.
+// read with the transposing LDS read.  The operand reads are pipelined by hand
+// (asm LDS reads 3 and 4 k-steps ahead of their MFMAs, counted lgkmcnt
+// waits), and the output rows leave through an LDS-staged tile, 16 bytes per
+// lane along each row.
 #include <type_traits>
 
 #include "common.hpp"
