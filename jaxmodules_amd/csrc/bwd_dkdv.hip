@@ -23,8 +23,7 @@ namespace mattn {
 // column; Q, dO_h, lse, delta and the partial-tile mask words are
 // double-buffered and filled by direct global->LDS loads.  The MFMA operand
 // reads are pipelined by hand: asm LDS reads issued two k-steps ahead of their
-// MFMAs, with counted lgkmcnt waits; bfloat16 and float16 MFMAs are grouped
-// by type.  The two query halves' dK/dV partials of
+// MFMAs, with counted lgkmcnt waits.  The two query halves' dK/dV partials of
 // a key are summed through LDS at the end, and the rows leave through an
 // LDS-staged tile, 16 bytes per lane along each row.
 // V_h is V itself for float16 inputs (vs_k = 1); for bfloat16 inputs the
@@ -209,9 +208,9 @@ void bwd_dkdv_mfma(KArgs a) {
     f32x16 st = f32x16{}, dp = f32x16{};
     {
       // S / dP pipelined by hand: the eight bfloat16 S MFMAs, then the eight
-      // float16 dP MFMAs (one switch of MFMA type, which costs issue cycles);
-      // step i reads its two 16-byte operands PS steps ahead (dO_h sits BM * D
-      // elements after Q, V_h TILE * D after K: immediate offsets)
+      // float16 dP MFMAs; step i reads its two 16-byte operands PS steps ahead
+      // (dO_h sits BM * D elements after Q, V_h TILE * D after K: immediate
+      // offsets)
       constexpr int PS = 2;
       const uint32_t qa0 = lds_addr(BUF ? Q1 : Q0) + 2 * (uint32_t)qrow;
       const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
@@ -268,10 +267,8 @@ void bwd_dkdv_mfma(KArgs a) {
     {
       // dV^T / dK^T pipelined by hand like S / dP.  Per 16-query k-step ks, the
       // four float16 dV MFMAs (one per 32-row d tile mt), then the four bfloat16
-      // dK MFMAs: switching between the two MFMA types costs issue cycles, so
-      // each type runs four at a time (and an accumulator recurs 8 MFMAs later).
-      // Step i reads the two transposed 8-byte halves of its A operand, issued
-      // PT steps ahead.
+      // dK MFMAs (an accumulator recurs 8 MFMAs later).  Step i reads the two
+      // transposed 8-byte halves of its A operand, issued PT steps ahead.
       constexpr int PT = 2;
       const uint32_t qb0 = lds_addr(BUF ? Q1 : Q0);  // dO_h rows at +2 BM D bytes
       const int tzo = opaque(tz);
