@@ -117,6 +117,26 @@ def test_lpt_xcd_order():
         assert list(w[col]) == sorted(w[col], reverse=True)
 
 
+def test_lpt_xcd_order_blocks_of_groups():
+    """An XCD with more than HEADS_AT_ONCE groups takes them block by block,
+    heaviest first inside a block."""
+    rng = np.random.default_rng(3)
+    ng, per = 8 * 3 * bm.HEADS_AT_ONCE, 5          # three blocks per XCD
+    g = np.repeat(np.arange(ng), per)
+    w = rng.integers(1, 100, size=g.size)
+    o = bm._lpt_xcd_order(w, g)
+    assert sorted(o[o >= 0].tolist()) == list(range(g.size))
+    slots = o.reshape(-1, bm.NUM_XCD)
+    for x in range(bm.NUM_XCD):
+        col = [int(i) for i in slots[:, x] if i >= 0]
+        assert all(g[i] % bm.NUM_XCD == x for i in col)
+        blocks = [(g[i] // bm.NUM_XCD) // bm.HEADS_AT_ONCE for i in col]
+        assert blocks == sorted(blocks)
+        for blk in set(blocks):
+            ws = [w[i] for i, b_ in zip(col, blocks) if b_ == blk]
+            assert ws == sorted(ws, reverse=True)
+
+
 def test_reference_exceptions():
     with pytest.raises(ValueError):
         bm.make_plan((8, 4, 16), (8, 4, 16), (8, 4, 16), is_causal=True, mask_fn=lambda h, a, b: True)
