@@ -66,3 +66,25 @@ def test_checker_flags_a_missing_wait(dkdv_asm):
     planted = body[:k] + ["\ts_nop 0"] + body[k + 1:]
     _, problems = lds_waits.check(planted)
     assert problems
+
+
+_BRANCHY = """\
+;;#ASMSTART
+\tds_read_b128 v[4:7], v1 offset:0
+;;#ASMEND
+\ts_cbranch_scc1 .LBB0_2
+\tv_mov_b32_e32 v9, 0
+\ts_waitcnt lgkmcnt(0)
+.LBB0_2:
+\tv_add_f32_e32 v8, v4, v8
+\ts_endpgm
+"""
+
+
+def test_checker_follows_forward_branches():
+    """A read still outstanding on the branch path reaches the label: using its
+    registers there is reported even though the fall-through path waited."""
+    _, problems = lds_waits.check(_BRANCHY.split("\n"))
+    assert any("touches the registers" in p for p in problems)
+    fixed = _BRANCHY.replace(".LBB0_2:\n", ".LBB0_2:\n\ts_waitcnt lgkmcnt(0)\n")
+    assert lds_waits.check(fixed.split("\n"))[1] == []
