@@ -305,7 +305,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the (b, kv head) sharding needs no collective and is described in DESIGN.md",
+              "the path shards over (b, kv head) with no collective, so each GPU would run this "
+              "single-GPU step on its own shard",
               file=sys.stderr)
         sys.exit(2)
 
