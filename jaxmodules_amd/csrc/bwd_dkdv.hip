@@ -138,40 +138,83 @@ void bwd_dkdv_mfma(KArgs a) {
   const uint32_t hbytes = (uint32_t)(((int64_t)(a.Lq - 1) * drow + D) * 2);
   __amdgpu_buffer_rsrc_t rq, rh;
   int rh_head = -1;
+  // Tile loads of the next sub-block on the fast path, prepared by launch()
+  // and issued by the step, one per S / dP k-step, so that the 1 KiB DMA
+  // instructions of the eight waves enter the load unit behind the MFMA chains
+  // rather than all at the top of the step.
+  bool dma_on = false;
+  uint32_t dma_qso = 0, dma_hso = 0;
+  auto dma = [&](auto bufc, auto ic) {  // load i of the sub-block that goes into buffer BUF
+    constexpr int BUF = decltype(bufc)::value, i = decltype(ic)::value, k = i / 2;
+    if (dma_on) {
+      if constexpr (i % 2 == 0) lds_load16_buf(rq, qld[k], dma_qso, (BUF ? Q1 : Q0) + wofs + k * BLK);
+      else lds_load16_buf(rh, dld[k], dma_hso, (BUF ? H1 : H0) + wofs + k * BLK);
+    }
+  };
 
-  auto issue = [&](auto bufc) {  // global -> LDS loads of the sub-block at the cursor
+  // Entry of the column list at the cursor (the same for both 64-query halves
+  // of a query tile), and per query head the row pointers of lse / delta and
+  // the Q / dO_h buffer resources: updated only when they change.  The branches
+  // below test wave-uniform values (scalar registers), not per-lane ones.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  int cur_qt = 0, cur_mid = -1;
+  const float* lrow = nullptr;  // lse (wave 6) or delta (wave 7) row of the current head
+
+  // The next sub-block's loads in two parts: prep() advances the cursor
+  // before the step's barrier (waves that reach the barrier early do it while
+  // they would wait anyway; per-wave stamps put the whole bookkeeping at 400-
+  // 600 cycles when all eight waves ran it right after the barrier); launch()
+  // issues the loads after the barrier, once the buffer they fill is free.
+  int nq0 = 0;  // first query row of the prepared sub-block
+  auto prep = [&](auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
-    while (le >= lend) {  // next query head of the group: another column list
-      ++lg;
-      const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
-      le = a.col_ptr[mc];
-      lend = a.col_ptr[mc + 1];
-      ec.reset();
+    if (lhalf == 0) {
+      while (le >= lend) {  // next query head of the group: another column list
+        ++lg;
+        const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
+        le = a.col_ptr[mc];
+        lend = a.col_ptr[mc + 1];
+        ec.reset();
+      }
+      ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid);
+      const int h = hk * a.G + lg;
+      if (h != rh_head) {
+        rh_head = h;
+        rq = make_rsrc((const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2], qbytes);
+        rh = make_rsrc((const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D, hbytes);
+        lrow = (wv == 6 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq;
+      }
     }
-    const int h = hk * a.G + lg;
-    int qt, mid;
-    ec.get(a.col_ent, le, lend, lane, qt, mid);
-    (BUF ? mid1 : mid0) = mid;
-    const int q0 = qt * TILE + lhalf * BM;
-    if (mid >= 0 && wave < 4) {  // 32 keys' mask words per wave (256 bytes), one dword per lane
-      const uint32_t* src = (const uint32_t*)(a.col_bits + ((int64_t)mid * 2 + lhalf) * TILE + wave * 32);
-      __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
+    (BUF ? mid1 : mid0) = cur_mid;
+    nq0 = cur_qt * TILE + lhalf * BM;
+    if (lhalf == 0) {
+      lhalf = 1;
+    } else {
+      lhalf = 0;
+      ++le;
+    }
+  };
+  auto launch = [&](auto bufc) {  // global -> LDS loads of the prepared sub-block into buffer BUF
+    constexpr int BUF = decltype(bufc)::value;
+    const int mid = BUF ? mid1 : mid0;
+    const int q0 = nq0;
+    const int mh = (q0 / BM) & 1;  // query half of its tile
+    if (mid >= 0 && wv < 4) {  // 32 keys' mask words per wave (256 bytes), one dword per lane
+      const uint32_t* src = (const uint32_t*)(a.col_bits + ((int64_t)mid * 2 + mh) * TILE + wv * 32);
+      __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wv * 32),
                                        4, 0, 0);
-    }
-    if (h != rh_head) {
-      rh_head = h;
-      rq = make_rsrc((const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2], qbytes);
-      rh = make_rsrc((const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D, hbytes);
     }
     uint16_t* ql = (BUF ? Q1 : Q0) + wofs;
     uint16_t* hl = (BUF ? H1 : H0) + wofs;
     if (q0 + BM <= a.Lq) {
-      const uint32_t qso = (uint32_t)((int64_t)q0 * a.qs[1] * 2), hso = (uint32_t)((int64_t)q0 * drow * 2);
-#pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        lds_load16_buf(rq, qld[i], qso, ql + i * BLK);
-        lds_load16_buf(rh, dld[i], hso, hl + i * BLK);
-      }
+      // the step issues these 2 NS tile loads, one per S / dP k-step
+      dma_on = true;
+      dma_qso = (uint32_t)((int64_t)q0 * a.qs[1] * 2);
+      dma_hso = (uint32_t)((int64_t)q0 * drow * 2);
+      if (wv >= 6)  // lse (wave 6) and delta (wave 7) of the 64 rows
+        __builtin_amdgcn_global_load_lds(lrow + q0 + lane,
+                                         (__attribute__((address_space(3))) void*)(wv == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0)),
+                                         4, 0, 0);
     } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
@@ -180,18 +223,10 @@ void bwd_dkdv_mfma(KArgs a) {
         lds_load16_buf(rq, (uint32_t)(qq * a.qs[1] + 8 * c) * 2, 0, ql + i * BLK);
         lds_load16_buf(rh, (uint32_t)(qq * drow + 8 * c) * 2, 0, hl + i * BLK);
       }
-    }
-    if (wave >= 6) {  // lse (wave 6) and delta (wave 7) of the 64 rows
-      const int qq = min(q0 + lane, a.Lq - 1);
-      const float* src = (wave == 6 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq + qq;
-      float* dst = wave == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0);
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
-    }
-    if (lhalf == 0) {
-      lhalf = 1;
-    } else {
-      lhalf = 0;
-      ++le;
+      if (wv >= 6)
+        __builtin_amdgcn_global_load_lds(lrow + min(q0 + lane, a.Lq - 1),
+                                         (__attribute__((address_space(3))) void*)(wv == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0)),
+                                         4, 0, 0);
     }
   };
 
@@ -235,7 +270,9 @@ void bwd_dkdv_mfma(KArgs a) {
           st = E::mfma(oa[sl], ob[sl], st);
           hold(st);
         }
+        if constexpr (i < 2 * NS) dma(std::integral_constant<int, 1 - BUF>{}, ic);
       });
+      dma_on = false;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -312,13 +349,19 @@ void bwd_dkdv_mfma(KArgs a) {
   // the loop is unrolled by two so that every buffer index is static
   auto iter = [&](int s, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
+    if (s + 1 < tot) prep(std::integral_constant<int, 1 - BUF>{});
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     const bool masked = (BUF ? mid1 : mid0) >= 0;
-    if (s + 1 < tot) issue(std::integral_constant<int, 1 - BUF>{});
+    if (s + 1 < tot) launch(std::integral_constant<int, 1 - BUF>{});
     step(bufc, masked);
   };
-  if (tot > 0) issue(std::integral_constant<int, 0>{});
+  if (tot > 0) {
+    prep(std::integral_constant<int, 0>{});
+    launch(std::integral_constant<int, 0>{});
+    static_for<2 * NS>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
+    dma_on = false;
+  }
   if constexpr (IS_BF16) {
     // V tile in float16 for the dP product, each key row scaled by a power of
     // two vs_k with max_d |V vs_k| in [2^13, 2^14): a bfloat16 value has 8
