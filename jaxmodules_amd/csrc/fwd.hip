@@ -84,11 +84,19 @@ void fwd_mfma(KArgs a) {
 
   const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);  // this wave's load block
   EntryCache ec;
-  auto issue = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
+  // The next sub-block's loads in two parts: prep() reads its map entry before
+  // the step's barrier (a wave that arrives early does it while it would wait
+  // anyway), launch() issues the loads after the barrier, once the buffer
+  // they fill is free.
+  int nkey0 = 0, nmask = -1;  // first key and mask id of the prepared sub-block
+  auto prep = [&](int s) {
+    int kt;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
+    nkey0 = kt * TILE + (s & 1) * BN;
+  };
+  auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
     constexpr int BUF = decltype(bufc)::value;
-    int kt, mask;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
-    const int key0 = kt * TILE + (s & 1) * BN;
+    const int mask = nmask, key0 = nkey0;
     uint16_t* kl = (BUF ? KV1 : KV0) + wofs;
     uint16_t* vl = (BUF ? KV1 : KV0) + BN * D + wofs;
     if (mask >= 0) {  // this wave's 32 mask words (256 bytes), one dword per lane
@@ -214,14 +222,17 @@ void fwd_mfma(KArgs a) {
   // sub-block s computes from buffer s % 2 while s + 1 loads into the other;
   // the loop is unrolled by two so that every buffer index is static
   auto iter = [&](int s, auto bufc) {
+    const bool masked = nmask >= 0;  // sub-block s, prepared one iteration ago
+    if (s + 1 < nsb) prep(s + 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
-    int kt, mask;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, mask);
-    if (s + 1 < nsb) issue(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, mask >= 0);
+    if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
+    step(bufc, masked);
   };
-  if (nsb > 0) issue(0, std::integral_constant<int, 0>{});
+  if (nsb > 0) {
+    prep(0);
+    launch(0, std::integral_constant<int, 0>{});
+  }
   for (int s = 0; s < nsb; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
