@@ -274,14 +274,19 @@ void bwd_dkdv_mfma(KArgs a) {
       });
       dma_on = false;
     }
+    // lse, delta and the mask words read together: one LDS round trip
+    const uint64_t mw = (BUF ? M1 : M0)[kloc];
+    f32x4 dv4[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
+      dv4[j] = *(const f32x4*)&Gb[8 * j + 4 * hi];
 #pragma unroll
       for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], c2, -lv[i]));
     }
+    asm volatile("" ::"v"(mw));  // keeps the mask-word read with the others (not sunk into the branch)
     if (masked) {
-      const uint32_t w32 = (uint32_t)((BUF ? M1 : M0)[kloc] >> (32 * qh)) >> (4 * hi);
+      const uint32_t w32 = (uint32_t)(mw >> (32 * qh)) >> (4 * hi);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (!mask_bit(w32, r)) st[r] = 0.f;
@@ -289,11 +294,10 @@ void bwd_dkdv_mfma(KArgs a) {
     u32x4 pk[2], sk[2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const f32x4 dv4 = *(const f32x4*)&Gb[8 * j + 4 * hi];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * j + i;
-        dp[r] = st[r] * fmaf(dp[r], dsc, -dv4[i]);
+        dp[r] = st[r] * fmaf(dp[r], dsc, -dv4[j][i]);
       }
     }
 #pragma unroll
