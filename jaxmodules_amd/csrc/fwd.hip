@@ -89,6 +89,21 @@ void fwd_mfma(KArgs a) {
   // anyway), launch() issues the loads after the barrier, once the buffer
   // they fill is free.
   int nkey0 = 0, nmask = -1;  // first key and mask id of the prepared sub-block
+  // K / V tile loads of the next sub-block on the fast path, set up by
+  // launch() and issued by the step, one per S k-step, as in dK/dV.  Issued
+  // together they held each wave ~800 cycles in launch() (per-wave s_memtime
+  // stamps, target shape); spread out, that time moves into the MFMA phases
+  // and the kernel time is unchanged to -1%.
+  bool dma_on = false;
+  const char* dma_kp = nullptr;
+  const char* dma_vp = nullptr;
+  auto dma = [&](auto bufc, auto ic) {  // load i of the sub-block that goes into buffer BUF
+    constexpr int BUF = decltype(bufc)::value, i = decltype(ic)::value, k = i / 2;
+    if (dma_on) {
+      if constexpr (i % 2 == 0) lds_load16(dma_kp + kld[k], (BUF ? KV1 : KV0) + wofs + k * BLK);
+      else lds_load16(dma_vp + vld[k], (BUF ? KV1 : KV0) + BN * D + wofs + k * BLK);
+    }
+  };
   auto prep = [&](int s) {
     int kt;
     ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
@@ -104,14 +119,10 @@ void fwd_mfma(KArgs a) {
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
                                        4, 0, 0);
     }
-    if (key0 + BN <= a.Lk) {
-      const char* kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
-      const char* vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        lds_load16(kp + kld[i], kl + i * BLK);
-        lds_load16(vp + vld[i], vl + i * BLK);
-      }
+    if (key0 + BN <= a.Lk) {  // the step issues the 2 NI tile loads
+      dma_on = true;
+      dma_kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
+      dma_vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
     } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -157,7 +168,10 @@ void fwd_mfma(KArgs a) {
         st[1] = E::mfma(k1[sl], qf[kd], st[1]);
         hold(st[0]);
         hold(st[1]);
+        if constexpr (kd < 2 * NI) dma(std::integral_constant<int, 1 - BUF>{}, kc);
       });
+      static_assert(2 * NI <= NKD, "one tile load per S k-step");
+      dma_on = false;
     }
     if (masked) {
       const uint64_t mw = (BUF ? M1 : M0)[qloc];
@@ -232,6 +246,8 @@ void fwd_mfma(KArgs a) {
   if (nsb > 0) {
     prep(0);
     launch(0, std::integral_constant<int, 0>{});
+    static_for<2 * NI>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
+    dma_on = false;
   }
   for (int s = 0; s < nsb; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
