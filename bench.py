@@ -161,6 +161,9 @@ class Runner:
         nws = int(self.lib.mattn_workspace_bytes(ctypes.byref(self.p)))
         self.ws = torch.empty(nws + 256, dtype=torch.uint8, device=dev)
         self.wptr = (self.ws.data_ptr() + 255) & ~255
+        nfw = int(self.lib.mattn_fwd_workspace_bytes(ctypes.byref(self.p)))
+        self.fws = torch.empty(nfw + 256, dtype=torch.uint8, device=dev)
+        self.fwptr = (self.fws.data_ptr() + 255) & ~255
         self.bm = A.device_blockmap(tm, dev)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.pairs = tm.pairs
@@ -170,7 +173,8 @@ class Runner:
     def fwd(self):
         self._lib.check(self.lib.mattn_fwd(ctypes.byref(self.p), ctypes.byref(self.bm),
                                            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                                           self.o.data_ptr(), self.lse.data_ptr(), self.stream), "fwd")
+                                           self.o.data_ptr(), self.lse.data_ptr(), self.fwptr,
+                                           self.stream), "fwd")
 
     def bwd(self, stage):
         self._lib.check(self.lib.mattn_bwd_stage(

@@ -26,8 +26,9 @@
  *     gradients (attention.py:91-100).
  *   - All buffers are caller-owned device memory.  The library never
  *     allocates, frees or synchronises on the call path; every launch is
- *     enqueued on the caller's stream.  No atomics are used, so results are
- *     bitwise reproducible.
+ *     enqueued on the caller's stream.  The only atomics are maxima of
+ *     non-negative floats in the backward preprocess, whose result does not
+ *     depend on their order, so results are bitwise reproducible.
  *   - Return value 0 is success, a negative value is an error code whose text
  *     is given by mattn_strerror().
  */
@@ -119,13 +120,19 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
 /* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer). */
 size_t mattn_workspace_bytes(const mattn_problem* p);
 
+/* Bytes of device workspace mattn_fwd needs (256-byte aligned pointer; 0 for
+ * float32 inputs).  16-bit inputs: V as float16 times a power of two per
+ * 128-key tile, which the P V product reads. */
+size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
+
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).
- *   o   : [B, Lq, Hq, D] of o_dtype
- *   lse : [B, Hq, Lq] float32, base-2 log-sum-exp of the scaled scores
- *         (-inf for a row with no allowed key); a residual for mattn_bwd. */
+ *   o         : [B, Lq, Hq, D] of o_dtype
+ *   lse       : [B, Hq, Lq] float32, base-2 log-sum-exp of the scaled scores
+ *               (-inf for a row with no allowed key); a residual for mattn_bwd
+ *   workspace : mattn_fwd_workspace_bytes(p) bytes (scratch; NULL when 0). */
 int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* q, const void* k, const void* v,
-              void* o, float* lse, void* stream);
+              void* o, float* lse, void* workspace, void* stream);
 
 /* Backward (replaces the custom_vjp bwd rule, attention.py:266-342).
  *   do_       : upstream gradient, [B, Lq, Hq, D] of o_dtype
@@ -137,11 +144,12 @@ int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* o, const void* do_, const float* lse,
               void* workspace, void* dq, void* dk, void* dv, void* stream);
 
-/* The three kernels of mattn_bwd, in the order they must run on one stream:
- * MATTN_BWD_PRE (delta = rowsum(dO * O), dO in the MFMA dtype, into the
- * workspace), then MATTN_BWD_DKDV and MATTN_BWD_DQ (independent of each other;
- * both read the workspace).  mattn_bwd == the three stages in order.  Same
- * arguments as mattn_bwd; exposed so a caller can time or overlap the stages. */
+/* The three stages of mattn_bwd, in the order they must run on one stream:
+ * MATTN_BWD_PRE (delta = rowsum(dO * O) and the float16 copies of dO and Q,
+ * into the workspace), MATTN_BWD_DKDV (also writes the float16 copies of K and
+ * V into the workspace), then MATTN_BWD_DQ (reads all of them).  mattn_bwd ==
+ * the three stages in order.  Same arguments as mattn_bwd; exposed so a caller
+ * can time the stages. */
 enum mattn_bwd_stage { MATTN_BWD_PRE = 0, MATTN_BWD_DKDV = 1, MATTN_BWD_DQ = 2 };
 int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     const void* q, const void* k, const void* v,

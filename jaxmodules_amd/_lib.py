@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
 
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 TILE_Q = TILE_K = 128
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 STATUS = {
     0: "MATTN_OK",
@@ -32,7 +32,7 @@ STATUS = {
 }
 
 # every symbol include/mattn.h declares
-EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_fwd", "mattn_bwd",
+EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_fwd_workspace_bytes", "mattn_fwd", "mattn_bwd",
            "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version", "mattn_maskspec_validate",
            "mattn_tilemap_classify", "mattn_tilemap_bits")
 BWD_PRE, BWD_DKDV, BWD_DQ = 0, 1, 2
@@ -105,7 +105,9 @@ def load():
         lib.mattn_validate.restype = ctypes.c_int
         lib.mattn_workspace_bytes.argtypes = [P]
         lib.mattn_workspace_bytes.restype = ctypes.c_size_t
-        lib.mattn_fwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp]
+        lib.mattn_fwd_workspace_bytes.argtypes = [P]
+        lib.mattn_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mattn_fwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_fwd.restype = ctypes.c_int
         lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_bwd.restype = ctypes.c_int

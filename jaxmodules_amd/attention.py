@@ -37,7 +37,16 @@ from . import _lib
 from . import blockmap as bmap
 
 __all__ = ["masked_attention_via_map", "flex_attention", "flex_attention_slow", "default_kernel",
-           "threshold_kernel", "trace_call", "clear_cache", "mattn_forward", "mattn_backward"]
+           "threshold_kernel", "use_custom_einsum", "kernel_scale", "trace_call", "clear_cache",
+           "mattn_forward", "mattn_backward"]
+
+
+def use_custom_einsum():
+    """attention.py:12-15: the reference switches its P.V contraction to the
+    vmap-based einsum of vectorize.py:264-382 for precision (its own tests call
+    this first).  Here P.V is a float16 MFMA product accumulated in float32, so
+    there is nothing to switch; kept so that such code imports and runs."""
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -72,12 +81,62 @@ def threshold_kernel(threshold: Optional[float] = None):
     return kernel_fn
 
 
-def _kernel_scale(kernel_fn, d: int) -> float:
+_PROBED: dict = {}
+
+
+def _call_kernel(kernel_fn, q, k) -> float:
+    """kernel_fn on 1-D float64 vectors: numpy arrays first, torch tensors if the
+    function cannot take those (the reference's kernels use jnp.dot / jnp.exp)."""
+    try:
+        return float(kernel_fn(q, k))
+    except Exception:
+        return float(kernel_fn(torch.from_numpy(q), torch.from_numpy(k)))
+
+
+def kernel_scale(kernel_fn, d: int) -> float:
+    """The softmax scale s of a kernel_fn(q, k) = exp(s * q.k + c).
+
+    The reference normalises the kernel's scores over each row's allowed keys
+    (attention.py:83-100), so a constant factor exp(c) cancels and every such
+    kernel is a softmax with scale s: default_kernel has s = 1/sqrt(d),
+    threshold_kernel(t) s = 1 (attention.py:18-50), and a user kernel such as
+    the reference test's exp(q.k / (2 sqrt(d))) (test_mapped_attention.py:1122-1144)
+    s = 1/(2 sqrt(d)).  Other kernels are probed: log kernel_fn(q, k) on 12
+    seeded random pairs of length d must be an affine function of q.k (relative
+    residual <= 1e-5), else NotImplementedError, since a kernel of any other form
+    has no counterpart in the HIP kernels.  s may be negative or zero (the caller
+    folds the sign into Q)."""
     s = getattr(kernel_fn, "_mattn_scale", "missing")
-    if s == "missing":
+    if s != "missing":
+        return 1.0 / math.sqrt(d) if s is None else float(s)
+    key = (kernel_fn, d)
+    if key in _PROBED:
+        return _PROBED[key]
+    rng = np.random.default_rng(1234)
+    xs, ys = [], []
+    for _ in range(12):
+        q = rng.standard_normal(d) * d ** -0.25
+        k = rng.standard_normal(d) * d ** -0.25
+        try:
+            val = _call_kernel(kernel_fn, q, k)
+        except Exception as e:
+            raise NotImplementedError(f"kernel_fn could not be evaluated on vectors of length {d}: {e}")
+        if not (val > 0 and math.isfinite(val)):
+            raise NotImplementedError("kernel_fn must be exp(s * q.k + c) (positive, finite scores)")
+        xs.append(float(np.dot(q, k)))
+        ys.append(math.log(val))
+    A = np.stack([np.array(xs), np.ones(len(xs))], 1)
+    (sc, c), *_ = np.linalg.lstsq(A, np.array(ys), rcond=None)
+    resid = np.abs(A @ np.array([sc, c]) - np.array(ys))
+    if resid.max() > 1e-5 * (1.0 + np.abs(ys).max()):
         raise NotImplementedError(
-            "only default_kernel and threshold_kernel are supported by the HIP kernels")
-    return 1.0 / math.sqrt(d) if s is None else float(s)
+            "only kernels of the form exp(s * q.k + c) are supported by the HIP kernels "
+            f"(log kernel_fn is not affine in q.k: residual {resid.max():.3g})")
+    # snap to the nearest float32 value: the probe sees float32 arithmetic in
+    # jnp-based kernels, while the scale itself is a float32 kernel argument
+    sc = float(np.float32(sc))
+    _PROBED[key] = sc
+    return sc
 
 
 # ---------------------------------------------------------------------------
@@ -211,10 +270,21 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
     _check_map(tm, q, k)
     p = _problem(q, k, v, o, scale)
     bm = device_blockmap(tm, q.device)
+    nws = int(lib.mattn_fwd_workspace_bytes(ctypes.byref(p)))
+    ws, wptr = _workspace(nws, q.device)
     _lib.check(lib.mattn_fwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
-                             v.data_ptr(), o.data_ptr(), lse.data_ptr(), _stream(q.device)),
+                             v.data_ptr(), o.data_ptr(), lse.data_ptr(), wptr, _stream(q.device)),
                "mattn_fwd")
     return o, lse
+
+
+def _workspace(nbytes: int, device):
+    """(tensor, 256-byte aligned pointer) of at least nbytes of device memory
+    (None, None when nbytes is 0)."""
+    if nbytes == 0:
+        return None, None
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    return ws, (ws.data_ptr() + 255) & ~255
 
 
 def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
@@ -225,9 +295,7 @@ def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     p = _problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
-    ws = torch.empty(max(int(lib.mattn_workspace_bytes(ctypes.byref(p))), 256) + 256,
-                     dtype=torch.uint8, device=q.device)
-    wptr = (ws.data_ptr() + 255) & ~255
+    ws, wptr = _workspace(max(int(lib.mattn_workspace_bytes(ctypes.byref(p))), 256), q.device)
     bm = device_blockmap(tm, q.device)
     _lib.check(lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
                              v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(), wptr,
@@ -239,14 +307,20 @@ def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
 class _MaskedAttention(torch.autograd.Function):
     """The reference's custom_vjp (attention.py:180, 244-345).  Residuals are
     (Q, K, V, O, LSE) instead of (Q, K, V): the backward reads the saved
-    log-sum-exp rather than re-running the forward scan."""
+    log-sum-exp rather than re-running the forward scan.
+
+    O is always computed and saved in float32 (the reference's own output
+    dtype); a 16-bit ``out_dtype`` is a rounded copy of it.  The backward's
+    delta = rowsum(dO * O) then uses the unrounded O: where one key dominates
+    a row, dS = P (dP - delta) cancels, and a bfloat16 O would leave its
+    rounding (2^-9 of |V|) in dQ and dK."""
 
     @staticmethod
     def forward(ctx, q, k, v, tm, scale, out_dtype, heads_major=False):
-        o, lse = mattn_forward(q, k, v, tm, scale, out_dtype, heads_major)
+        o, lse = mattn_forward(q, k, v, tm, scale, torch.float32, heads_major)
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.tm, ctx.scale = tm, scale
-        return o
+        return o if out_dtype == torch.float32 else o.to(out_dtype)
 
     @staticmethod
     def backward(ctx, do):
@@ -285,8 +359,10 @@ def masked_attention_via_map(
 
     K: [B, L, Hkv, d] or [L, Hkv, d]; Q: [B, N, Hq, d] or [N, Hq, d]; V like K.
     is_causal: mask q >= k (exclusive with mask_fn, ValueError otherwise).
-    kernel_fn: default_kernel (softmax with scale 1/sqrt(d)) or threshold_kernel(t)
-        (scale 1); other kernels raise NotImplementedError.
+    kernel_fn: exp(s * q.k + c): default_kernel (softmax with scale 1/sqrt(d)),
+        threshold_kernel(t) (scale 1) or a user kernel of that form, whose s
+        is probed (kernel_scale); kernels of any other form raise
+        NotImplementedError.
     mask_fn: boolean function of (b, h, q, k) or (h, q, k), elementwise in its
         index arguments (it is evaluated on broadcast numpy index arrays).
     block_size / window_size: as the reference: the window is block-granular,
@@ -301,7 +377,7 @@ def masked_attention_via_map(
     plan, tm = trace_call(tuple(Q.shape), tuple(K.shape), tuple(V.shape), is_causal=is_causal,
                           mask_fn=mask_fn, block_size=block_size, window_size=window_size,
                           device=Q.device if Q.is_cuda else None)
-    scale = _kernel_scale(kernel_fn, plan.d)
+    scale = kernel_scale(kernel_fn, plan.d)
     if not (Q.is_cuda and K.is_cuda and V.is_cuda):
         raise RuntimeError("masked_attention_via_map runs on the GPU only (no CPU code path)")
     dt = torch.promote_types(torch.promote_types(Q.dtype, K.dtype), V.dtype)
@@ -310,6 +386,12 @@ def masked_attention_via_map(
     if plan.squeeze_batch:
         Q, K, V = Q[None], K[None], V[None]
     D = _kernel_dim(plan.d)
+    Q = Q.to(dt)
+    # softmax(s q.k) == softmax(|s| (-q).k); s == 0 gives uniform weights: q = 0, scale 1
+    if scale < 0:
+        Q, scale = -Q, -scale
+    elif scale == 0:
+        Q, scale = Q * 0, 1.0
     q, k, v = (_ready(_pad_dim(x.to(dt), D)) for x in (Q, K, V))
     od = _out_dtype(dt, out_dtype)
     out = _MaskedAttention.apply(q, k, v, tm, scale, od)

@@ -363,8 +363,12 @@ def _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_f
     bi = np.arange(B) % map_b
     hi = np.arange(Hq) % map_h
     qw = row_cnt[bi][:, hi].reshape(B * Hq * nqt) + 1                  # item (b*Hq + h)*nqt + qt
-    qgroups = np.repeat(np.arange(B * Hq), nqt)
     G = Hq // Hkv
+    # The query heads of one GQA group read the same K/V: their items share an
+    # XCD (group (b*Hq + h) // G = b*Hkv + h // G), so each K/V tile is fetched
+    # into one L2 -- unless there are fewer such groups than XCDs, when the
+    # per-head groups spread the work over more dies.
+    qgroups = np.repeat(np.arange(B * Hq) // (G if B * Hkv >= NUM_XCD else 1), nqt)
     cc = col_cnt[bi][:, hi]                                            # [B, Hq, nkt]
     kvw = cc.reshape(B, Hkv, G, nkt).sum(axis=2).reshape(B * Hkv * nkt) + 1
     kvgroups = np.repeat(np.arange(B * Hkv), nkt)

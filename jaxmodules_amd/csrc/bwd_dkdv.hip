@@ -2,7 +2,7 @@
 // /root/reference/jaxmodules/attention.py:266-342): one workgroup per
 // 128-key map column of (b, kv head) walking the column's present query tiles
 // for every query head of the GQA group; dK and dV accumulated in registers and
-// written once each -- no atomics.
+// written once each -- no atomics.  Every product runs on float16 operands.
 #include <type_traits>
 
 #include "common.hpp"
@@ -13,28 +13,33 @@ namespace mattn {
 // dK / dV (MFMA, no atomics)
 // ---------------------------------------------------------------------------
 // 8 waves (2 per SIMD).  Wave w owns keys 32 (w % 4) .. +31 of the tile and
-// query half w / 4 of every 64-query sub-block:
-//   S    = Q K^T          (A: Q rows, B: K rows; both from LDS)
-//   dP   = dO_h V_h^T     (float16: dO * s and V * vs_k; B: V_h rows from LDS)
-//   P    = exp2(scale_log2 S - lse),  dS = P * (dP / (s vs_k) - delta)
-//   dV^T += dO_h^T P      (A: transposed reads of the dO_h tile, float16)
-//   dK^T += Q^T dS        (A: transposed reads of the Q tile)
-// The K and V_h tiles of the workgroup's 128 keys stay in LDS for the whole
-// column; Q, dO_h, lse, delta and the partial-tile mask words are
-// double-buffered and filled by direct global->LDS loads.  The MFMA operand
-// reads are pipelined by hand: asm LDS reads issued two k-steps ahead of their
-// MFMAs, with counted lgkmcnt waits.  The two query halves' dK/dV partials of
-// a key are summed through LDS at the end, and the rows leave through an
-// LDS-staged tile, 16 bytes per lane along each row.
-// V_h is V itself for float16 inputs (vs_k = 1); for bfloat16 inputs the
-// prologue converts the column's V rows to float16, each scaled by vs_k.
+// query half w / 4 of every 64-query sub-block.  With the float16 copies
+// Q' = Q r_h, dO' = dO s_h (bwd_pre) and K' = K k_t, V' = V v_t (the
+// prologue; k_t, v_t powers of two per 128-key tile):
+//   S'   = Q' K'^T          (A: Q' rows, B: K' rows; both from LDS)
+//   dP'  = dO' V'^T         (B: V' rows from LDS)
+//   P~   = f exp2(S' c2 / (r_h k_t) - lse)          (f: see below)
+//   dS~  = P~ (dP' / v_t - delta s_h)   = f s_h dS
+//   dV^T += dO'^T P~      (A: transposed reads of the dO' tile)
+//   dK^T += Q'^T dS~      (A: transposed reads of the Q' tile)
+// f is a power of two that keeps |dS~| < 2^14 (ds_scale of the head bounds
+// bwd_pre left in hst and the tile's max |V|), so dS~ loses nothing to
+// float16's range; the accumulators are in units of f s_h (dV) and f s_h r_h
+// (dK), rescaled when a GQA group's walk moves to a head with other scales.
+// The K' and V' tiles of the workgroup's 128 keys stay in LDS for the whole
+// column (and are written to kh, vh for the dQ kernel); Q', dO', lse, delta
+// and the partial-tile mask words are double-buffered and filled by direct
+// global->LDS loads.  The MFMA operand reads are pipelined by hand: asm LDS
+// reads issued two k-steps ahead of their MFMAs, with counted lgkmcnt waits.
+// The two query halves' dK/dV partials of a key are summed through LDS at the
+// end, and the rows leave through an LDS-staged tile, 16 bytes per lane along
+// each row.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
-  constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BM = 64;              // queries per sub-block
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
@@ -46,7 +51,7 @@ void bwd_dkdv_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) float L0[BM], L1[BM];        // lse
   __shared__ __attribute__((aligned(16))) float G0[BM], G1[BM];        // delta
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
-  // per buffer: Q rows, then dO_h rows (BM * D elements each); K tile, then V_h tile
+  // per buffer: Q' rows, then dO' rows (BM * D elements each); K' tile, then V' tile
   __shared__ __attribute__((aligned(16))) uint16_t QH0[2 * BM * D], QH1[2 * BM * D];
   __shared__ __attribute__((aligned(16))) uint16_t KV[2 * TILE * D];
   uint16_t* const Q0 = QH0;
@@ -55,7 +60,7 @@ void bwd_dkdv_mfma(KArgs a) {
   uint16_t* const H1 = QH1 + BM * D;
   uint16_t* const Ks = KV;
   uint16_t* const Vs = KV + TILE * D;
-  __shared__ float VI[TILE];  // bfloat16 inputs: 1 / vs_k of the tile's keys
+  __shared__ f32x2 red[8];
 
   const int item = a.kv_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
@@ -68,35 +73,15 @@ void bwd_dkdv_mfma(KArgs a) {
   const int kg = wave & 3, qh = wave >> 2;
   const int kloc = 32 * kg + l32;
   const float c2 = a.scale_log2;
-  const float inv_s = a.dscale[1];
-  // dP = (dO_h V_h^T) / (s vs_k): one factor per lane, since a lane owns one key
-  // (set once the V tile is converted, below)
-  float dsc = inv_s;
 
-  // K tile of the column (and V for float16 inputs): loaded once, by all 8 waves
-  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  {
-    const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-#pragma unroll
-    for (int i = 0; i < 2 * NS; ++i) {
-      const int n = 2 * NS * wave + i;
-      const int kk = min(kt * TILE + TL::row_of(n, lane), a.Lk - 1);
-      const int c = TL::chunk_of(n, lane);
-      lds_load16(kb + (int64_t)kk * a.ks[1] + 8 * c, Ks + n * BLK);
-      if constexpr (!IS_BF16) lds_load16(vb + (int64_t)kk * a.vs[1] + 8 * c, Vs + n * BLK);
-    }
-  }
-
-  // bfloat16 inputs: this thread's share of the V tile (4 threads per key row),
-  // loaded now so that the column-list reads below overlap its latency
-  constexpr int CPL = D / 32;  // 16-byte chunks per thread
-  u32x4 vx[CPL];
-  if constexpr (IS_BF16) {
-    const int kk = min(kt * TILE + (tid >> 2), a.Lk - 1);
-    const uint16_t* vp = vb + (int64_t)kk * a.vs[1] + 8 * CPL * (tid & 3);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) vx[j] = *(const u32x4*)(vp + 8 * j);
-  }
+  // this thread's share of the column's K and V rows (4 threads per key row),
+  // loaded now so that the column-list reads below overlap their latency;
+  // converted to float16 once the tile maxima are known
+  TileRows<D> tkr, tvr;
+  tile_load<D>(tkr, (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)(kt * TILE) * a.ks[1] +
+                        (int64_t)hk * a.ks[2], a.ks[1], a.Lk - kt * TILE);
+  tile_load<D>(tvr, (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)(kt * TILE) * a.vs[1] +
+                        (int64_t)hk * a.vs[2], a.vs[1], a.Lk - kt * TILE);
 
   // Flattened walk over (query head g of the group, column entry, half).
   int tot = 0;
@@ -112,13 +97,11 @@ void bwd_dkdv_mfma(KArgs a) {
     lend = a.col_ptr[mc + 1];
   }
 
-  const int64_t drow = (int64_t)a.Hq * D;   // row stride of the dense dO_h copy
-  uint32_t qld[NS], dld[NS];  // loop-invariant source byte offsets of this lane's load slots
+  // loop-invariant source byte offsets of this lane's load slots (Q' and dO'
+  // rows are dense: row stride D in both copies)
+  uint32_t qld[NS];
 #pragma unroll
-  for (int i = 0; i < NS; ++i) {
-    qld[i] = 2 * TL::src_off(NS * wave + i, lane, a.qs[1]);
-    dld[i] = 2 * TL::src_off(NS * wave + i, lane, drow);
-  }
+  for (int i = 0; i < NS; ++i) qld[i] = 2 * TL::src_off(NS * wave + i, lane, D);
   // LDS operand addresses, formed per use from lane seeds (one v_xad_u32 each)
   // rather than held in 24 registers across the loop (element offsets):
   //   row read, chunk 2 kd + hi of row r:   r D + ((16 kd) ^ rx),  rx = 8 hi ^ 8 swz(r)
@@ -133,28 +116,31 @@ void bwd_dkdv_mfma(KArgs a) {
   const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
   EntryCache ec;
   int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
-  // buffer resources of the current query head's Q and dO_h slices
-  const uint32_t qbytes = (uint32_t)(((int64_t)(a.Lq - 1) * a.qs[1] + D) * 2);
-  const uint32_t hbytes = (uint32_t)(((int64_t)(a.Lq - 1) * drow + D) * 2);
+  // per-head scales (s_h, r_h) of the sub-block in each buffer
+  float sh0 = 1.f, rh0 = 1.f, sh1 = 1.f, rh1 = 1.f;
+  // buffer resources of the current query head's Q' and dO' slices
+  const int64_t hrows = (int64_t)a.nqt * TILE;  // rows per head in the copies
+  const uint32_t hbytes = (uint32_t)(hrows * D * 2);
   __amdgpu_buffer_rsrc_t rq, rh;
   int rh_head = -1;
+  float cur_s = 1.f, cur_r = 1.f;  // scales of the prepared sub-block's head
   // Tile loads of the next sub-block on the fast path, prepared by launch()
   // and issued by the step, one per S / dP k-step, so that the 1 KiB DMA
   // instructions of the eight waves enter the load unit behind the MFMA chains
   // rather than all at the top of the step.
   bool dma_on = false;
-  uint32_t dma_qso = 0, dma_hso = 0;
+  uint32_t dma_so = 0;
   auto dma = [&](auto bufc, auto ic) {  // load i of the sub-block that goes into buffer BUF
     constexpr int BUF = decltype(bufc)::value, i = decltype(ic)::value, k = i / 2;
     if (dma_on) {
-      if constexpr (i % 2 == 0) lds_load16_buf(rq, qld[k], dma_qso, (BUF ? Q1 : Q0) + wofs + k * BLK);
-      else lds_load16_buf(rh, dld[k], dma_hso, (BUF ? H1 : H0) + wofs + k * BLK);
+      if constexpr (i % 2 == 0) lds_load16_buf(rq, qld[k], dma_so, (BUF ? Q1 : Q0) + wofs + k * BLK);
+      else lds_load16_buf(rh, qld[k], dma_so, (BUF ? H1 : H0) + wofs + k * BLK);
     }
   };
 
   // Entry of the column list at the cursor (the same for both 64-query halves
-  // of a query tile), and per query head the row pointers of lse / delta and
-  // the Q / dO_h buffer resources: updated only when they change.  The branches
+  // of a query tile), and per query head the row pointers of lse / delta, the
+  // Q' / dO' buffer resources and the head's scales: updated only when they change.  The branches
   // below test wave-uniform values (scalar registers), not per-lane ones.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   int cur_qt = 0, cur_mid = -1;
@@ -180,12 +166,18 @@ void bwd_dkdv_mfma(KArgs a) {
       const int h = hk * a.G + lg;
       if (h != rh_head) {
         rh_head = h;
-        rq = make_rsrc((const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2], qbytes);
-        rh = make_rsrc((const uint16_t*)a.dOh + ((int64_t)b * a.Lq * a.Hq + h) * D, hbytes);
+        const int64_t hb = ((int64_t)b * a.Hq + h) * hrows * D;
+        rq = make_rsrc(a.qh + hb, hbytes);
+        rh = make_rsrc(a.doh + hb, hbytes);
         lrow = (wv == 6 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq;
+        const float2 sc = a.hsc[b * a.Hq + h];
+        cur_s = sc.x;
+        cur_r = sc.y;
       }
     }
     (BUF ? mid1 : mid0) = cur_mid;
+    (BUF ? sh1 : sh0) = cur_s;
+    (BUF ? rh1 : rh0) = cur_r;
     nq0 = cur_qt * TILE + lhalf * BM;
     if (lhalf == 0) {
       lhalf = 1;
@@ -204,48 +196,47 @@ void bwd_dkdv_mfma(KArgs a) {
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wv * 32),
                                        4, 0, 0);
     }
-    uint16_t* ql = (BUF ? Q1 : Q0) + wofs;
-    uint16_t* hl = (BUF ? H1 : H0) + wofs;
-    if (q0 + BM <= a.Lq) {
-      // the step issues these 2 NS tile loads, one per S / dP k-step
-      dma_on = true;
-      dma_qso = (uint32_t)((int64_t)q0 * a.qs[1] * 2);
-      dma_hso = (uint32_t)((int64_t)q0 * drow * 2);
-      if (wv >= 6)  // lse (wave 6) and delta (wave 7) of the 64 rows
-        __builtin_amdgcn_global_load_lds(lrow + q0 + lane,
-                                         (__attribute__((address_space(3))) void*)(wv == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0)),
-                                         4, 0, 0);
-    } else {  // ragged last sub-block: rows past Lq re-read row Lq-1 (masked anyway)
-#pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        const int qq = min(q0 + TL::row_of(NS * wave + i, lane), a.Lq - 1);
-        const int c = TL::chunk_of(NS * wave + i, lane);
-        lds_load16_buf(rq, (uint32_t)(qq * a.qs[1] + 8 * c) * 2, 0, ql + i * BLK);
-        lds_load16_buf(rh, (uint32_t)(qq * drow + 8 * c) * 2, 0, hl + i * BLK);
-      }
-      if (wv >= 6)
-        __builtin_amdgcn_global_load_lds(lrow + min(q0 + lane, a.Lq - 1),
-                                         (__attribute__((address_space(3))) void*)(wv == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0)),
-                                         4, 0, 0);
-    }
+    // the step issues the 2 NS tile loads, one per S / dP k-step (the Q' and
+    // dO' copies are padded to whole tiles, so no row is out of range)
+    dma_on = true;
+    dma_so = (uint32_t)(q0 * D * 2);
+    if (wv >= 6)  // lse (wave 6) and delta (wave 7) of the 64 rows; rows past Lq re-read row Lq-1
+      __builtin_amdgcn_global_load_lds(lrow + min(q0 + lane, a.Lq - 1),
+                                       (__attribute__((address_space(3))) void*)(wv == 6 ? (BUF ? L1 : L0) : (BUF ? G1 : G0)),
+                                       4, 0, 0);
   };
 
   f32x16 dk[NMD], dv[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+  // set by the prologue: the column's K' / V' tile scales and the dS scale f
+  float ksc = 1.f, ivs = 1.f, fds = 1.f;
+  float acc_s = 1.f, acc_r = 1.f;  // head scales the accumulators are in
+  float m2c = c2;                   // c2 / (r_h k_t) of the accumulators' head
 
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
+    // the sub-block's head scales (uniform); another head of the GQA group
+    // with other scales rescales the accumulators (powers of two: exact)
+    const float ss = BUF ? sh1 : sh0, rr = BUF ? rh1 : rh0;
+    if (ss != acc_s || rr != acc_r) {
+      const float fv = ss / acc_s, fk = fv * (rr / acc_r);
+#pragma unroll
+      for (int i = 0; i < NMD; ++i) { dv[i] *= fv; dk[i] *= fk; }
+      acc_s = ss;
+      acc_r = rr;
+      m2c = c2 / (rr * ksc);
+    }
+    const float mc = m2c;
     const float* Lb = (BUF ? L1 : L0) + 32 * qh;
     const float* Gb = (BUF ? G1 : G0) + 32 * qh;
     // seeds re-defined here, so the addresses derived from them stay per use;
     const int rxo = opaque(rx);
     f32x16 st = f32x16{}, dp = f32x16{};
     {
-      // S / dP pipelined by hand: the eight bfloat16 S MFMAs, then the eight
-      // float16 dP MFMAs; step i reads its two 16-byte operands PS steps ahead
-      // (dO_h sits BM * D elements after Q, V_h TILE * D after K: immediate
-      // offsets)
+      // S / dP pipelined by hand: the eight S MFMAs, then the eight dP MFMAs;
+      // step i reads its two 16-byte operands PS steps ahead (dO' sits BM * D
+      // elements after Q', V' TILE * D after K': immediate offsets)
       constexpr int PS = 2;
       const uint32_t qa0 = lds_addr(BUF ? Q1 : Q0) + 2 * (uint32_t)qrow;
       const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
@@ -267,7 +258,7 @@ void bwd_dkdv_mfma(KArgs a) {
           dp = H::mfma(oa[sl], ob[sl], dp);
           hold(dp);
         } else {
-          st = E::mfma(oa[sl], ob[sl], st);
+          st = H::mfma(oa[sl], ob[sl], st);
           hold(st);
         }
         if constexpr (i < 2 * NS) dma(std::integral_constant<int, 1 - BUF>{}, ic);
@@ -282,7 +273,7 @@ void bwd_dkdv_mfma(KArgs a) {
       const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
       dv4[j] = *(const f32x4*)&Gb[8 * j + 4 * hi];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], c2, -lv[i]));
+      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], mc, -lv[i])) * fds;
     }
     asm volatile("" ::"v"(mw));  // keeps the mask-word read with the others (not sunk into the branch)
     if (masked) {
@@ -297,21 +288,21 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * j + i;
-        dp[r] = st[r] * fmaf(dp[r], dsc, -dv4[j][i]);
+        dp[r] = st[r] * fmaf(dp[r], ivs, -dv4[j][i]);
       }
     }
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       pk[r >> 3][(r & 7) >> 1] = H::pack2(st[r], st[r + 1]);
-      sk[r >> 3][(r & 7) >> 1] = E::pack2(dp[r], dp[r + 1]);
+      sk[r >> 3][(r & 7) >> 1] = H::pack2(dp[r], dp[r + 1]);
     }
     {
       // dV^T / dK^T pipelined by hand like S / dP.  Per 16-query k-step ks, the
-      // four float16 dV MFMAs (one per 32-row d tile mt), then the four bfloat16
-      // dK MFMAs (an accumulator recurs 8 MFMAs later).  Step i reads the two
-      // transposed 8-byte halves of its A operand, issued PT steps ahead.
+      // four dV MFMAs (one per 32-row d tile mt), then the four dK MFMAs (an
+      // accumulator recurs 8 MFMAs later).  Step i reads the two transposed
+      // 8-byte halves of its A operand, issued PT steps ahead.
       constexpr int PT = 2;
-      const uint32_t qb0 = lds_addr(BUF ? Q1 : Q0);  // dO_h rows at +2 BM D bytes
+      const uint32_t qb0 = lds_addr(BUF ? Q1 : Q0);  // dO' rows at +2 BM D bytes
       const int tzo = opaque(tz);
       uint32_t am0[NMD], am1[NMD];
 #pragma unroll
@@ -342,7 +333,7 @@ void bwd_dkdv_mfma(KArgs a) {
           dv[mt] = H::mfma(aop, pk[ks], dv[mt]);
           hold(dv[mt]);
         } else {
-          dk[mt] = E::mfma(aop, sk[ks], dk[mt]);
+          dk[mt] = H::mfma(aop, sk[ks], dk[mt]);
           hold(dk[mt]);
         }
       });
@@ -366,37 +357,47 @@ void bwd_dkdv_mfma(KArgs a) {
     static_for<2 * NS>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
     dma_on = false;
   }
-  if constexpr (IS_BF16) {
-    // V tile in float16 for the dP product, each key row scaled by a power of
-    // two vs_k with max_d |V vs_k| in [2^13, 2^14): a bfloat16 value has 8
-    // significant bits, so V vs_k is exact in float16 down to 2^-16 (subnormals
-    // included), 2^29 below the row's largest element.  4 lanes per key row.
+  {
+    // K' and V' tiles: float16 times a power of two per tile with max |x| in
+    // [2^13, 2^14) (a bfloat16 or float16 value is then exact in float16 down
+    // to 2^-17 relative to the tile's largest element), into the resident LDS
+    // tiles and to kh / vh for the dQ kernel.  4 threads per key row.
+    constexpr int CPL = TileRows<D>::CPL;
+    const f32x2 m = block_max2_512(tile_absmax2<D, Tag>(tkr, tvr), red);
+    const float kscl = pow2_scale(m[0], 14), vscl = pow2_scale(m[1], 14);
     const int r = tid >> 2, part = tid & 3;
-    const u32x4* x = vx;
-    float m = 0.f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(E::to_f32(elt16(x[j], e))));
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    float vs = 1.f;
-    if (m > 0.f && m <= 3.4e38f) {
-      int e;
-      frexpf(m, &e);  // m < 2^e
-      vs = ldexpf(1.f, min(126, max(-126, 14 - e)));
-    }
+    const int64_t col = (int64_t)(b * a.Hkv + hk) * a.nkt + kt;
+    uint16_t* kd = a.kh + (col * TILE + r) * D + 8 * CPL * part;
+    uint16_t* vd = a.vh + (col * TILE + r) * D + 8 * CPL * part;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      u32x4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = H::pack2(E::to_f32(elt16(x[j], 2 * e)) * vs, E::to_f32(elt16(x[j], 2 * e + 1)) * vs);
-      *(u32x4*)&Vs[sw_off<D>(r, CPL * part + j)] = y;
+      const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl), yv = chunk_f16<Tag>(tvr.x[j], vscl);
+      *(u32x4*)&Ks[sw_off<D>(r, CPL * part + j)] = yk;
+      *(u32x4*)&Vs[sw_off<D>(r, CPL * part + j)] = yv;
+      *(u32x4*)(kd + 8 * j) = yk;
+      *(u32x4*)(vd + 8 * j) = yv;
     }
-    if (part == 0) VI[r] = 1.f / vs;
-    __syncthreads();
-    dsc = inv_s * VI[kloc];
+    if (tid == 0) {
+      a.ksc[col] = kscl;
+      a.vsc[col] = vscl;
+      a.vmax[col] = m[1];
+    }
+    // dS scale: |dS s_h| <= max_q |dO'_q|_1 max |V| + max |delta s_h| over the group's heads
+    f32x2 hb = {0.f, 0.f};
+    if (tid < a.G) {
+      const float2 t = a.hst[b * a.Hq + hk * a.G + tid];
+      hb = f32x2{t.x, t.y};
+    }
+    for (int g = tid + 512; g < a.G; g += 512) {
+      const float2 t = a.hst[b * a.Hq + hk * a.G + g];
+      hb = f32x2{fmaxf(hb[0], t.x), fmaxf(hb[1], t.y)};
+    }
+    hb = block_max2_512(hb, red);
+    ksc = kscl;
+    ivs = 1.f / vscl;
+    fds = ds_scale(fmaf(hb[0], m[1], hb[1]));
+    m2c = c2 / (acc_r * ksc);
+    __syncthreads();  // the K' / V' tiles are complete
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
@@ -449,8 +450,8 @@ void bwd_dkdv_mfma(KArgs a) {
                     E::pack2(acc[mt][4 * j + 2] * sc, acc[mt][4 * j + 3] * sc)};
       }
     };
-    finish(dk, redk, a.scale);
-    finish(dv, redv, inv_s);
+    finish(dk, redk, a.scale / (fds * acc_s * acc_r));
+    finish(dv, redv, 1.f / (fds * acc_s));
   }
   __syncthreads();
   constexpr int CPR = D / 8;  // 16-byte chunks per row

@@ -1,6 +1,7 @@
 // dQ kernel of the masked-attention backward (the custom_vjp bwd rule,
 // /root/reference/jaxmodules/attention.py:266-342): one workgroup per
-// 128-query map row, dQ accumulated in registers and written once.
+// 128-query map row, dQ accumulated in registers and written once.  Every
+// product runs on float16 operands.
 #include <type_traits>
 
 #include "common.hpp"
@@ -10,12 +11,18 @@ namespace mattn {
 // ---------------------------------------------------------------------------
 // dQ (MFMA)
 // ---------------------------------------------------------------------------
-// Each wave owns 32 queries; per 64-key sub-block:
-//   S^T  = K Q^T         (A: K rows from LDS, B: Q^T in registers)
-//   dP^T = V dO^T        (A: V rows from LDS, B: dO^T in registers)
-//   dS^T = P^T * (dP^T - delta)    (each lane owns one query: lse, delta scalars)
-//   dQ^T += K^T dS^T     (A: K^T by transposed reads of the same K tile)
-// K and V are double-buffered (one array per buffer, loop unrolled by two),
+// Each wave owns 32 queries.  With the float16 copies Q' = Q r_h, dO' = dO s_h
+// (bwd_pre) and K' = K k_t, V' = V v_t (written by the dK/dV kernel, which
+// runs first; k_t, v_t powers of two per 128-key tile), per 64-key sub-block:
+//   S'^T  = K' Q'^T       (A: K' rows from LDS, B: Q'^T in registers)
+//   dP'^T = V' dO'^T      (A: V' rows from LDS, B: dO'^T in registers)
+//   P     = exp2(S' c2 / (k_t r_h) - lse)     (each lane owns one query)
+//   dS~^T = P^T * (dP'^T t / v_t - delta s_h t) = t s_h dS^T
+//   dQ^T += K'^T dS~^T    (A: K'^T by transposed reads of the same K' tile)
+// t is a power of two that keeps |dS~| < 2^14 (the head bounds bwd_pre left
+// in hst and the kv head's max |V|); the accumulator is in units of
+// t s_h k_t, rescaled when the walk reaches a tile with another k_t.
+// K' and V' are double-buffered (one array per buffer, loop unrolled by two),
 // swizzled row-major tiles filled by direct global->LDS loads.  The operand
 // reads are pipelined by hand (asm LDS reads one or two k-steps ahead of their
 // MFMAs, counted lgkmcnt waits), and the dQ rows leave through an LDS-staged
@@ -24,8 +31,8 @@ template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {
   using E = Elt<Tag>;
+  using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
-  constexpr bool IS_BF16 = __is_same(Tag, bf16_tag);
   constexpr int BN = 64;
   constexpr int NKD = D / 16;
   constexpr int NMD = D / 32;
@@ -56,11 +63,10 @@ void bwd_dq_mfma(KArgs a) {
 
   u32x4 qf[NKD], df[NKD];
   {
-    const uint16_t* qp = (const uint16_t*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
-                         (int64_t)h * a.qs[2] + 8 * hi;
-    // bfloat16 inputs: dO rounded to bfloat16; float16 inputs: dO * s in float16
-    const void* dsrc = IS_BF16 ? a.dO16 : a.dOh;
-    const uint16_t* dp = (const uint16_t*)dsrc + (((int64_t)b * a.Lq + qc) * a.Hq + h) * D + 8 * hi;
+    // the padded rows of the copies are zero, so q needs no clamp here
+    const int64_t row = ((int64_t)b * a.Hq + h) * a.nqt * TILE + q;
+    const uint16_t* qp = a.qh + row * D + 8 * hi;
+    const uint16_t* dp = a.doh + row * D + 8 * hi;
 #pragma unroll
     for (int kd = 0; kd < NKD; ++kd) {
       qf[kd] = *(const u32x4*)(qp + 16 * kd);
@@ -69,17 +75,24 @@ void bwd_dq_mfma(KArgs a) {
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
   const float nlse = -a.lse[rs];
-  const float dl = IS_BF16 ? a.delta16[rs] : a.delta[rs];  // delta of the dO copy dP uses
-  const float dps = IS_BF16 ? 1.f : a.dscale[1];  // undoes the dO scale of float16 inputs
-
-  const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  uint32_t kld[NI], vld[NI];  // source byte offsets of this lane's load slots
+  const float2 hsc = a.hsc[b * a.Hq + h];  // (s_h, r_h)
+  const float2 hst = a.hst[b * a.Hq + h];  // (max |dO'|_1 of a row, max |delta s_h|)
+  const int tb = (b * a.Hkv + hk) * a.nkt;  // first tile of this kv head in the per-tile arrays
+  // t from the bound |dS s_h| <= max |dO'_q|_1 max |V| + max |delta s_h| (max |V| over the kv head)
+  float vm = 0.f;
+  for (int t = lane; t < a.nkt; t += 64) vm = fmaxf(vm, a.vmax[tb + t]);
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
-    vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
-  }
+  for (int o = 32; o >= 1; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
+  const float tds = pow2_scale(fmaf(hst.x, vm, hst.y), 14);
+  const float bq = -a.delta[rs] * tds;  // delta is stored in units of s_h
+  const float c2r = c2 / hsc.y;
+
+  // float16 K' / V' rows of this kv head: dense, row stride D, padded to whole tiles
+  const uint16_t* kb = a.kh + (int64_t)tb * TILE * D;
+  const uint16_t* vb = a.vh + (int64_t)tb * TILE * D;
+  uint32_t kld[NI];  // source byte offsets of this lane's load slots (K' and V' alike)
+#pragma unroll
+  for (int i = 0; i < NI; ++i) kld[i] = 2 * TL::src_off(NI * wave + i, lane, D);
   // LDS operand addresses, formed per use from lane seeds (one v_xad_u32 each)
   // rather than held in 16 registers across the loop (element offsets):
   //   row read, chunk 2 kd + hi of row l32 (+32 t):  l32 D + ((16 kd) ^ rx)
@@ -97,10 +110,13 @@ void bwd_dq_mfma(KArgs a) {
   // anyway), launch() issues the loads after the barrier, once the buffer
   // they fill is free.
   int nkey0 = 0, nmask = -1;  // first key and mask id of the prepared sub-block
+  float nks = 1.f, nvs = 1.f;   // its tile's K' and V' scales
   auto prep = [&](int s) {
     int kt;
     ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
     nkey0 = kt * TILE + (s & 1) * BN;
+    nks = a.ksc[tb + kt];
+    nvs = a.vsc[tb + kt];
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
     constexpr int BUF = decltype(bufc)::value;
@@ -112,33 +128,31 @@ void bwd_dq_mfma(KArgs a) {
       __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)((BUF ? M1 : M0) + wave * 32),
                                        4, 0, 0);
     }
-    if (key0 + BN <= a.Lk) {
-      const char* kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
-      const char* vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
+    // K' and V' are padded to whole tiles: no row is out of range
+    const char* kp = (const char*)(kb + (int64_t)key0 * D);
+    const char* vp = (const char*)(vb + (int64_t)key0 * D);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        lds_load16(kp + kld[i], kl + i * BLK);
-        lds_load16(vp + vld[i], vl + i * BLK);
-      }
-    } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int key = min(key0 + TL::row_of(NI * wave + i, lane), a.Lk - 1);
-        const int c = TL::chunk_of(NI * wave + i, lane);
-        lds_load16(kb + (int64_t)key * a.ks[1] + 8 * c, kl + i * BLK);
-        lds_load16(vb + (int64_t)key * a.vs[1] + 8 * c, vl + i * BLK);
-      }
+    for (int i = 0; i < NI; ++i) {
+      lds_load16(kp + kld[i], kl + i * BLK);
+      lds_load16(vp + kld[i], vl + i * BLK);
     }
   };
 
   f32x16 acc[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
+  float kcur = 1.f;  // K' tile scale the accumulator is in
 
-  // Each 32-key half t of the sub-block is carried through S^T, dP^T, dS^T and
-  // its two dQ k-steps before the next half starts (halves the live state).
-  auto step = [&](auto bufc, bool masked) {
+  auto step = [&](auto bufc, bool masked, float sks, float svs) {
     constexpr int BUF = decltype(bufc)::value;
+    if (sks != kcur) {  // a tile with another K' scale (uniform; powers of two: exact)
+      const float f = sks / kcur;
+#pragma unroll
+      for (int i = 0; i < NMD; ++i) acc[i] *= f;
+      kcur = sks;
+    }
+    const float mq = c2r / sks;   // S = S' / (k_t r_h)
+    const float adp = tds / svs;  // dS~ = P (dP' t / v_t - delta s_h t)
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
     // operand reads pipelined by hand (asm LDS reads issued PS / PQ k-steps
     // ahead of their MFMAs, counted lgkmcnt waits); the V tile sits BN * D
@@ -167,13 +181,13 @@ void bwd_dq_mfma(KArgs a) {
         lgkm_wait<2 * (kd + PS < NKD ? PS : NKD - 1 - kd)>();
         hold(ka[sl]);
         hold(va[sl]);
-        st = E::mfma(ka[sl], qf[kd], st);
-        dp = E::mfma(va[sl], df[kd], dp);
+        st = H::mfma(ka[sl], qf[kd], st);
+        dp = H::mfma(va[sl], df[kd], dp);
         hold(st);
         hold(dp);
       });
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], c2, nlse));
+      for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], mq, nlse));
       if (masked) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
 #pragma unroll
@@ -183,9 +197,9 @@ void bwd_dq_mfma(KArgs a) {
       u32x4 pk[2];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float d0 = st[r] * fmaf(dp[r], dps, -dl);
-        const float d1 = st[r + 1] * fmaf(dp[r + 1], dps, -dl);
-        pk[r >> 3][(r & 7) >> 1] = E::pack2(d0, d1);
+        const float d0 = st[r] * fmaf(dp[r], adp, bq);
+        const float d1 = st[r + 1] * fmaf(dp[r + 1], adp, bq);
+        pk[r >> 3][(r & 7) >> 1] = H::pack2(d0, d1);
       }
       // dQ^T += K^T dS^T over the half's two k-steps, K^T by transposed reads
       u32x2 lo[PQ + 1], up[PQ + 1];
@@ -202,7 +216,7 @@ void bwd_dq_mfma(KArgs a) {
         lgkm_wait<2 * (i + PQ < 2 * NMD ? PQ : 2 * NMD - 1 - i)>();
         hold(lo[sl]);
         hold(up[sl]);
-        acc[mt] = E::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[kk], acc[mt]);
+        acc[mt] = H::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[kk], acc[mt]);
         hold(acc[mt]);
       });
     });
@@ -211,11 +225,12 @@ void bwd_dq_mfma(KArgs a) {
 
   auto iter = [&](int s, auto bufc) {
     const bool masked = nmask >= 0;  // sub-block s, prepared one iteration ago
+    const float sks = nks, svs = nvs;
     if (s + 1 < nsb) prep(s + 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, masked);
+    step(bufc, masked, sks, svs);
   };
   if (nsb > 0) {
     prep(0);
@@ -232,7 +247,7 @@ void bwd_dq_mfma(KArgs a) {
   uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * 32 * D;
   static_assert(2 * 32 * D <= 2 * BN * D, "output staging");
   const int r0 = qt * TILE + 32 * wave;
-  store_rows<D, 2>(acc, a.scale, stage, a.dq,
+  store_rows<D, 2>(acc, a.scale / (tds * hsc.x * kcur), stage, a.dq,
                    (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2], a.dqs[1],
                    min(32, a.Lq - r0), lane, E::pack2);
 }

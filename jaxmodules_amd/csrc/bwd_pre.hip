@@ -3,184 +3,206 @@
 //
 // The reference recomputes each query block's key scan and back-propagates
 // through it, adding full-size dK/dV contributions per query block.  Here the
-// gradient is computed from the saved base-2 log-sum-exp in three kernels:
-//   bwd_pre  : delta = rowsum(dO * O) per query row; dO converted to the MFMA
-//              dtypes (this file, with the float32 SIMT kernels);
-//   bwd_dkdv : one workgroup per 128-key map column of (b, kv head); it walks
-//              the column's present query tiles for every query head of the
-//              GQA group and accumulates dK, dV in registers -- each element
-//              written exactly once, no atomics;
-//   bwd_dq   : one workgroup per 128-query map row; dQ accumulated in registers.
+// gradient is computed from the saved base-2 log-sum-exp in four kernels:
+//   bwd_absmax : per (b, head, chunk of CHUNK query rows) the largest |dO| and
+//                |Q| (partial maxima, no atomics);
+//   bwd_pre    : per (b, head, 64-row sub-block) the float16 copies dOh =
+//                dO * s_h and Qh = Q * r_h (powers of two from the head's
+//                maxima), delta = rowsum(O * dOh), and the head's bounds on
+//                the dS the backward kernels form (maxima by atomic max of
+//                non-negative floats: the result does not depend on the order);
+//   bwd_dkdv   : one workgroup per 128-key map column of (b, kv head); it walks
+//                the column's present query tiles for every query head of the
+//                GQA group and accumulates dK, dV in registers -- each element
+//                written exactly once, no atomics (bwd_dkdv.hip);
+//   bwd_dq     : one workgroup per 128-query map row; dQ accumulated in
+//                registers (bwd_dq.hip).
 // With P = exp2(scale_log2 * S - lse) and dS = P * (dO V^T - delta):
 //   dV = P^T dO,  dK = scale * dS^T Q,  dQ = scale * dS K.
+// Every product of the 16-bit paths runs on float16 operands (11 significant
+// bits): a bfloat16 dS or dO (8 bits) leaves 2^-9 relative errors that the
+// 2e-3 parity gate does not absorb where one term dominates a sum.
 #include <type_traits>
 
 #include "common.hpp"
 
 namespace mattn {
 
-
 // ---------------------------------------------------------------------------
 // preprocess
 // ---------------------------------------------------------------------------
-// The dV product P^T dO runs on float16 MFMA: P lies in [0, 1] and float16
-// keeps 11 significant bits against bfloat16's 8, which matters because dO
-// arrives in float32 (the reference's output dtype).  dO is scaled by a power
-// of two s so that max |dO * s| < 2^14 (the scale is exact and undone on the
-// float32 result).  s comes from a deterministic two-pass max: bwd_absmax
-// writes NPART partial maxima, bwd_pre reduces them.
 
-// Element loads of one 16-lane row group: PER = D / 16 consecutive values.
-template <int D, class Tag, bool O_F32>
-__device__ __forceinline__ void load_row(const void* base, int64_t off, int sub, float* g) {
+// PER consecutive values of a row (o_dtype float32 or the 16-bit Tag) as floats.
+template <int PER, class Tag, bool F32>
+__device__ __forceinline__ void load_vals(const void* base, int64_t off, float* g) {
   using E = Elt<Tag>;
-  constexpr int PER = D / 16;
-  if constexpr (O_F32) {
-    const float* p = (const float*)base + off + sub * PER;
+  if constexpr (F32) {
+    const float* p = (const float*)base + off;
 #pragma unroll
     for (int i = 0; i < PER; i += 4) {
       const f32x4 y = *(const f32x4*)(p + i);
       g[i] = y[0]; g[i + 1] = y[1]; g[i + 2] = y[2]; g[i + 3] = y[3];
     }
   } else {
-    const uint16_t* p = (const uint16_t*)base + off + sub * PER;
+    const uint16_t* p = (const uint16_t*)base + off;
+    if constexpr (PER % 8 == 0) {
 #pragma unroll
-    for (int i = 0; i < PER; i += 4) {
-      const u32x2 y = *(const u32x2*)(p + i);
+      for (int i = 0; i < PER; i += 8) {
+        const u32x4 y = *(const u32x4*)(p + i);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) g[i + j] = E::to_f32((y[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+        for (int j = 0; j < 8; ++j) g[i + j] = E::to_f32(elt16(y, j));
+      }
+    } else {
+      static_assert(PER == 4, "row slice of 4 or a multiple of 8 values");
+      const u32x2 y = *(const u32x2*)p;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) g[j] = E::to_f32((y[j >> 1] >> (16 * (j & 1))) & 0xffffu);
     }
   }
 }
 
-__device__ __forceinline__ float block_max256(float x, float* red) {
+// Element-wise maximum of x over the 256 threads of a workgroup (red: 4 entries).
+__device__ __forceinline__ f32x2 block_max2_256(f32x2 x, f32x2* red) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  for (int o = 32; o >= 1; o >>= 1) {
+    x[0] = fmaxf(x[0], __shfl_xor(x[0], o));
+    x[1] = fmaxf(x[1], __shfl_xor(x[1], o));
+  }
+  __syncthreads();  // red may still be read by a previous call
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  f32x2 r = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    r[0] = fmaxf(r[0], red[w][0]);
+    r[1] = fmaxf(r[1], red[w][1]);
+  }
+  return r;
 }
 
-// NPART workgroups; grid-stride over (b, q, h) rows, 16 lanes per row, four
-// rows in flight per lane group.
+// Partial maxima of |dO| and |Q| over CHUNK query rows of one (b, head):
+// grid B * Hq * nch, 16 lanes per row, 16 rows per pass.
 template <int D, class Tag, bool O_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
 void bwd_absmax(KArgs a) {
   constexpr int PER = D / 16;
-  constexpr int UNR = 4;
-  __shared__ float red[4];
-  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
+  __shared__ f32x2 red[4];
+  const int bh = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
+  const int h = bh % a.Hq, b = bh / a.Hq;
   const int sub = threadIdx.x & 15;
-  const uint32_t step = gridDim.x * 16;
-  float mx = 0.f;
-  for (uint32_t r0 = blockIdx.x * 16 + (threadIdx.x >> 4); r0 < nrows; r0 += UNR * step) {
-    float g[UNR][PER];
+  const int q1 = min(a.Lq, (ch + 1) * CHUNK);
+  f32x2 mx = {0.f, 0.f};
+  const int64_t dbase = (int64_t)b * a.dos[0] + (int64_t)h * a.dos[2] + sub * PER;
+  const int64_t qbase = (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2] + sub * PER;
+#pragma unroll 4
+  for (int q = ch * CHUNK + (threadIdx.x >> 4); q < q1; q += 16) {
+    float g[PER], x[PER];
+    load_vals<PER, Tag, O_F32>(a.dO, dbase + (int64_t)q * a.dos[1], g);
+    load_vals<PER, Tag, false>(a.q, qbase + (int64_t)q * a.qs[1], x);
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const uint32_t row = min(r0 + u * step, nrows - 1);  // a repeated row leaves the max unchanged
-      const int h = (int)(row % (uint32_t)a.Hq);
-      const uint32_t bq = row / (uint32_t)a.Hq;
-      const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
-      load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
-                              sub, g[u]);
+    for (int i = 0; i < PER; ++i) {
+      mx[0] = fmaxf(mx[0], fabsf(g[i]));
+      mx[1] = fmaxf(mx[1], fabsf(x[i]));
     }
-#pragma unroll
-    for (int u = 0; u < UNR; ++u)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) mx = fmaxf(mx, fabsf(g[u][i]));
   }
-  mx = block_max256(mx, red);
-  if (threadIdx.x == 0) a.part[blockIdx.x] = mx;
-}
-
-// One workgroup: the power-of-two scale s with max |dO * s| < 2^14, and 1/s.
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
-void bwd_scale(KArgs a) {
-  __shared__ float red[4];
-  float m = 0.f;
-  for (int i = threadIdx.x; i < NPART; i += 256) m = fmaxf(m, a.part[i]);
-  m = block_max256(m, red);
+  mx = block_max2_256(mx, red);
   if (threadIdx.x == 0) {
-    float s = 1.f;
-    if (m > 0.f && m <= 3.4e38f) {
-      int e;
-      frexpf(m, &e);  // m < 2^e
-      s = ldexpf(1.f, min(126, max(-126, 14 - e)));
-    }
-    a.dscale[0] = s;
-    a.dscale[1] = 1.f / s;
+    a.part[blockIdx.x] = float2{mx[0], mx[1]};
+    if (ch == 0) a.hst[bh] = float2{0.f, 0.f};  // bwd_pre raises it
   }
 }
 
-// 16 lanes per (b, q, h) row, 16 rows per workgroup.  MODE 0: delta only
-// (float32 inputs); 1: also dO * s in float16 (float16 inputs); 2: also dO in
-// bfloat16 (bfloat16 inputs).
-template <int D, class Tag, bool O_F32, int MODE>
+// One workgroup per (b, head, 64-row sub-block), 4 threads per row.  Rows past
+// Lq (up to the 128-row padding of the copies) are written as zeros.
+template <int D, class Tag, bool O_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
 void bwd_pre(KArgs a) {
-  using E = Elt<Tag>;
   using H = Elt<f16_tag>;
+  constexpr int PER = D / 4;
+  __shared__ f32x2 red[4];
+  const int nsb = 2 * a.nqt;
+  const int bh = blockIdx.x / nsb, sb = blockIdx.x % nsb;
+  const int h = bh % a.Hq, b = bh / a.Hq;
+  const int tid = threadIdx.x, part = tid & 3;
+  const int q = sb * SUB_ROWS + (tid >> 2);
+  const bool live = q < a.Lq;
+
+  // the head's scales from its partial maxima (every workgroup of the head
+  // computes the same values)
+  f32x2 hm = {0.f, 0.f};
+  for (int i = tid; i < a.nch; i += 256) {
+    const float2 p = a.part[bh * a.nch + i];
+    hm[0] = fmaxf(hm[0], p.x);
+    hm[1] = fmaxf(hm[1], p.y);
+  }
+  hm = block_max2_256(hm, red);
+  const float s = pow2_scale(hm[0], 14), r = pow2_scale(hm[1], 14);
+  if (sb == 0 && tid == 0) a.hsc[bh] = float2{s, r};
+
+  float o[PER], g[PER], x[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) o[i] = g[i] = x[i] = 0.f;
+  if (live) {
+    load_vals<PER, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * PER, o);
+    load_vals<PER, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + part * PER, g);
+    load_vals<PER, Tag, false>(a.q, (int64_t)b * a.qs[0] + (int64_t)q * a.qs[1] + (int64_t)h * a.qs[2] + part * PER, x);
+  }
+  // float16 copies; delta and the row's L1 norm from dOh exactly as rounded,
+  // so that dS = P (dP - delta) cancels exactly where the exact dS is zero
+  // (a row with a single allowed key) and its rounding error scales with V - O.
+  uint32_t hp[PER / 2], qp[PER / 2];
+  float dl = 0.f, l1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; i += 2) {
+    hp[i / 2] = H::pack2(g[i] * s, g[i + 1] * s);
+    qp[i / 2] = H::pack2(x[i] * r, x[i + 1] * r);
+    const float h0 = H::to_f32(hp[i / 2] & 0xffffu), h1 = H::to_f32(hp[i / 2] >> 16);
+    dl = fmaf(o[i], h0, fmaf(o[i + 1], h1, dl));
+    l1 += fabsf(h0) + fabsf(h1);
+  }
+#pragma unroll
+  for (int m = 1; m < 4; m <<= 1) {
+    dl += __shfl_xor(dl, m);
+    l1 += __shfl_xor(l1, m);
+  }
+  const int64_t row = (int64_t)bh * (a.nqt * TILE) + q;
+  uint16_t* wd = a.doh + row * D + part * PER;
+  uint16_t* wq = a.qh + row * D + part * PER;
+#pragma unroll
+  for (int i = 0; i < PER; i += 8) {
+    *(u32x4*)(wd + i) = u32x4{hp[i / 2], hp[i / 2 + 1], hp[i / 2 + 2], hp[i / 2 + 3]};
+    *(u32x4*)(wq + i) = u32x4{qp[i / 2], qp[i / 2 + 1], qp[i / 2 + 2], qp[i / 2 + 3]};
+  }
+  if (live && part == 0) a.delta[(int64_t)bh * a.Lq + q] = dl;
+  const f32x2 st = block_max2_256(f32x2{l1, fabsf(dl)}, red);
+  if (tid == 0) {  // non-negative floats order like their bit patterns
+    atomicMax((unsigned int*)&a.hst[bh].x, __float_as_uint(st[0]));
+    atomicMax((unsigned int*)&a.hst[bh].y, __float_as_uint(st[1]));
+  }
+}
+
+// float32 inputs: delta = rowsum(dO * O) only (the SIMT kernels read dO
+// directly).  16 lanes per (b, q, h) row, 16 rows per workgroup.
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
+void bwd_pre_f32(KArgs a) {
   constexpr int PER = D / 16;
   const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
   const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
-  const float s = MODE > 0 ? a.dscale[0] : 1.f;
   const int h = (int)(row % (uint32_t)a.Hq);
   const uint32_t bq = row / (uint32_t)a.Hq;
   const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
   float x[PER], g[PER];
-  load_row<D, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2], sub, x);
-  load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2],
-                          sub, g);
-  // delta = rowsum(dO * O) with dO as rounded in the copy whose dP it meets:
-  // dS = P (dP - delta) then cancels exactly where it should (a row with one
-  // allowed key has dS = 0), and its error scales with V - O rather than V.
-  // MODE 0: float32 dO; MODE 1, 2: the float16 dO * s copy (divided by s),
-  // and MODE 2 also delta16 from the bfloat16 copy (the dQ kernel's dP).
-  uint32_t hp[PER / 2], bp[PER / 2];
-  float acc = 0.f, acc16 = 0.f;
-  if constexpr (MODE == 0) {
+  load_vals<PER, bf16_tag, true>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + sub * PER, x);
+  load_vals<PER, bf16_tag, true>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + sub * PER, g);
+  float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) acc = fmaf(x[i], g[i], acc);
-  } else {
-    const float inv = a.dscale[1];
+  for (int i = 0; i < PER; ++i) acc = fmaf(x[i], g[i], acc);
 #pragma unroll
-    for (int i = 0; i < PER; i += 2) {
-      hp[i / 2] = H::pack2(g[i] * s, g[i + 1] * s);
-      acc = fmaf(x[i], H::to_f32(hp[i / 2] & 0xffffu) * inv, acc);
-      acc = fmaf(x[i + 1], H::to_f32(hp[i / 2] >> 16) * inv, acc);
-    }
-  }
-  if constexpr (MODE == 2) {
-#pragma unroll
-    for (int i = 0; i < PER; i += 2) {
-      bp[i / 2] = E::pack2(g[i], g[i + 1]);
-      acc16 = fmaf(x[i], E::to_f32(bp[i / 2] & 0xffffu), acc16);
-      acc16 = fmaf(x[i + 1], E::to_f32(bp[i / 2] >> 16), acc16);
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    acc += __shfl_xor(acc, o, 16);
-    if constexpr (MODE == 2) acc16 += __shfl_xor(acc16, o, 16);
-  }
-  const int64_t rr = ((int64_t)b * a.Hq + h) * a.Lq + q;
-  if (sub == 0) {
-    a.delta[rr] = acc;
-    if constexpr (MODE == 2) a.delta16[rr] = acc16;
-  }
-  if constexpr (MODE > 0) {
-    // dense [B, Lq, Hq, D] copies
-    uint16_t* w = (uint16_t*)a.dOhw + (int64_t)row * D + sub * PER;
-#pragma unroll
-    for (int i = 0; i < PER; i += 4) *(u32x2*)(w + i) = u32x2{hp[i / 2], hp[i / 2 + 1]};
-  }
-  if constexpr (MODE == 2) {
-    uint16_t* w = (uint16_t*)a.dO16w + (int64_t)row * D + sub * PER;
-#pragma unroll
-    for (int i = 0; i < PER; i += 4) *(u32x2*)(w + i) = u32x2{bp[i / 2], bp[i / 2 + 1]};
-  }
+  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 16);
+  if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -356,15 +378,21 @@ void bwd_dkdv_simt(KArgs a) {
 hipError_t launch_dq(const KArgs& a, int D, int dtype, int grid, hipStream_t st);
 hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st);
 
+template <int D, class Tag, bool OF32>
+static void launch_pre_16(const KArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((bwd_absmax<D, Tag, OF32>), dim3(a.B * a.Hq * a.nch), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((bwd_pre<D, Tag, OF32>), dim3(a.B * a.Hq * 2 * a.nqt), dim3(256), 0, st, a);
+}
+
 hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,
                             int kv_grid, hipStream_t st) {
-  const int64_t rows = (int64_t)a.B * a.Lq * a.Hq;
-  const int pre_grid = (int)((rows + 15) / 16);
   const bool of32 = (o_dtype == MATTN_F32);
   if (dtype == MATTN_F32) {
     if (stage == MATTN_BWD_PRE) {
-      if (D == 64) hipLaunchKernelGGL((bwd_pre<64, bf16_tag, true, 0>), dim3(pre_grid), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((bwd_pre<128, bf16_tag, true, 0>), dim3(pre_grid), dim3(256), 0, st, a);
+      const int64_t rows = (int64_t)a.B * a.Lq * a.Hq;
+      const int pre_grid = (int)((rows + 15) / 16);
+      if (D == 64) hipLaunchKernelGGL((bwd_pre_f32<64>), dim3(pre_grid), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((bwd_pre_f32<128>), dim3(pre_grid), dim3(256), 0, st, a);
     } else if (stage == MATTN_BWD_DKDV) {
       if (D == 64) hipLaunchKernelGGL((bwd_dkdv_simt<64>), dim3(kv_grid), dim3(512), 0, st, a);
       else hipLaunchKernelGGL((bwd_dkdv_simt<128>), dim3(kv_grid), dim3(512), 0, st, a);
@@ -376,20 +404,13 @@ hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int s
   }
   if (stage == MATTN_BWD_DKDV) return launch_dkdv(a, D, dtype, kv_grid, st);
   if (stage == MATTN_BWD_DQ) return launch_dq(a, D, dtype, q_grid, st);
-#define MATTN_PRE(DD, TAG, OF32, MODE)                                                           \
-  do {                                                                                           \
-    hipLaunchKernelGGL((bwd_absmax<DD, TAG, OF32>), dim3(NPART), dim3(256), 0, st, a);           \
-    hipLaunchKernelGGL(bwd_scale, dim3(1), dim3(256), 0, st, a);                                 \
-    hipLaunchKernelGGL((bwd_pre<DD, TAG, OF32, MODE>), dim3(pre_grid), dim3(256), 0, st, a);     \
-  } while (0)
   if (dtype == MATTN_BF16) {
-    if (D == 64) { if (of32) MATTN_PRE(64, bf16_tag, true, 2); else MATTN_PRE(64, bf16_tag, false, 2); }
-    else { if (of32) MATTN_PRE(128, bf16_tag, true, 2); else MATTN_PRE(128, bf16_tag, false, 2); }
+    if (D == 64) { if (of32) launch_pre_16<64, bf16_tag, true>(a, st); else launch_pre_16<64, bf16_tag, false>(a, st); }
+    else { if (of32) launch_pre_16<128, bf16_tag, true>(a, st); else launch_pre_16<128, bf16_tag, false>(a, st); }
   } else {
-    if (D == 64) { if (of32) MATTN_PRE(64, f16_tag, true, 1); else MATTN_PRE(64, f16_tag, false, 1); }
-    else { if (of32) MATTN_PRE(128, f16_tag, true, 1); else MATTN_PRE(128, f16_tag, false, 1); }
+    if (D == 64) { if (of32) launch_pre_16<64, f16_tag, true>(a, st); else launch_pre_16<64, f16_tag, false>(a, st); }
+    else { if (of32) launch_pre_16<128, f16_tag, true>(a, st); else launch_pre_16<128, f16_tag, false>(a, st); }
   }
-#undef MATTN_PRE
   return hipGetLastError();
 }
 

@@ -1,6 +1,6 @@
 // C ABI of the library (declared in include/mattn.h): argument validation,
-// kernel-argument packing and launch selection.  Host code only; the kernels
-// live in fwd.hip and bwd.hip.
+// workspace layouts, kernel-argument packing and launch selection.  Host code
+// only; the kernels live in fwd.hip, bwd_pre.hip, bwd_dkdv.hip and bwd_dq.hip.
 #include <math.h>
 
 #include "common.hpp"
@@ -15,7 +15,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 
@@ -31,23 +31,52 @@ bool strides_ok(const int64_t s[3], int esz) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Backward workspace: delta (f32 per query row), the partial maxima of |dO|
-// and the scale pair, dO * s in float16, and for bfloat16 inputs dO in
-// bfloat16 with its own delta.
+// Forward workspace (16-bit inputs): V as float16 times a power of two per
+// 128-key tile, [B, Hkv, nkt * 128, D], with each tile's scale and max |V|.
+struct FwdWs {
+  size_t vh, vsc, vmax, total;
+};
+
+FwdWs fwd_ws_layout(const mattn_problem* p) {
+  FwdWs w{};
+  if (p->dtype == MATTN_F32) return w;
+  const size_t tiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
+  w.vh = 0;
+  w.vsc = align256(tiles * MATTN_TILE_K * p->D * 2);
+  w.vmax = w.vsc + align256(tiles * sizeof(float));
+  w.total = w.vmax + align256(tiles * sizeof(float));
+  return w;
+}
+
+// Backward workspace: delta (f32 per query row); for 16-bit inputs also the
+// partial maxima of |dO| and |Q|, the per-head scales and dS bounds, the
+// float16 copies dO', Q' ([B, Hq, nqt * 128, D]) and K', V'
+// ([B, Hkv, nkt * 128, D]), and each K' / V' tile's scale and max |V|.
 struct WsLayout {
-  size_t delta, part, scale, doh, do16, delta16, total;
+  size_t delta, part, hsc, hst, doh, qh, kh, vh, ksc, vsc, vmax, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
   const size_t rows = (size_t)p->B * p->Hq * p->Lq;
   WsLayout w{};
   w.delta = 0;
-  w.part = align256(rows * sizeof(float));
-  w.scale = w.part + align256(NPART * sizeof(float));
-  w.doh = w.scale + 256;
-  w.do16 = w.doh + (p->dtype == MATTN_F32 ? 0 : align256(rows * p->D * 2));
-  w.delta16 = w.do16 + (p->dtype == MATTN_BF16 ? align256(rows * p->D * 2) : 0);
-  w.total = w.delta16 + (p->dtype == MATTN_BF16 ? align256(rows * sizeof(float)) : 0);
+  w.total = align256(rows * sizeof(float));
+  if (p->dtype == MATTN_F32) return w;
+  const size_t heads = (size_t)p->B * p->Hq;
+  const size_t nch = cdiv(p->Lq, CHUNK);
+  const size_t qrows = heads * cdiv(p->Lq, MATTN_TILE_Q) * MATTN_TILE_Q;
+  const size_t tiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
+  w.part = w.total;
+  w.hsc = w.part + align256(heads * nch * 8);
+  w.hst = w.hsc + align256(heads * 8);
+  w.doh = w.hst + align256(heads * 8);
+  w.qh = w.doh + align256(qrows * p->D * 2);
+  w.kh = w.qh + align256(qrows * p->D * 2);
+  w.vh = w.kh + align256(tiles * MATTN_TILE_K * p->D * 2);
+  w.ksc = w.vh + align256(tiles * MATTN_TILE_K * p->D * 2);
+  w.vsc = w.ksc + align256(tiles * sizeof(float));
+  w.vmax = w.vsc + align256(tiles * sizeof(float));
+  w.total = w.vmax + align256(tiles * sizeof(float));
   return w;
 }
 
@@ -69,6 +98,7 @@ KArgs make_args(const mattn_problem* p, const mattn_blockmap* bm) {
   a.Hq = p->Hq;
   a.Hkv = p->Hkv;
   a.G = p->Hq / p->Hkv;
+  a.nch = (int)cdiv(p->Lq, CHUNK);
   a.scale = p->scale;
   a.scale_log2 = p->scale * 1.4426950408889634f;
   a.map_b = bm->map_b;
@@ -125,11 +155,14 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if ((int64_t)p->B * p->Hq * p->Lq >= (1ll << 31) || (int64_t)p->B * p->Hkv * p->Lk >= (1ll << 31) || (int64_t)p->B * p->Hq * nqt >= (1ll << 31) || (int64_t)p->B * p->Hkv * nkt >= (1ll << 31) ||
       (int64_t)p->Lq + MATTN_TILE_Q >= (1ll << 31) || (int64_t)p->Lk + MATTN_TILE_K >= (1ll << 31))
     return MATTN_ERR_TOO_LARGE;
-  // kernels address rows inside one (batch, head) slice with 32-bit element offsets
+  // kernels address rows inside one (batch, head) slice with 32-bit offsets:
+  // element offsets along the inputs' sequence strides, and byte offsets
+  // (buffer resources of the dK/dV kernel) inside one head's float16 copy
   const int64_t lim = (1ll << 31) - 1;
   if ((int64_t)(nqt * MATTN_TILE_Q) * p->q_stride[1] > lim ||
       (int64_t)(nkt * MATTN_TILE_K) * p->k_stride[1] > lim ||
-      (int64_t)(nkt * MATTN_TILE_K) * p->v_stride[1] > lim)
+      (int64_t)(nkt * MATTN_TILE_K) * p->v_stride[1] > lim ||
+      (int64_t)(nqt * MATTN_TILE_Q) * p->D * 2 > lim || (int64_t)(nkt * MATTN_TILE_K) * p->D * 2 > lim)
     return MATTN_ERR_TOO_LARGE;
   if (!bm) return MATTN_OK;
   if (bm->nqt != nqt || bm->nkt != nkt) return MATTN_ERR_BLOCKMAP;
@@ -150,19 +183,33 @@ size_t mattn_workspace_bytes(const mattn_problem* p) {
   return ws_layout(p).total;
 }
 
+size_t mattn_fwd_workspace_bytes(const mattn_problem* p) {
+  if (mattn_validate(p, nullptr) != MATTN_OK) return 0;
+  return fwd_ws_layout(p).total;
+}
+
 int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
-              const void* v, void* o, float* lse, void* stream) {
+              const void* v, void* o, float* lse, void* workspace, void* stream) {
   int rc = mattn_validate(p, bm);
   if (rc != MATTN_OK) return rc;
   if (!bm) return MATTN_ERR_NULL;
   if (!q || !k || !v || !o || !lse) return MATTN_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return MATTN_ERR_STRIDE;
+  const FwdWs w = fwd_ws_layout(p);
+  if (w.total > 0 && !workspace) return MATTN_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ((uintptr_t)workspace & 255u))
+    return MATTN_ERR_STRIDE;
   KArgs a = make_args(p, bm);
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = o;
   a.lse = lse;
+  char* ws = (char*)workspace;
+  if (w.total > 0) {
+    a.vh = (uint16_t*)(ws + w.vh);
+    a.vsc = (float*)(ws + w.vsc);
+    a.vmax = (float*)(ws + w.vmax);
+  }
   hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
 }
@@ -191,13 +238,18 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
-  a.delta16 = (float*)(ws + w.delta16);
-  a.part = (float*)(ws + w.part);
-  a.dscale = (float*)(ws + w.scale);
-  a.dOhw = ws + w.doh;
-  a.dOh = a.dOhw;
-  a.dO16w = ws + w.do16;
-  a.dO16 = a.dO16w;
+  if (p->dtype != MATTN_F32) {
+    a.part = (float2*)(ws + w.part);
+    a.hsc = (float2*)(ws + w.hsc);
+    a.hst = (float2*)(ws + w.hst);
+    a.doh = (uint16_t*)(ws + w.doh);
+    a.qh = (uint16_t*)(ws + w.qh);
+    a.kh = (uint16_t*)(ws + w.kh);
+    a.vh = (uint16_t*)(ws + w.vh);
+    a.ksc = (float*)(ws + w.ksc);
+    a.vsc = (float*)(ws + w.vsc);
+    a.vmax = (float*)(ws + w.vmax);
+  }
   hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
                                   bm->n_kv_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;

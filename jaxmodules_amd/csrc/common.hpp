@@ -38,29 +38,42 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int TILE = 128;  // map tile edge (MATTN_TILE_Q == MATTN_TILE_K)
-constexpr int NPART = 1024;  // workgroups of the max |dO| pass
+constexpr int SUB_ROWS = 64;  // rows of a backward sub-block (the unit of the per-sub-block bounds)
+constexpr int CHUNK = 256; // query rows per workgroup of the max |dO|, |Q| pass
 constexpr float NEG_INF = -__builtin_inff();
 
 // Arguments of every kernel (passed by value in the kernarg segment).
+//
+// The 16-bit paths multiply float16 operands only.  Every float16 working copy
+// is the input times a power of two (exact for bfloat16 and float16 values in
+// range), written head-major and dense, [B, H, rows padded to 128, D], rows
+// past the sequence end zero:
+//   vh = V * vsc[b, hk, tile], kh = K * ksc[b, hk, tile]  (per 128-key tile)
+//   dOh = dO * hsc[b, h].x,  qh = Q * hsc[b, h].y          (per head)
+// so each product's scale is a per-step scalar, undone on the float32 result.
 struct KArgs {
   const void* q;
   const void* k;
   const void* v;
   const void* o;     // forward output (read by the backward preprocess)
   const void* dO;    // upstream gradient in o_dtype
-  const void* dO16;  // upstream gradient in bfloat16 (workspace; bf16 inputs only)
-  const void* dOh;   // upstream gradient * dscale[0] in float16 (workspace)
-  float* dscale;     // [2] (s, 1/s): power-of-two scale of dOh (workspace)
-  float* part;       // [NPART] partial max |dO| (workspace)
   void* out;         // forward output O
   float* lse;        // [B, Hq, Lq] base-2 log-sum-exp
-  float* delta;      // [B, Hq, Lq] rowsum(dO * O), dO as in dOh (workspace)
-  float* delta16;    // [B, Hq, Lq] rowsum(dO * O), dO as in dO16 (workspace; bf16 inputs only)
+  float* delta;      // [B, Hq, Lq] rowsum(O * dOh): delta in units of hsc.x
   void* dq;
   void* dk;
   void* dv;
-  void* dO16w;       // writable aliases for the preprocess kernel
-  void* dOhw;
+  uint16_t* vh;      // [B, Hkv, nkt*128, D] float16 V * vsc
+  uint16_t* kh;      // [B, Hkv, nkt*128, D] float16 K * ksc (backward)
+  uint16_t* qh;      // [B, Hq, nqt*128, D] float16 Q * hsc.y (backward)
+  uint16_t* doh;     // [B, Hq, nqt*128, D] float16 dO * hsc.x (backward)
+  float* vsc;        // [B*Hkv*nkt] scale of each V tile
+  float* vmax;       // [B*Hkv*nkt] max |V| of each tile
+  float* ksc;        // [B*Hkv*nkt] scale of each K tile (backward)
+  float2* hsc;       // [B*Hq] (dO scale, Q scale) of each head (backward)
+  float2* part;      // [B*Hq*nch] partial (max |dO|, max |Q|) (backward)
+  float2* hst;       // [B*Hq] (max row L1 norm of dOh, max |delta|) of each head (backward)
+  int nch;           // query chunks of CHUNK rows per head
   int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3];
   int B, Lq, Lk, Hq, Hkv, G;
   float scale;       // softmax scale
@@ -75,6 +88,21 @@ struct KArgs {
   const int* q_order;
   const int* kv_order;
 };
+
+// Power of two s with m * s in [2^(top-1), 2^top) for finite m > 0 (1 otherwise).
+__device__ __forceinline__ float pow2_scale(float m, int top) {
+  if (!(m > 0.f) || !(m <= 3.4e38f)) return 1.f;
+  int e;
+  frexpf(m, &e);  // m in [2^(e-1), 2^e)
+  return ldexpf(1.f, min(126, max(-126, top - e)));
+}
+
+// Scale f of the float16 dS of a sub-block: |dS| <= bound (in the units dS
+// is computed in) keeps |dS * f| < 2^14, and f <= 2^15 keeps f * P (P <= 1)
+// inside float16 too.
+__device__ __forceinline__ float ds_scale(float bound) {
+  return fminf(pow2_scale(bound, 14), 32768.f);
+}
 
 struct bf16_tag {};
 struct f16_tag {};
@@ -396,6 +424,76 @@ __device__ __forceinline__ int opaque(int x) {
 
 __device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int t) {
   return ((a.map_b == 1 ? 0 : b) * a.map_h + (a.map_h == 1 ? 0 : h)) * n + t;
+}
+
+// One 128-row tile of a 16-bit [rows, D] tensor held by 512 threads, 4 per row
+// (thread t: row t / 4, 16-byte chunks CPL * (t % 4) .. + CPL - 1), and its
+// conversion to float16 times a power of two: tile_load, then tile_scale
+// (the tile's max |x| and scale, one workgroup barrier), then tile_f16.
+template <int D>
+struct TileRows {
+  static constexpr int CPL = D / 32;  // 16-byte chunks per thread
+  u32x4 x[CPL];
+};
+
+// Rows r >= n are zero.  src points at row 0; rs is the row stride in elements.
+template <int D>
+__device__ __forceinline__ void tile_load(TileRows<D>& t, const uint16_t* src, int64_t rs, int n) {
+  const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
+#pragma unroll
+  for (int j = 0; j < TileRows<D>::CPL; ++j) t.x[j] = u32x4{0u, 0u, 0u, 0u};
+  if (r < n) {
+    const uint16_t* p = src + (int64_t)r * rs + 8 * TileRows<D>::CPL * part;
+#pragma unroll
+    for (int j = 0; j < TileRows<D>::CPL; ++j) t.x[j] = *(const u32x4*)(p + 8 * j);
+  }
+}
+
+// max |x| over this thread's values of each of two tiles
+template <int D, class Tag>
+__device__ __forceinline__ f32x2 tile_absmax2(const TileRows<D>& t0, const TileRows<D>& t1) {
+  using E = Elt<Tag>;
+  f32x2 m = {0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < TileRows<D>::CPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      m[0] = fmaxf(m[0], fabsf(E::to_f32(elt16(t0.x[j], e))));
+      m[1] = fmaxf(m[1], fabsf(E::to_f32(elt16(t1.x[j], e))));
+    }
+  return m;
+}
+
+// maximum over the 512 threads of a workgroup (red: 8 entries; one barrier
+// before the write guards a previous use of red)
+__device__ __forceinline__ f32x2 block_max2_512(f32x2 x, f32x2* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    x[0] = fmaxf(x[0], __shfl_xor(x[0], o));
+    x[1] = fmaxf(x[1], __shfl_xor(x[1], o));
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  f32x2 r = red[0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) {
+    r[0] = fmaxf(r[0], red[w][0]);
+    r[1] = fmaxf(r[1], red[w][1]);
+  }
+  return r;
+}
+
+// float16 x * s of chunk j (s a power of two: exact for bfloat16 and float16
+// values whose product stays in float16's range)
+template <class Tag>
+__device__ __forceinline__ u32x4 chunk_f16(const u32x4& x, float s) {
+  using E = Elt<Tag>;
+  using H = Elt<f16_tag>;
+  u32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = H::pack2(E::to_f32(elt16(x, 2 * e)) * s, E::to_f32(elt16(x, 2 * e + 1)) * s);
+  return y;
 }
 
 }  // namespace mattn

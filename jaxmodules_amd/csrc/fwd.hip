@@ -1,16 +1,22 @@
 // Forward pass of the masked attention (the custom_vjp primal,
 // /root/reference/jaxmodules/attention.py:180-241, per-tile maths :52-105).
 //
-// One workgroup (4 waves) owns a 128-query map row of one (b, h) and walks the
-// row's present key tiles from the block map; fully masked tiles are never
-// visited.  Each wave owns 32 queries and computes, per 64-key sub-block,
-//     S^T = K Q^T        (MFMA, K from LDS, Q^T kept in registers)
+// cvt_v first writes V as float16 times a power of two per 128-key tile
+// (vh, vsc).  Then one workgroup (4 waves) owns a 128-query map row of one
+// (b, h) and walks the row's present key tiles from the block map; fully
+// masked tiles are never visited.  Each wave owns 32 queries and computes, per
+// 64-key sub-block,
+//     S^T = K Q^T        (MFMA in the input dtype, K from LDS, Q^T in registers)
 //     online softmax     (each lane owns one query, so the row max needs one
 //                         cross-lane exchange and the row sum none)
-//     O^T += V^T P^T     (MFMA, V^T by transposed reads of the V tile)
-// K and V are double-buffered in LDS; the next sub-block's global loads are
-// in flight while the current one is computed.  K and V tiles are moved by
-// direct global->LDS loads into swizzled row-major tiles; V^T operands are
+//     O^T += V'^T P^T    (float16 MFMA, V'^T by transposed reads of the V' tile)
+// P enters the product rounded to float16 (11 significant bits; bfloat16's 8
+// leave O and the backward's delta = rowsum(dO * O) outside the 2e-3 gate on
+// unit-variance inputs), and the row sum adds up exactly those rounded values,
+// so that O is the exact attention output for the weights P / sum(P).
+// K and V' are double-buffered in LDS; the next sub-block's global loads are
+// in flight while the current one is computed.  K and V' tiles are moved by
+// direct global->LDS loads into swizzled row-major tiles; V'^T operands are
 // read with the transposing LDS read.  The operand reads are pipelined by hand
 // (asm LDS reads 3 and 4 k-steps ahead of their MFMAs, counted lgkmcnt
 // waits), and the output rows leave through an LDS-staged tile, 16 bytes per
@@ -21,10 +27,34 @@
 
 namespace mattn {
 
+// V -> vh = float16 V * vsc[tile], one workgroup of 512 threads per
+// (b, kv head, 128-key tile); rows past Lk are zero.
+template <int D, class Tag>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
+void cvt_v(KArgs a) {
+  __shared__ f32x2 red[8];
+  const int kt = blockIdx.x % a.nkt, bh = blockIdx.x / a.nkt;
+  const int hk = bh % a.Hkv, b = bh / a.Hkv;
+  const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
+  TileRows<D> t;
+  tile_load<D>(t, (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)(kt * TILE) * a.vs[1] +
+                      (int64_t)hk * a.vs[2], a.vs[1], a.Lk - kt * TILE);
+  const f32x2 m = block_max2_512(tile_absmax2<D, Tag>(t, t), red);
+  const float s = pow2_scale(m[0], 14);
+  uint16_t* dst = a.vh + ((int64_t)bh * a.nkt * TILE + kt * TILE + r) * D + 8 * TileRows<D>::CPL * part;
+#pragma unroll
+  for (int j = 0; j < TileRows<D>::CPL; ++j) *(u32x4*)(dst + 8 * j) = chunk_f16<Tag>(t.x[j], s);
+  if (threadIdx.x == 0) {
+    a.vsc[blockIdx.x] = s;
+    a.vmax[blockIdx.x] = m[0];
+  }
+}
+
 template <int D, class Tag, bool OUT_F32>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
   using E = Elt<Tag>;
+  using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
   constexpr int BN = 64;             // keys per sub-block
   constexpr int NKD = D / 16;        // k-steps of S^T over the head dimension
@@ -67,12 +97,14 @@ void fwd_mfma(KArgs a) {
   }
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-  const uint16_t* vb = (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
+  // float16 V' rows of this kv head: dense, row stride D, padded to whole tiles
+  const uint16_t* vb = a.vh + (int64_t)(b * a.Hkv + hk) * a.nkt * TILE * D;
+  const float* vsc = a.vsc + (b * a.Hkv + hk) * a.nkt;
   uint32_t kld[NI], vld[NI];  // loop-invariant source byte offsets of this lane's load slots
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     kld[i] = 2 * TL::src_off(NI * wave + i, lane, a.ks[1]);
-    vld[i] = 2 * TL::src_off(NI * wave + i, lane, a.vs[1]);
+    vld[i] = 2 * TL::src_off(NI * wave + i, lane, D);
   }
   // LDS operand addresses, formed per use from lane seeds (element offsets):
   //   K row read, chunk 2 kd + hi of row r:  r D + ((16 kd) ^ rx),  rx = 8 hi ^ 8 swz(r)
@@ -89,6 +121,7 @@ void fwd_mfma(KArgs a) {
   // anyway), launch() issues the loads after the barrier, once the buffer
   // they fill is free.
   int nkey0 = 0, nmask = -1;  // first key and mask id of the prepared sub-block
+  float nnu = 1.f;            // V' scale of the prepared sub-block's tile
   // K / V tile loads of the next sub-block on the fast path, set up by
   // launch() and issued by the step, one per S k-step, as in dK/dV.  Issued
   // together they held each wave ~800 cycles in launch() (per-wave s_memtime
@@ -108,6 +141,7 @@ void fwd_mfma(KArgs a) {
     int kt;
     ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
     nkey0 = kt * TILE + (s & 1) * BN;
+    nnu = vsc[kt];
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
     constexpr int BUF = decltype(bufc)::value;
@@ -122,14 +156,14 @@ void fwd_mfma(KArgs a) {
     if (key0 + BN <= a.Lk) {  // the step issues the 2 NI tile loads
       dma_on = true;
       dma_kp = (const char*)(kb + (int64_t)key0 * a.ks[1]);
-      dma_vp = (const char*)(vb + (int64_t)key0 * a.vs[1]);
-    } else {  // ragged last sub-block: rows past Lk re-read row Lk-1 (masked anyway)
+      dma_vp = (const char*)(vb + (int64_t)key0 * D);
+    } else {  // ragged last sub-block: K rows past Lk re-read row Lk-1 (masked anyway); V' is padded
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int key = min(key0 + TL::row_of(NI * wave + i, lane), a.Lk - 1);
         const int c = TL::chunk_of(NI * wave + i, lane);
         lds_load16(kb + (int64_t)key * a.ks[1] + 8 * c, kl + i * BLK);
-        lds_load16(vb + (int64_t)key * a.vs[1] + 8 * c, vl + i * BLK);
+        lds_load16((const char*)(vb + (int64_t)key0 * D) + vld[i], vl + i * BLK);
       }
     }
   };
@@ -138,8 +172,9 @@ void fwd_mfma(KArgs a) {
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
   float m2 = NEG_INF, l = 0.f;  // running max (base-2 units) and partial row sum
+  float nu = 1.f;               // V' scale the accumulators are in: acc = nu * sum P V
 
-  auto step = [&](auto bufc, bool masked) {
+  auto step = [&](auto bufc, bool masked, float snu) {
     constexpr int BUF = decltype(bufc)::value;
     // operand reads pipelined by hand (asm LDS reads issued PS / PV steps ahead
     // of their MFMAs, counted lgkmcnt waits); V sits BN * D elements after K
@@ -189,24 +224,30 @@ void fwd_mfma(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
     const float mx2 = wave_max32(mx) * c2;
-    if (__any(mx2 > m2 + RESCALE_SLACK)) {
+    // a new V' tile scale (uniform) is folded into the same rescale
+    if (snu != nu || __any(mx2 > m2 + RESCALE_SLACK)) {
       const float mn = fmaxf(m2, mx2);
       const float alpha = (mn == NEG_INF) ? 1.f : fast_exp2(m2 - mn);
       l *= alpha;
+      const float aa = alpha * (snu / nu);  // powers of two: exact
 #pragma unroll
-      for (int i = 0; i < NMD; ++i) acc[i] *= alpha;
+      for (int i = 0; i < NMD; ++i) acc[i] *= aa;
       m2 = mn;
+      nu = snu;
     }
     const float nmu = (m2 == NEG_INF) ? 0.f : -m2;
     u32x4 pk[4];
+    const f16x2 one2 = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(fmaf(st[t][r], c2, nmu));
         const float p1 = fast_exp2(fmaf(st[t][r + 1], c2, nmu));
-        l += p0 + p1;
-        pk[2 * t + (r >> 3)][(r & 7) >> 1] = E::pack2(p0, p1);
+        const uint32_t w = H::pack2(p0, p1);
+        // the row sum of the rounded values the product uses (v_dot2_f32_f16)
+        l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one2, l, false);
+        pk[2 * t + (r >> 3)][(r & 7) >> 1] = w;
       }
     }
     // O^T += V^T P^T, V^T operands by transposed reads of the row-major V tile;
@@ -227,7 +268,7 @@ void fwd_mfma(KArgs a) {
         lgkm_wait<2 * (i + PV < 4 * NMD ? PV : 4 * NMD - 1 - i)>();
         hold(lo[sl]);
         hold(up[sl]);
-        acc[mt] = E::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[ks], acc[mt]);
+        acc[mt] = H::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[ks], acc[mt]);
         hold(acc[mt]);
       });
     }
@@ -237,11 +278,12 @@ void fwd_mfma(KArgs a) {
   // the loop is unrolled by two so that every buffer index is static
   auto iter = [&](int s, auto bufc) {
     const bool masked = nmask >= 0;  // sub-block s, prepared one iteration ago
+    const float snu = nnu;
     if (s + 1 < nsb) prep(s + 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, masked);
+    step(bufc, masked, snu);
   };
   if (nsb > 0) {
     prep(0);
@@ -255,7 +297,7 @@ void fwd_mfma(KArgs a) {
   }
 
   l = wave_sum32(l);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = l > 0.f ? 1.f / (l * nu) : 0.f;
   if (hi == 0 && q < a.Lq)
     a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
   // O through LDS (one K / V buffer per wave, free once every wave is done)
@@ -368,6 +410,7 @@ void fwd_simt(KArgs a) {
 
 template <int D, class Tag>
 static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStream_t st) {
+  hipLaunchKernelGGL((cvt_v<D, Tag>), dim3(a.B * a.Hkv * a.nkt), dim3(512), 0, st, a);
   if (out_f32)
     hipLaunchKernelGGL((fwd_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
   else

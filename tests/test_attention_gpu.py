@@ -1,9 +1,12 @@
 """GPU parity: the HIP path (through the C ABI) against the fp64 oracle.
 
 Inputs are seeded, rounded to the kernel dtype once, and the oracle runs on
-those exact values.  Tolerances are the parity gates of the north star:
-|a - b| <= 2e-3 + 2e-3 |b| for 16-bit O and gradients, 1e-5 for float32.
+those exact values, under the parity gate of tests/helpers.py (the north
+star's 2e-3 + 2e-3 |b| for 16-bit O and gradients, 1e-5 for float32; half an
+output ulp where that is coarser).
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -190,3 +193,31 @@ def test_deterministic():
         outs.append([o.detach(), q.grad, k.grad, v.grad])
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_reference_custom_kernel(dtype):
+    """The reference's test_masked_attention_different_kernel
+    (test_mapped_attention.py:1122-1144): kernel exp(q.k / (2 sqrt(d))) on
+    N(0, 1) inputs of shape [8, 4, 16], here against the oracle at scale
+    1 / (2 sqrt(d)), forward and backward; and, as there, the result differs
+    from the default kernel's."""
+    import jaxmodules_amd as jm
+
+    def custom_kernel(q, k):
+        return np.exp(np.dot(q, k) / (2 * np.sqrt(k.shape[-1])))
+
+    N, Hq, d = 8, 4, 16
+    rng = np.random.default_rng(42)
+    Q, K, V, dO = (rng.standard_normal((N, Hq, d)).astype(np.float32) for _ in range(4))
+    td = getattr(torch, dtype)
+    q, k, v = (torch.from_numpy(x).to("cuda", td).requires_grad_() for x in (Q, K, V))
+    o = jm.masked_attention_via_map(q, k, v, kernel_fn=custom_kernel)
+    Qr, Kr, Vr = (x.detach().float().cpu().numpy() for x in (q, k, v))
+    O_ref, _, g_ref, _ = oracle(Qr, Kr, Vr, dO, {}, scale=1 / (2 * math.sqrt(d)))
+    assert_close(o.detach().float().cpu().numpy(), O_ref, dtype, "O", "float32")
+    o.backward(torch.from_numpy(dO).to("cuda"))
+    for name, t, r in (("dQ", q, g_ref[0]), ("dK", k, g_ref[1]), ("dV", v, g_ref[2])):
+        assert_close(t.grad.float().cpu().numpy(), r, dtype, name)
+    o_def = jm.masked_attention_via_map(q.detach(), k.detach(), v.detach())
+    assert not torch.allclose(o.detach(), o_def, rtol=1e-2)

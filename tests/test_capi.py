@@ -124,25 +124,56 @@ def test_validate_blockmap(lib):
 
 
 def test_workspace_bytes(lib):
-    p = _problem()
-    rows = 2 * 8 * 300
+    """The documented layouts: backward = delta, then (16-bit inputs) the
+    partial maxima, per-head scales and bounds, float16 dO' and Q' padded to
+    whole 128-row tiles per head, float16 K' and V' per kv-head tile, and
+    three per-tile float arrays; forward = V' and two per-tile float arrays."""
     align = lambda x: (x + 255) // 256 * 256
-    n = lib.mattn_workspace_bytes(ctypes.byref(p))
-    # delta + partial maxima + scale + two 16-bit copies of dO (float16 scaled, bfloat16)
-    assert n >= rows * 4 + 2 * rows * 128 * 2
+    B, L, Hq, Hkv, D = 2, 300, 8, 2, 128
+    heads, nch, nqt, tiles = B * Hq, -(-L // 256), -(-L // 128), B * Hkv * -(-L // 128)
+    want = (align(heads * L * 4) + align(heads * nch * 8) + 2 * align(heads * 8)
+            + 2 * align(heads * nqt * 128 * D * 2) + 2 * align(tiles * 128 * D * 2)
+            + 3 * align(tiles * 4))
+    p = _problem()
+    assert lib.mattn_workspace_bytes(ctypes.byref(p)) == want
     p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
-    # bfloat16 inputs add the bfloat16 dO copy and its delta
-    assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == n - align(rows * 128 * 2) - align(rows * 4)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == want
+    p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p32)) == align(heads * L * 4)
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == align(tiles * 128 * D * 2) + 2 * align(tiles * 4)
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p32)) == 0
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
+
+
+def test_heads_major_long_sequences_validate(lib):
+    """Heads-major views (flex_attention's layout) with Hq * Lq * D >= 2^31: the
+    float16 dO' and Q' copies are head-major with one buffer resource per head,
+    so only one head's copy must fit 32-bit byte offsets."""
+    Hq, L, D = 128, 262144, 128
+    p = _problem(B=1, Lq=L, Lk=L, Hq=Hq, Hkv=Hq)
+    hm = (ctypes.c_int64 * 3)(Hq * L * D, D, L * D)          # [B, H, L, D] memory, BLHD view
+    for name in ("q", "k", "v", "dq", "dk", "dv", "o", "do"):
+        setattr(p, f"{name}_stride", hm)
+    assert Hq * L * D * 2 >= 2 ** 31
+    assert _validate(lib, p) == 0
+    # one head's float16 copy past 2^31 bytes is refused
+    L2 = 2 ** 23
+    p2 = _problem(B=1, Lq=L2, Lk=128, Hq=1, Hkv=1)
+    for name in ("q", "dq", "o", "do"):
+        setattr(p2, f"{name}_stride", (ctypes.c_int64 * 3)(L2 * D, D, D))
+    for name in ("k", "v", "dk", "dv"):
+        setattr(p2, f"{name}_stride", (ctypes.c_int64 * 3)(128 * D, D, D))
+    assert _validate(lib, p2) == -8
 
 
 def test_entry_points_reject_before_launch(lib):
     """Error paths return codes without touching the GPU (no device here)."""
     p = _problem(D=96)
-    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None)
+    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None, None)
     assert rc == -3
     p = _problem()
-    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None)
+    rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None, None)
     assert rc == -1
     rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 11))
     assert rc == -1

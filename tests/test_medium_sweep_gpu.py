@@ -2,9 +2,10 @@
 drawn from 500-2500 (several 128-row tiles per column and row, ragged ends),
 GQA, D 64 or 128, bfloat16 or float16, block size 64 or 128, and one mask
 family per draw: causal, causal sliding window, packed documents, no mask,
-per-head tile table.  The five committed draws cover lengths 649-1548 and up
-to eight (b, head) groups.  Same gate as the small sweep (2e-3 + 2e-3 |b| +
-half an output ulp)."""
+per-head tile table.  The committed draws cover lengths 649-1548 and up to
+eight (b, head) groups: seeds 0-4, and seed 12 of a one-off 40-problem run,
+whose float16 document problem left one dV element 0.2% past the gate with
+the kernels' earlier operands.  Same gate as the small sweep (tests/helpers.py)."""
 import numpy as np
 import pytest
 
@@ -47,7 +48,7 @@ def draw(seed):
     return dict(shape=(B, N, N, Hq, Hkv, d), kw=kw, dtype=dtype, fam=fam)
 
 
-@pytest.mark.parametrize("seed", range(5))
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 12])
 def test_medium_problem(seed):
     import jaxmodules_amd as jm
 

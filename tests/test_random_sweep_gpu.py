@@ -1,18 +1,17 @@
 """A seeded random sweep of problem shapes and masks: the HIP path against the
-fp64 oracle under the parity gate (2e-3 + 2e-3 |b| + half an output ulp for
-16-bit inputs).  Each case draws batch size, query/key lengths (1..400, often
-ragged), GQA layout, head dim (16..128, padded to 64/128 by the host),
-dtype, block size, kernel function, output dtype and one mask family:
-causal, none, an element window with the reference's block window, packed
-documents, a per-head tile table, a head-specific lambda, or cross lengths.
-The draw is fixed by the seed, so every run checks the same 24 problems.
+fp64 oracle under the parity gate of tests/helpers.py.  Each case draws batch
+size, query/key lengths (1..400, often ragged), GQA layout, head dim
+(16..128, padded to 64/128 by the host), dtype, block size, kernel function,
+output dtype and one mask family: causal, none, an element window with the
+reference's block window, packed documents, a per-head tile table, a
+head-specific lambda, or cross lengths.  The draw is fixed by the seed, so
+every run checks the same problems: seeds 0-23, and the draws of a one-off
+600-problem run (seeds 24-623) that failed the gate with the kernels' earlier
+bfloat16 dS / dO operands (KNOWN_DRAWS).
 
-threshold_kernel is a softmax with scale 1 instead of 1/sqrt(d); its cases
-take Q and K scaled by a further d^-0.25, so their logits spread like the
-default kernel's.  At unit-variance logits with scale 1 (seven times sharper at
-d = 48) the bfloat16 rounding of dO and dS in the dQ products reaches 3e-3
-norm-relative, beyond the element-wise gate; test_threshold_kernel_fp32 checks
-the scale-1 path exactly in float32."""
+threshold_kernel is a softmax with scale 1 instead of 1/sqrt(d), so its
+draws see logits of unit variance (Q, K ~ N(0,1) d^-0.25), seven times
+sharper than the default kernel's at d = 48."""
 import numpy as np
 import pytest
 
@@ -69,8 +68,7 @@ def draw(seed):
     return dict(shape=(B, N, L, Hq, Hkv, d), kw=kw, dtype=dtype, out=out, fam=fam)
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_problem(seed):
+def run_draw(seed):
     import jaxmodules_amd as jm
 
     c = draw(seed)
@@ -78,8 +76,6 @@ def test_random_problem(seed):
     print(f"[sweep] seed={seed} {c['fam']} shape={c['shape']} dtype={c['dtype']} out={c['out']} "
           f"kw={ {k: v for k, v in c['kw'].items() if k != 'mask_fn'} }", flush=True)
     Q, K, V, dO = seeded_inputs(B, N, L, Hq, Hkv, d, seed)
-    if "kernel_fn" in c["kw"]:
-        Q, K = Q * d ** -0.25, K * d ** -0.25
     td = getattr(torch, c["dtype"])
     q = torch.from_numpy(Q).to("cuda", td).requires_grad_()
     k = torch.from_numpy(K).to("cuda", td).requires_grad_()
@@ -95,6 +91,35 @@ def test_random_problem(seed):
     for name, t, r in (("dQ", q, g_ref[0]), ("dK", k, g_ref[1]), ("dV", v, g_ref[2])):
         assert_close(t.grad.float().cpu().numpy(), r, c["dtype"], name)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_problem(seed):
+    run_draw(seed)
+
+
+# Draws of seeds 24-623 that failed the gate with bfloat16 dS (dK, dQ) and
+# dO (dQ) operands, every one a bfloat16 threshold_kernel problem.
+KNOWN_DRAWS = [25, 31, 94, 100, 118, 165, 196, 226, 231, 311, 332, 444, 478, 590]
+
+
+# With every operand in float16 (and O's weights summed as rounded), 11 of
+# them pass; the other three exceed the gate in single elements of dK / dV
+# whose sums of float16-rounded products cancel.  The CPU model of the
+# kernels' roundings (tests/test_rounding_model.py) reproduces them: the
+# floor of 16-bit matrix-core operands, not a kernel error.
+FLOOR = {
+    31: "1 dK element of 493056 at 1.007x the bound (float16 operand floor)",
+    94: "1 dV element of 92160 at 1.004x the bound (float16 operand floor)",
+    118: "dK/dV of 4 keys summed over 236 queries cancel to ~0.1 (54 of 3072 elements, "
+         "1.5x; float16 operand floor)",
+}
+
+
+@pytest.mark.parametrize("seed", [pytest.param(s, marks=pytest.mark.xfail(strict=True, reason=FLOOR[s]))
+                                  if s in FLOOR else s for s in KNOWN_DRAWS])
+def test_known_draw(seed):
+    run_draw(seed)
 
 
 def test_draws_cover_every_family():
