@@ -6,23 +6,30 @@ positions), and its fraction of the bf16 dense MFMA peak.
 
 A step is one forward + backward pass (mattn_fwd, then the three mattn_bwd
 stages) over one batch of synthetic bf16 inputs resident in HBM.  The
-workload is BASELINE configs[1] (causal, bf16, B=4, L=4096, H=32, d=128,
-block 128); the north-star target shape (B=1, L=8192, H=32, d=128, causal) is
-measured the same way and reported under "target".
+headline workload is the north star's target shape (causal, bf16, B=1,
+L=8192, H=32, d=128, block 128; the 40% bar is quoted on it); the other
+BASELINE configurations are measured the same way in the same run and
+reported under "configs": cfg2 (B=4 L=4096 H=32), cfg3 (sliding window),
+cfg4 (block-sparse, its tile map built by create_block_mask and
+BlockMask.tile_map as BASELINE words it), cfg5 (packed documents) and the
+target shape with 8 KV heads (GQA).
 
-The dominant kernel's time is measured with HIP events on the stream the
-kernels run on (torch's current stream, which the C ABI launches on).
-The CPU baseline is the restatement of the reference algorithm in
-oracle/attention_oracle.py (blockwise, dense per-tile mask, no tile skipping,
-per-query-block recompute in the backward pass), timed on a bounded sample of
-query blocks of one (batch, head) slice and scaled by the exact block count.
+Each kernel's time is measured with HIP events on the stream the kernels run
+on (torch's current stream, which the C ABI launches on).  The CPU baseline
+is the restatement of the reference algorithm in oracle/attention_oracle.py
+(blockwise, dense per-tile mask, no tile skipping, per-query-block recompute
+in the backward pass), timed on a bounded sample of query blocks of one
+(batch, head) slice and scaled by the exact block count.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|target|cfg3|cfg4|cfg5]
-                       [--no-target] [--no-cpu] [--copy-probe]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+                       [--only] [--no-cpu] [--copy-probe] [--tilemap]
+  --config NAME  headline workload: target (default), cfg2, cfg3, cfg4, cfg5, target_gqa
+  --only         measure the headline workload alone
 
 roofline.traffic is read from profiles/traffic_<config>.md (rocprofv3
 FETCH_SIZE and WRITE_SIZE of the dominant kernel, calibrated on the 1 GiB copy
-that --copy-probe launches); null when that file is absent.
+that --copy-probe launches) and stamped with the commit that file records;
+null when that file is absent.
 """
 from __future__ import annotations
 
@@ -43,23 +50,39 @@ PEAK_HBM_GBS = 8000.0
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: one int64 device copy of this size (PMC calibration)
 # kernel symbol of each timed stage (for the rocprofv3 counter summaries)
 SYMBOL = {"fwd": "fwd_mfma", "bwd_dkdv": "bwd_dkdv_mfma", "bwd_dq": "bwd_dq_mfma"}
+EXTRA = ["cfg2", "cfg3", "cfg4", "cfg5", "target_gqa"]
 
 
 def measured_traffic(config, stage):
-    """HBM bytes per launch of ``stage`` from the committed rocprofv3 counter
-    summary of this workload (FETCH_SIZE + WRITE_SIZE, scaled by the copy-probe
-    calibration); None when there is none."""
+    """(HBM bytes per launch of ``stage``, commit of the measured build) from the
+    committed rocprofv3 counter summary of this workload (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-probe calibration); (None, None) when there
+    is none."""
     import re
 
     path = os.path.join(ROOT, "profiles", f"traffic_{config}.md")
     if not os.path.exists(path):
-        return None
+        return None, None
     pat = re.compile(r"^traffic\[(\w+)\]\s*=\s*(\d+)\s*$")
+    commit, val = None, None
     for line in open(path):
         m = pat.match(line.strip())
         if m and m.group(1) == SYMBOL.get(stage):
-            return int(m.group(2))
-    return None
+            val = int(m.group(2))
+        c = re.match(r"^commit:\s*(\w+)", line.strip())
+        if c:
+            commit = c.group(1)
+    return val, commit
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _docs(L, seed, mean=2048, minlen=64):
@@ -101,28 +124,53 @@ def closed_form_mask(name):
 
 
 def workload(name):
-    """(B, L, H, d, kwargs, description) of a BASELINE configuration."""
+    """(B, L, Hq, Hkv, d, kwargs, description) of a BASELINE configuration."""
     if name == "cfg2":
-        return 4, 4096, 32, 128, dict(is_causal=True, block_size=128), \
+        return 4, 4096, 32, 32, 128, dict(is_causal=True, block_size=128), \
             "cfg2: causal bf16 B=4 L=4096 H=32 d=128 block 128, fwd+bwd"
     if name == "target":
-        return 1, 8192, 32, 128, dict(is_causal=True, block_size=128), \
+        return 1, 8192, 32, 32, 128, dict(is_causal=True, block_size=128), \
             "target: causal bf16 B=1 L=8192 H=32 d=128 block 128, fwd+bwd"
+    if name == "target_gqa":
+        return 1, 8192, 32, 8, 128, dict(is_causal=True, block_size=128), \
+            "target_gqa: causal bf16 B=1 L=8192 Hq=32 Hkv=8 d=128 block 128, fwd+bwd"
     if name == "cfg3":
-        return 2, 16384, 16, 128, dict(mask_fn=lambda b, h, q, k: (q >= k) & (q - k <= 512),
-                                       window_size=(512, 0), block_size=128), \
+        return 2, 16384, 16, 16, 128, dict(mask_fn=lambda b, h, q, k: (q >= k) & (q - k <= 512),
+                                           window_size=(512, 0), block_size=128), \
             "cfg3: sliding window (q>=k)&(q-k<=512), window (512,0), bf16 B=2 L=16384 H=16 d=128"
     if name == "cfg4":
         H, tbl = 32, _cfg4_tiles()
         mask = lambda b, h, q, k: tbl[h, q // 128, k // 128] & ((q // 128 != k // 128) | (q >= k))
-        return 1, 8192, H, 64, dict(mask_fn=mask, block_size=128), \
+        return 1, 8192, H, H, 64, dict(mask_fn=mask, block_size=128), \
             "cfg4: per-head random 128x128 tiles at 25% (full grid), diagonal causal, bf16 B=1 L=8192 H=32 d=64"
     if name == "cfg5":
         doc = _cfg5_docs()
         mask = lambda b, h, q, k: (doc[q] == doc[k]) & (q >= k)
-        return 1, 32768, 8, 128, dict(mask_fn=mask, block_size=128), \
+        return 1, 32768, 8, 8, 128, dict(mask_fn=mask, block_size=128), \
             f"cfg5: packed documents ({doc.max() + 1} docs, geometric mean 2048, min 64) & causal, bf16 B=1 L=32768 H=8 d=128"
     raise SystemExit(f"unknown config {name}")
+
+
+def tile_map_of(name):
+    """(tile map, seconds, how) for a workload: cfg4 through create_block_mask
+    and BlockMask.tile_map (block_mask.py:454-498, as BASELINE words cfg4);
+    cfg3 and cfg5 from their closed-form masks on the GPU classifier; the
+    causal shapes from is_causal (also on the GPU)."""
+    from jaxmodules_amd import attention as A
+    from jaxmodules_amd.block_mask import create_block_mask
+
+    B, L, Hq, Hkv, d, kw, _ = workload(name)
+    t0 = time.perf_counter()
+    if name == "cfg4":
+        bm = create_block_mask(kw["mask_fn"], B, Hq, L, L, 128)
+        tm = bm.tile_map(B, Hq, Hkv)
+        how = "create_block_mask + BlockMask.tile_map"
+    else:
+        if name in ("cfg3", "cfg5"):
+            kw = dict(kw, mask_fn=closed_form_mask(name))
+        _, tm = A.trace_call((B, L, Hq, d), (B, L, Hkv, d), (B, L, Hkv, d), device="cuda:0", **kw)
+        how = "GPU tile classifier"
+    return tm, time.perf_counter() - t0, how
 
 
 class Runner:
@@ -136,34 +184,33 @@ class Runner:
 
         self.torch, self.A, self._lib = torch, A, _lib
         self.lib = _lib.load()
-        B, L, H, d, kw, desc = workload(name)
+        B, L, Hq, Hkv, d, kw, desc = workload(name)
         self.desc, self.d = desc, d
-        t0 = time.perf_counter()
-        plan, tm = A.trace_call((B, L, H, d), (B, L, H, d), (B, L, H, d), **kw)
-        self.trace_s = time.perf_counter() - t0
-        self.tm = tm
+        self.tm, self.trace_s, self.trace_how = tile_map_of(name)
+        tm = self.tm
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         f = d ** -0.25
         bf = torch.bfloat16
-        self.q = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
-        self.k = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
-        self.v = (torch.randn((B, L, H, d), generator=g, device=dev) * f).to(bf)
-        self.do = torch.randn((B, L, H, d), generator=g, device=dev)           # float32, like O
-        self.o = torch.empty((B, L, H, d), dtype=torch.float32, device=dev)
-        self.lse = torch.empty((B, H, L), dtype=torch.float32, device=dev)
+        self.q = (torch.randn((B, L, Hq, d), generator=g, device=dev) * f).to(bf)
+        self.k = (torch.randn((B, L, Hkv, d), generator=g, device=dev) * f).to(bf)
+        self.v = (torch.randn((B, L, Hkv, d), generator=g, device=dev) * f).to(bf)
+        self.do = torch.randn((B, L, Hq, d), generator=g, device=dev)          # float32, like O
+        self.o = torch.empty((B, L, Hq, d), dtype=torch.float32, device=dev)
+        self.lse = torch.empty((B, Hq, L), dtype=torch.float32, device=dev)
         self.dq = torch.empty_like(self.q)
         self.dk = torch.empty_like(self.k)
         self.dv = torch.empty_like(self.v)
         self.p = A._problem(self.q, self.k, self.v, self.o, 1.0 / d ** 0.5, do=self.do, dq=self.dq,
                             dk=self.dk, dv=self.dv)
+        self.p.flags = _lib.MATTN_FWD_FOR_BWD
         nws = int(self.lib.mattn_workspace_bytes(ctypes.byref(self.p)))
         self.ws = torch.empty(nws + 256, dtype=torch.uint8, device=dev)
         self.wptr = (self.ws.data_ptr() + 255) & ~255
-        nfw = int(self.lib.mattn_fwd_workspace_bytes(ctypes.byref(self.p)))
-        self.fws = torch.empty(nfw + 256, dtype=torch.uint8, device=dev)
-        self.fwptr = (self.fws.data_ptr() + 255) & ~255
+        nres = int(self.lib.mattn_fwd_workspace_bytes(ctypes.byref(self.p)))
+        self.res = torch.empty(nres + 256, dtype=torch.uint8, device=dev)
+        self.rptr = (self.res.data_ptr() + 255) & ~255
         self.bm = A.device_blockmap(tm, dev)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.pairs = tm.pairs
@@ -173,14 +220,15 @@ class Runner:
     def fwd(self):
         self._lib.check(self.lib.mattn_fwd(ctypes.byref(self.p), ctypes.byref(self.bm),
                                            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                                           self.o.data_ptr(), self.lse.data_ptr(), self.fwptr,
+                                           self.o.data_ptr(), self.lse.data_ptr(), self.rptr,
                                            self.stream), "fwd")
 
     def bwd(self, stage):
         self._lib.check(self.lib.mattn_bwd_stage(
             ctypes.byref(self.p), ctypes.byref(self.bm), stage, self.q.data_ptr(), self.k.data_ptr(),
-            self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(), self.lse.data_ptr(), self.wptr,
-            self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.stream), f"bwd stage {stage}")
+            self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(), self.lse.data_ptr(), self.rptr,
+            self.wptr, self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.stream),
+            f"bwd stage {stage}")
 
     def measure(self, steps, warmup):
         torch = self.torch
@@ -214,7 +262,7 @@ def cpu_baseline(name, budget_s=12.0):
     """The CPU restatement of the reference algorithm on a bounded sample."""
     from oracle import attention_oracle as ao
 
-    B, L, H, d, kw, _ = workload(name)
+    B, L, H, _, d, kw, _ = workload(name)
     try:
         from threadpoolctl import threadpool_info
         cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
@@ -244,6 +292,7 @@ def cpu_baseline(name, budget_s=12.0):
     t_total = t_used * scale
     flop = 14 * d * _pairs_of(name)
     return {"value": flop / t_total / 1e12, "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{n_done} query-block steps (of {nq} per (batch, head) slice, {B * H} slices), "
                       f"fwd+bwd, float32 numpy restatement of attention.py:52-342, "
                       f"{t_used:.1f} s measured, scaled x{scale:.0f}",
@@ -269,7 +318,7 @@ def tilemap_build_times(repeats=5):
     out = {"metric": "tile-map build seconds, host tracer vs GPU classifier", "unit": "s",
            "higher_is_better": False, "configs": {}}
     for name in ("cfg3", "cfg4", "cfg5"):
-        B, L, H, d, kw, desc = workload(name)
+        B, L, H, _, d, kw, desc = workload(name)
         shape = (B, L, H, d)
         t0 = time.perf_counter()
         host = bmap.trace(bmap.make_plan(shape, shape, shape, **kw))
@@ -293,13 +342,28 @@ def tilemap_build_times(repeats=5):
     return out
 
 
+def summary(r, ms, kern):
+    total = r.fwd_flop + r.bwd_flop
+    value = total / (ms * 1e-3) / 1e12
+    return value, {"workload": r.desc, "value": round(value, 2), "unit": "TFLOP/s",
+                   "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+                   "pairs": r.pairs, "flop_per_step": total,
+                   "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
+                   "fwd_tflops": round(r.fwd_flop / (kern["fwd"] * 1e-3) / 1e12, 2),
+                   "bwd_tflops": round(r.bwd_flop / ((kern["bwd_pre"] + kern["bwd_dkdv"] +
+                                                      kern["bwd_dq"]) * 1e-3) / 1e12, 2),
+                   "tile_map": {"nnz": r.tm.nnz, "full": r.tm.n_full, "partial": r.tm.n_partial,
+                                "masks": r.tm.n_masks, "built_by": r.trace_how,
+                                "build_s": round(r.trace_s, 3)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg2")
-    ap.add_argument("--no-target", action="store_true")
+    ap.add_argument("--config", default="target")
+    ap.add_argument("--only", action="store_true", help="measure the headline workload alone")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-probe", action="store_true",
@@ -330,17 +394,19 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    total = r.fwd_flop + r.bwd_flop
-    value = total / (ms * 1e-3) / 1e12
+    value, head = summary(r, ms, kern)
     # dominant kernel and its algorithmic FLOPs per launch
     alg = {"fwd": r.fwd_flop, "bwd_dkdv": 8 * r.d * r.pairs, "bwd_dq": 2 * r.d * r.pairs}
     dom = max(("fwd", "bwd_dkdv", "bwd_dq"), key=lambda n: kern[n])
     ach = alg[dom] / (kern[dom] * 1e-3) / 1e12
+    traffic, commit = measured_traffic(args.config, dom)
     roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(args.config, dom),
-            "kernel_ms": round(kern[dom], 4),
-            "flop_per_launch": alg[dom]}
+            "traffic": traffic, "traffic_profile": f"profiles/traffic_{args.config}.md @ {commit}"
+            if traffic is not None else None,
+            "kernel_ms": round(kern[dom], 4), "flop_per_launch": alg[dom]}
+    head.pop("value")
+    head.pop("unit")
     out = {
         "metric": "attn fwd+bwd TFLOP/s (unmasked FLOPs) + % bf16 MFMA peak, 1 MI355X",
         "value": round(value, 2),
@@ -354,27 +420,20 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: Q,K,V ~ N(0,1)*d^-0.25 (bf16), dO ~ N(0,1) (float32, the output dtype)",
-        "config": {"workload": r.desc, "pairs": r.pairs, "flop_per_step": total,
-                   "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
-                   "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
-                   "fwd_tflops": round(r.fwd_flop / (kern["fwd"] * 1e-3) / 1e12, 2),
-                   "bwd_tflops": round(r.bwd_flop / ((kern["bwd_pre"] + kern["bwd_dkdv"] +
-                                                      kern["bwd_dq"]) * 1e-3) / 1e12, 2),
-                   "tile_map": {"nnz": r.tm.nnz, "full": r.tm.n_full, "partial": r.tm.n_partial,
-                                "masks": r.tm.n_masks, "trace_s": round(r.trace_s, 3)}},
+        "config": head,
         "roofline": roof,
     }
-    if not args.no_target and args.config != "target":
-        del r
-        torch.cuda.empty_cache()
-        t = Runner("target")
-        tms, tk = t.measure(args.steps, args.warmup)
-        tv = (t.fwd_flop + t.bwd_flop) / (tms * 1e-3) / 1e12
-        out["target"] = {"workload": t.desc, "value": round(tv, 2), "unit": "TFLOP/s",
-                         "ms_per_step": round(tms, 4),
-                         "pct_of_bf16_peak": round(100 * tv / PEAK_BF16_TFLOPS, 2),
-                         "kernel_ms": {k: round(v, 4) for k, v in tk.items()}}
-        del t
+    del r
+    if not args.only:
+        out["configs"] = {}
+        for name in EXTRA:
+            if name == args.config:
+                continue
+            torch.cuda.empty_cache()
+            t = Runner(name)
+            tms, tk = t.measure(args.steps, args.warmup)
+            out["configs"][name] = summary(t, tms, tk)[1]
+            del t
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
         out["cpu_baseline"].pop("seconds_extrapolated", None)

@@ -58,6 +58,10 @@ enum mattn_status {
   MATTN_ERR_TOO_LARGE = -8      /* a size exceeds 32-bit index ranges          */
 };
 
+/* mattn_problem.flags: the forward also leaves in its residual the float16
+ * copy of Q that mattn_bwd reads (set it for a forward whose backward runs). */
+#define MATTN_FWD_FOR_BWD 1
+
 /* Tile size of the block map, in queries x keys. */
 #define MATTN_TILE_Q 128
 #define MATTN_TILE_K 128
@@ -68,7 +72,7 @@ typedef struct mattn_problem {
   int32_t o_dtype;   /* enum mattn_dtype of O and dO: dtype, or MATTN_F32  */
   float scale;       /* softmax scale; the reference's default_kernel uses
                         1/sqrt(D) (attention.py:39-50)                     */
-  int32_t reserved;
+  int32_t flags;     /* MATTN_FWD_FOR_BWD or 0                             */
   /* element strides {batch, sequence, head}; D is contiguous */
   int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3];
   int64_t do_stride[3], dq_stride[3], dk_stride[3], dv_stride[3];
@@ -120,40 +124,44 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
 /* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer). */
 size_t mattn_workspace_bytes(const mattn_problem* p);
 
-/* Bytes of device workspace mattn_fwd needs (256-byte aligned pointer; 0 for
- * float32 inputs).  16-bit inputs: V as float16 times a power of two per
- * 128-key tile, which the P V product reads. */
+/* Bytes of the forward's residual buffer (256-byte aligned pointer; 0 for
+ * float32 inputs): float16 copies of V and (with MATTN_FWD_FOR_BWD) Q, each
+ * times a power of two per 128-row tile, which the forward's P V product and
+ * the backward read. */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
 
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).
  *   o         : [B, Lq, Hq, D] of o_dtype
  *   lse       : [B, Hq, Lq] float32, base-2 log-sum-exp of the scaled scores
  *               (-inf for a row with no allowed key); a residual for mattn_bwd
- *   workspace : mattn_fwd_workspace_bytes(p) bytes (scratch; NULL when 0). */
+ *   residual  : mattn_fwd_workspace_bytes(p) bytes (NULL when 0), written
+ *               here; with MATTN_FWD_FOR_BWD in p->flags, mattn_bwd reads it. */
 int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* q, const void* k, const void* v,
-              void* o, float* lse, void* workspace, void* stream);
+              void* o, float* lse, void* residual, void* stream);
 
 /* Backward (replaces the custom_vjp bwd rule, attention.py:266-342).
  *   do_       : upstream gradient, [B, Lq, Hq, D] of o_dtype
  *   o, lse    : the forward's outputs
- *   workspace : mattn_workspace_bytes(p) bytes
+ *   residual  : the forward's residual buffer (16-bit inputs; that forward
+ *               ran with MATTN_FWD_FOR_BWD), read only
+ *   workspace : mattn_workspace_bytes(p) bytes (scratch)
  *   dq, dk, dv: gradients of dtype, every element written (no pre-zeroing). */
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* q, const void* k, const void* v,
-              const void* o, const void* do_, const float* lse,
+              const void* o, const void* do_, const float* lse, const void* residual,
               void* workspace, void* dq, void* dk, void* dv, void* stream);
 
 /* The three stages of mattn_bwd, in the order they must run on one stream:
- * MATTN_BWD_PRE (delta = rowsum(dO * O) and the float16 copies of dO and Q,
- * into the workspace), MATTN_BWD_DKDV (also writes the float16 copies of K and
- * V into the workspace), then MATTN_BWD_DQ (reads all of them).  mattn_bwd ==
- * the three stages in order.  Same arguments as mattn_bwd; exposed so a caller
- * can time the stages. */
+ * MATTN_BWD_PRE (delta = rowsum(dO * O) and the float16 copy of dO, into the
+ * workspace), MATTN_BWD_DKDV (also writes the float16 copy of K into the
+ * workspace), then MATTN_BWD_DQ (reads both).  mattn_bwd == the three stages
+ * in order.  Same arguments as mattn_bwd; exposed so a caller can time the
+ * stages. */
 enum mattn_bwd_stage { MATTN_BWD_PRE = 0, MATTN_BWD_DKDV = 1, MATTN_BWD_DQ = 2 };
 int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     const void* q, const void* k, const void* v,
-                    const void* o, const void* do_, const float* lse,
+                    const void* o, const void* do_, const float* lse, const void* residual,
                     void* workspace, void* dq, void* dk, void* dv, void* stream);
 
 /*

@@ -16,8 +16,9 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libmattn.so")
 
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
+MATTN_FWD_FOR_BWD = 1
 TILE_Q = TILE_K = 128
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 STATUS = {
     0: "MATTN_OK",
@@ -45,7 +46,7 @@ class MattnProblem(ctypes.Structure):
         ("B", ctypes.c_int32), ("Lq", ctypes.c_int32), ("Lk", ctypes.c_int32),
         ("Hq", ctypes.c_int32), ("Hkv", ctypes.c_int32), ("D", ctypes.c_int32),
         ("dtype", ctypes.c_int32), ("o_dtype", ctypes.c_int32),
-        ("scale", ctypes.c_float), ("reserved", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("flags", ctypes.c_int32),
         ("q_stride", _I64x3), ("k_stride", _I64x3), ("v_stride", _I64x3), ("o_stride", _I64x3),
         ("do_stride", _I64x3), ("dq_stride", _I64x3), ("dk_stride", _I64x3), ("dv_stride", _I64x3),
     ]
@@ -109,9 +110,9 @@ def load():
         lib.mattn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mattn_fwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_fwd.restype = ctypes.c_int
-        lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_bwd.restype = ctypes.c_int
-        lib.mattn_bwd_stage.argtypes = [P, M, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.mattn_bwd_stage.argtypes = [P, M, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_bwd_stage.restype = ctypes.c_int
         lib.mattn_strerror.argtypes = [ctypes.c_int]
         lib.mattn_strerror.restype = ctypes.c_char_p

@@ -256,10 +256,12 @@ def _stream(device) -> int:
 
 
 def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float32,
-                  heads_major: bool = False):
-    """O [B, N, Hq, d] (out_dtype) and base-2 LSE [B, Hq, N] via mattn_fwd.
-    ``heads_major`` lays O out in memory as [B, Hq, N, d] (the returned tensor
-    is the [B, N, Hq, d] view of it)."""
+                  heads_major: bool = False, for_backward: bool = False):
+    """(O [B, N, Hq, d] in out_dtype, base-2 LSE [B, Hq, N], residual) via
+    mattn_fwd.  ``heads_major`` lays O out in memory as [B, Hq, N, d] (the
+    returned tensor is the [B, N, Hq, d] view of it).  The residual (a uint8
+    tensor, None for float32 inputs) holds the float16 V copy and, with
+    ``for_backward``, the float16 Q copy that mattn_backward reads."""
     lib = _lib.load()
     B, N, Hq, d = q.shape
     if heads_major:
@@ -269,13 +271,14 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
     lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
     _check_map(tm, q, k)
     p = _problem(q, k, v, o, scale)
+    p.flags = _lib.MATTN_FWD_FOR_BWD if for_backward else 0
     bm = device_blockmap(tm, q.device)
     nws = int(lib.mattn_fwd_workspace_bytes(ctypes.byref(p)))
-    ws, wptr = _workspace(nws, q.device)
+    res, rptr = _workspace(nws, q.device)
     _lib.check(lib.mattn_fwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
-                             v.data_ptr(), o.data_ptr(), lse.data_ptr(), wptr, _stream(q.device)),
+                             v.data_ptr(), o.data_ptr(), lse.data_ptr(), rptr, _stream(q.device)),
                "mattn_fwd")
-    return o, lse
+    return o, lse, res
 
 
 def _workspace(nbytes: int, device):
@@ -284,11 +287,16 @@ def _workspace(nbytes: int, device):
     if nbytes == 0:
         return None, None
     ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
-    return ws, (ws.data_ptr() + 255) & ~255
+    return ws, _aligned(ws)
 
 
-def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
-    """(dQ, dK, dV) via mattn_bwd."""
+def _aligned(t):
+    return None if t is None else (t.data_ptr() + 255) & ~255
+
+
+def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None):
+    """(dQ, dK, dV) via mattn_bwd; ``res`` is mattn_forward's residual (run
+    with for_backward=True)."""
     lib = _lib.load()
     _check_map(tm, q, k)
     dq = torch.empty_like(q)
@@ -298,8 +306,8 @@ def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float):
     ws, wptr = _workspace(max(int(lib.mattn_workspace_bytes(ctypes.byref(p))), 256), q.device)
     bm = device_blockmap(tm, q.device)
     _lib.check(lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
-                             v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(), wptr,
-                             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)),
+                             v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(), _aligned(res),
+                             wptr, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)),
                "mattn_bwd")
     return dq, dk, dv
 
@@ -317,16 +325,17 @@ class _MaskedAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, tm, scale, out_dtype, heads_major=False):
-        o, lse = mattn_forward(q, k, v, tm, scale, torch.float32, heads_major)
+        grads = any(ctx.needs_input_grad[:3])
+        o, lse, res = mattn_forward(q, k, v, tm, scale, torch.float32, heads_major, for_backward=grads)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.tm, ctx.scale = tm, scale
+        ctx.tm, ctx.scale, ctx.res = tm, scale, res
         return o if out_dtype == torch.float32 else o.to(out_dtype)
 
     @staticmethod
     def backward(ctx, do):
         q, k, v, o, lse = ctx.saved_tensors
         do = _ready(do.to(o.dtype))
-        dq, dk, dv = mattn_backward(q, k, v, o, lse, do, ctx.tm, ctx.scale)
+        dq, dk, dv = mattn_backward(q, k, v, o, lse, do, ctx.tm, ctx.scale, ctx.res)
         return dq, dk, dv, None, None, None, None
 
 

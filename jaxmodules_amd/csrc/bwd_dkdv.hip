@@ -14,20 +14,21 @@ namespace mattn {
 // ---------------------------------------------------------------------------
 // 8 waves (2 per SIMD).  Wave w owns keys 32 (w % 4) .. +31 of the tile and
 // query half w / 4 of every 64-query sub-block.  With the float16 copies
-// Q' = Q r_h, dO' = dO s_h (bwd_pre) and K' = K k_t, V' = V v_t (the
-// prologue; k_t, v_t powers of two per 128-key tile):
+// Q' = Q r, V' = V v (the forward's), dO' = dO s (bwd_pre) and K' = K k (the
+// prologue), each times a power of two per 128-row tile:
 //   S'   = Q' K'^T          (A: Q' rows, B: K' rows; both from LDS)
 //   dP'  = dO' V'^T         (B: V' rows from LDS)
-//   P~   = f exp2(S' c2 / (r_h k_t) - lse)          (f: see below)
-//   dS~  = P~ (dP' / v_t - delta s_h)   = f s_h dS
+//   P~   = exp2(S' c2 / (r k) - (lse - log2 f)) = f P
+//   dS~  = P~ (dP' / v - delta s)   = f s dS
 //   dV^T += dO'^T P~      (A: transposed reads of the dO' tile)
 //   dK^T += Q'^T dS~      (A: transposed reads of the Q' tile)
-// f is a power of two that keeps |dS~| < 2^14 (ds_scale of the head bounds
-// bwd_pre left in hst and the tile's max |V|), so dS~ loses nothing to
-// float16's range; the accumulators are in units of f s_h (dV) and f s_h r_h
-// (dK), rescaled when a GQA group's walk moves to a head with other scales.
+// f is bwd_pre's power of two per query tile that keeps |dS~| < 2^14, so dS~
+// loses nothing to float16's range; bwd_pre folds it into the lse copy (lsf)
+// this kernel reads.  The accumulators are in units of f s (dV) and f s r
+// (dK) of the query tile last walked, rescaled when a tile with other scales
+// comes (rare: the scales move in steps of 2^4).
 // The K' and V' tiles of the workgroup's 128 keys stay in LDS for the whole
-// column (and are written to kh, vh for the dQ kernel); Q', dO', lse, delta
+// column (K' is also written to kh for the dQ kernel); Q', dO', lse, delta
 // and the partial-tile mask words are double-buffered and filled by direct
 // global->LDS loads.  The MFMA operand reads are pipelined by hand: asm LDS
 // reads issued two k-steps ahead of their MFMAs, with counted lgkmcnt waits.
@@ -74,14 +75,22 @@ void bwd_dkdv_mfma(KArgs a) {
   const int kloc = 32 * kg + l32;
   const float c2 = a.scale_log2;
 
-  // this thread's share of the column's K and V rows (4 threads per key row),
-  // loaded now so that the column-list reads below overlap their latency;
-  // converted to float16 once the tile maxima are known
-  TileRows<D> tkr, tvr;
+  // the forward's V' tile of the column, by direct loads into LDS, and this
+  // thread's share of its K rows (4 threads per key row), converted to
+  // float16 once the tile's max |K| is known; both issued now so that the
+  // column-list reads below overlap their latency
+  const int col = item;  // (b * Hkv + hk) * nkt + kt
+  {
+    const uint16_t* vsrc = a.vh + (int64_t)col * TILE * D;
+#pragma unroll
+    for (int i = 0; i < 2 * NS; ++i) {
+      const int n = 2 * NS * wave + i;
+      lds_load16(vsrc + (int64_t)TL::row_of(n, lane) * D + 8 * TL::chunk_of(n, lane), Vs + n * BLK);
+    }
+  }
+  TileRows<D> tkr;
   tile_load<D>(tkr, (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)(kt * TILE) * a.ks[1] +
                         (int64_t)hk * a.ks[2], a.ks[1], a.Lk - kt * TILE);
-  tile_load<D>(tvr, (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)(kt * TILE) * a.vs[1] +
-                        (int64_t)hk * a.vs[2], a.vs[1], a.Lk - kt * TILE);
 
   // Flattened walk over (query head g of the group, column entry, half).
   int tot = 0;
@@ -116,14 +125,16 @@ void bwd_dkdv_mfma(KArgs a) {
   const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
   EntryCache ec;
   int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
-  // per-head scales (s_h, r_h) of the sub-block in each buffer
+  // dO' and Q' tile scales (s, r) of the sub-block in each buffer
   float sh0 = 1.f, rh0 = 1.f, sh1 = 1.f, rh1 = 1.f;
   // buffer resources of the current query head's Q' and dO' slices
   const int64_t hrows = (int64_t)a.nqt * TILE;  // rows per head in the copies
   const uint32_t hbytes = (uint32_t)(hrows * D * 2);
   __amdgpu_buffer_rsrc_t rq, rh;
   int rh_head = -1;
-  float cur_s = 1.f, cur_r = 1.f;  // scales of the prepared sub-block's head
+  const float* qsc_h = a.qsc;  // the current query head's per-tile scales
+  const float* asc_h = a.asc;
+  float cur_s = 1.f, cur_r = 1.f;  // scales f s and r of the prepared sub-block's query tile
   // Tile loads of the next sub-block on the fast path, prepared by launch()
   // and issued by the step, one per S / dP k-step, so that the 1 KiB DMA
   // instructions of the eight waves enter the load unit behind the MFMA chains
@@ -144,7 +155,7 @@ void bwd_dkdv_mfma(KArgs a) {
   // below test wave-uniform values (scalar registers), not per-lane ones.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   int cur_qt = 0, cur_mid = -1;
-  const float* lrow = nullptr;  // lse (wave 6) or delta (wave 7) row of the current head
+  const float* lrow = nullptr;  // lse - log2 f (wave 6) or delta (wave 7) row of the current head
 
   // The next sub-block's loads in two parts: prep() advances the cursor
   // before the step's barrier (waves that reach the barrier early do it while
@@ -162,18 +173,17 @@ void bwd_dkdv_mfma(KArgs a) {
         lend = a.col_ptr[mc + 1];
         ec.reset();
       }
-      ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid);
       const int h = hk * a.G + lg;
       if (h != rh_head) {
         rh_head = h;
         const int64_t hb = ((int64_t)b * a.Hq + h) * hrows * D;
         rq = make_rsrc(a.qh + hb, hbytes);
         rh = make_rsrc(a.doh + hb, hbytes);
-        lrow = (wv == 6 ? a.lse : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq;
-        const float2 sc = a.hsc[b * a.Hq + h];
-        cur_s = sc.x;
-        cur_r = sc.y;
+        lrow = (wv == 6 ? a.lsf : a.delta) + ((int64_t)b * a.Hq + h) * a.Lq;
+        qsc_h = a.qsc + (b * a.Hq + h) * a.nqt;
+        asc_h = a.asc + (b * a.Hq + h) * a.nqt;
       }
+      ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s);
     }
     (BUF ? mid1 : mid0) = cur_mid;
     (BUF ? sh1 : sh0) = cur_s;
@@ -209,15 +219,15 @@ void bwd_dkdv_mfma(KArgs a) {
   f32x16 dk[NMD], dv[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
-  // set by the prologue: the column's K' / V' tile scales and the dS scale f
-  float ksc = 1.f, ivs = 1.f, fds = 1.f;
-  float acc_s = 1.f, acc_r = 1.f;  // head scales the accumulators are in
-  float m2c = c2;                   // c2 / (r_h k_t) of the accumulators' head
+  // set by the prologue: the column's K' / V' tile scales
+  float ksc = 1.f, ivs = 1.f;
+  float acc_s = 1.f, acc_r = 1.f;  // scales f s and r the accumulators are in
+  float m2c = c2;                   // c2 / (r k) of those scales
 
   auto step = [&](auto bufc, bool masked) {
     constexpr int BUF = decltype(bufc)::value;
-    // the sub-block's head scales (uniform); another head of the GQA group
-    // with other scales rescales the accumulators (powers of two: exact)
+    // the sub-block's dO' / Q' scales (uniform); other scales than the
+    // accumulators' rescale them (powers of two: exact)
     const float ss = BUF ? sh1 : sh0, rr = BUF ? rh1 : rh0;
     if (ss != acc_s || rr != acc_r) {
       const float fv = ss / acc_s, fk = fv * (rr / acc_r);
@@ -225,7 +235,7 @@ void bwd_dkdv_mfma(KArgs a) {
       for (int i = 0; i < NMD; ++i) { dv[i] *= fv; dk[i] *= fk; }
       acc_s = ss;
       acc_r = rr;
-      m2c = c2 / (rr * ksc);
+      m2c = c2 * pow2_rcp(rr * ksc);
     }
     const float mc = m2c;
     const float* Lb = (BUF ? L1 : L0) + 32 * qh;
@@ -273,7 +283,7 @@ void bwd_dkdv_mfma(KArgs a) {
       const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
       dv4[j] = *(const f32x4*)&Gb[8 * j + 4 * hi];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], mc, -lv[i])) * fds;
+      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], mc, -lv[i]));
     }
     asm volatile("" ::"v"(mw));  // keeps the mask-word read with the others (not sunk into the branch)
     if (masked) {
@@ -358,46 +368,24 @@ void bwd_dkdv_mfma(KArgs a) {
     dma_on = false;
   }
   {
-    // K' and V' tiles: float16 times a power of two per tile with max |x| in
-    // [2^13, 2^14) (a bfloat16 or float16 value is then exact in float16 down
-    // to 2^-17 relative to the tile's largest element), into the resident LDS
-    // tiles and to kh / vh for the dQ kernel.  4 threads per key row.
+    // K' tile: float16 times the tile's copy_scale, into the resident LDS tile
+    // and to kh for the dQ kernel.  4 threads per key row.
     constexpr int CPL = TileRows<D>::CPL;
-    const f32x2 m = block_max2_512(tile_absmax2<D, Tag>(tkr, tvr), red);
-    const float kscl = pow2_scale(m[0], 14), vscl = pow2_scale(m[1], 14);
+    const float kscl = copy_scale(block_max2_512(f32x2{tile_absmax<D, Tag>(tkr), 0.f}, red)[0]);
     const int r = tid >> 2, part = tid & 3;
-    const int64_t col = (int64_t)(b * a.Hkv + hk) * a.nkt + kt;
-    uint16_t* kd = a.kh + (col * TILE + r) * D + 8 * CPL * part;
-    uint16_t* vd = a.vh + (col * TILE + r) * D + 8 * CPL * part;
+    uint16_t* kd = a.kh + ((int64_t)col * TILE + r) * D + 8 * CPL * part;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl), yv = chunk_f16<Tag>(tvr.x[j], vscl);
+      const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl);
       *(u32x4*)&Ks[sw_off<D>(r, CPL * part + j)] = yk;
-      *(u32x4*)&Vs[sw_off<D>(r, CPL * part + j)] = yv;
       *(u32x4*)(kd + 8 * j) = yk;
-      *(u32x4*)(vd + 8 * j) = yv;
     }
-    if (tid == 0) {
-      a.ksc[col] = kscl;
-      a.vsc[col] = vscl;
-      a.vmax[col] = m[1];
-    }
-    // dS scale: |dS s_h| <= max_q |dO'_q|_1 max |V| + max |delta s_h| over the group's heads
-    f32x2 hb = {0.f, 0.f};
-    if (tid < a.G) {
-      const float2 t = a.hst[b * a.Hq + hk * a.G + tid];
-      hb = f32x2{t.x, t.y};
-    }
-    for (int g = tid + 512; g < a.G; g += 512) {
-      const float2 t = a.hst[b * a.Hq + hk * a.G + g];
-      hb = f32x2{fmaxf(hb[0], t.x), fmaxf(hb[1], t.y)};
-    }
-    hb = block_max2_512(hb, red);
+    if (tid == 0) a.ksc[col] = kscl;
     ksc = kscl;
-    ivs = 1.f / vscl;
-    fds = ds_scale(fmaf(hb[0], m[1], hb[1]));
-    m2c = c2 / (acc_r * ksc);
-    __syncthreads();  // the K' / V' tiles are complete
+    ivs = pow2_rcp(a.vsc[col]);
+    m2c = c2 * pow2_rcp(acc_r * ksc);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's V' loads have landed
+    __syncthreads();                // the K' / V' tiles are complete
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
@@ -450,8 +438,8 @@ void bwd_dkdv_mfma(KArgs a) {
                     E::pack2(acc[mt][4 * j + 2] * sc, acc[mt][4 * j + 3] * sc)};
       }
     };
-    finish(dk, redk, a.scale / (fds * acc_s * acc_r));
-    finish(dv, redv, 1.f / (fds * acc_s));
+    finish(dk, redk, a.scale * pow2_rcp(acc_s * acc_r));
+    finish(dv, redv, pow2_rcp(acc_s));
   }
   __syncthreads();
   constexpr int CPR = D / 8;  // 16-byte chunks per row

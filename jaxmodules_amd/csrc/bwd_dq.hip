@@ -11,17 +11,19 @@ namespace mattn {
 // ---------------------------------------------------------------------------
 // dQ (MFMA)
 // ---------------------------------------------------------------------------
-// Each wave owns 32 queries.  With the float16 copies Q' = Q r_h, dO' = dO s_h
-// (bwd_pre) and K' = K k_t, V' = V v_t (written by the dK/dV kernel, which
-// runs first; k_t, v_t powers of two per 128-key tile), per 64-key sub-block:
+// Each wave owns 32 queries.  With the float16 copies Q' = Q r, V' = V v_t
+// (the forward's), dO' = dO s (bwd_pre) and K' = K k_t (the dK/dV kernel's,
+// which runs first) -- r, s for the workgroup's 128-row query tile, k_t, v_t
+// for each 128-key tile -- per 64-key sub-block:
 //   S'^T  = K' Q'^T       (A: K' rows from LDS, B: Q'^T in registers)
 //   dP'^T = V' dO'^T      (A: V' rows from LDS, B: dO'^T in registers)
-//   P     = exp2(S' c2 / (k_t r_h) - lse)     (each lane owns one query)
-//   dS~^T = P^T * (dP'^T t / v_t - delta s_h t) = t s_h dS^T
+//   P     = exp2(S' c2 / (k_t r) - lse)       (each lane owns one query)
+//   dS~^T = P^T * (dP'^T t / v_t - delta s t) = t s dS^T
 //   dQ^T += K'^T dS~^T    (A: K'^T by transposed reads of the same K' tile)
-// t is a power of two that keeps |dS~| < 2^14 (the head bounds bwd_pre left
-// in hst and the kv head's max |V|); the accumulator is in units of
-// t s_h k_t, rescaled when the walk reaches a tile with another k_t.
+// t is a power of two that keeps |dS~| < 2^14 (the tile bounds bwd_pre left
+// in tst and the kv head's max |V|); the accumulator is in units of t s k_t,
+// rescaled when the walk reaches a tile with another k_t (rare: the scales
+// move in steps of 2^4).
 // K' and V' are double-buffered (one array per buffer, loop unrolled by two),
 // swizzled row-major tiles filled by direct global->LDS loads.  The operand
 // reads are pipelined by hand (asm LDS reads one or two k-steps ahead of their
@@ -75,21 +77,23 @@ void bwd_dq_mfma(KArgs a) {
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
   const float nlse = -a.lse[rs];
-  const float2 hsc = a.hsc[b * a.Hq + h];  // (s_h, r_h)
-  const float2 hst = a.hst[b * a.Hq + h];  // (max |dO'|_1 of a row, max |delta s_h|)
+  const float qs_r = a.qsc[item], ds_s = a.dsc[item];  // the tile's Q' and dO' scales
+  const float2 ts = a.tst[item];  // (max |dO'_q|_1 of a row, max |delta s|)
   const int tb = (b * a.Hkv + hk) * a.nkt;  // first tile of this kv head in the per-tile arrays
-  // t from the bound |dS s_h| <= max |dO'_q|_1 max |V| + max |delta s_h| (max |V| over the kv head)
+  // t from the bound |dS s| <= max |dO'_q|_1 max |V| + max |delta s| (max |V| over the kv head)
   float vm = 0.f;
   for (int t = lane; t < a.nkt; t += 64) vm = fmaxf(vm, a.vmax[tb + t]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
-  const float tds = pow2_scale(fmaf(hst.x, vm, hst.y), 14);
-  const float bq = -a.delta[rs] * tds;  // delta is stored in units of s_h
-  const float c2r = c2 / hsc.y;
+  const float tds = pow2_scale(fmaf(ts.x, vm, ts.y), 14);
+  const float bq = -a.delta[rs] * tds;  // delta is stored in units of s
+  const float c2r = c2 * pow2_rcp(qs_r);
 
   // float16 K' / V' rows of this kv head: dense, row stride D, padded to whole tiles
   const uint16_t* kb = a.kh + (int64_t)tb * TILE * D;
   const uint16_t* vb = a.vh + (int64_t)tb * TILE * D;
+  const float* ksc = a.ksc + tb;
+  const float* vsc = a.vsc + tb;
   uint32_t kld[NI];  // source byte offsets of this lane's load slots (K' and V' alike)
 #pragma unroll
   for (int i = 0; i < NI; ++i) kld[i] = 2 * TL::src_off(NI * wave + i, lane, D);
@@ -113,10 +117,8 @@ void bwd_dq_mfma(KArgs a) {
   float nks = 1.f, nvs = 1.f;   // its tile's K' and V' scales
   auto prep = [&](int s) {
     int kt;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask, ksc, vsc, nks, nvs);
     nkey0 = kt * TILE + (s & 1) * BN;
-    nks = a.ksc[tb + kt];
-    nvs = a.vsc[tb + kt];
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
     constexpr int BUF = decltype(bufc)::value;
@@ -151,8 +153,8 @@ void bwd_dq_mfma(KArgs a) {
       for (int i = 0; i < NMD; ++i) acc[i] *= f;
       kcur = sks;
     }
-    const float mq = c2r / sks;   // S = S' / (k_t r_h)
-    const float adp = tds / svs;  // dS~ = P (dP' t / v_t - delta s_h t)
+    const float mq = c2r * pow2_rcp(sks);   // S = S' / (k_t r)
+    const float adp = tds * pow2_rcp(svs);  // dS~ = P (dP' t / v_t - delta s t)
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
     // operand reads pipelined by hand (asm LDS reads issued PS / PQ k-steps
     // ahead of their MFMAs, counted lgkmcnt waits); the V tile sits BN * D
@@ -247,7 +249,7 @@ void bwd_dq_mfma(KArgs a) {
   uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * 32 * D;
   static_assert(2 * 32 * D <= 2 * BN * D, "output staging");
   const int r0 = qt * TILE + 32 * wave;
-  store_rows<D, 2>(acc, a.scale / (tds * hsc.x * kcur), stage, a.dq,
+  store_rows<D, 2>(acc, a.scale * pow2_rcp(tds * ds_s * kcur), stage, a.dq,
                    (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2], a.dqs[1],
                    min(32, a.Lq - r0), lane, E::pack2);
 }

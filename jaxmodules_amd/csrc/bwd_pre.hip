@@ -3,20 +3,18 @@
 //
 // The reference recomputes each query block's key scan and back-propagates
 // through it, adding full-size dK/dV contributions per query block.  Here the
-// gradient is computed from the saved base-2 log-sum-exp in four kernels:
-//   bwd_absmax : per (b, head, chunk of CHUNK query rows) the largest |dO| and
-//                |Q| (partial maxima, no atomics);
-//   bwd_pre    : per (b, head, 64-row sub-block) the float16 copies dOh =
-//                dO * s_h and Qh = Q * r_h (powers of two from the head's
-//                maxima), delta = rowsum(O * dOh), and the head's bounds on
-//                the dS the backward kernels form (maxima by atomic max of
-//                non-negative floats: the result does not depend on the order);
-//   bwd_dkdv   : one workgroup per 128-key map column of (b, kv head); it walks
-//                the column's present query tiles for every query head of the
-//                GQA group and accumulates dK, dV in registers -- each element
-//                written exactly once, no atomics (bwd_dkdv.hip);
-//   bwd_dq     : one workgroup per 128-query map row; dQ accumulated in
-//                registers (bwd_dq.hip).
+// gradient is computed from the saved base-2 log-sum-exp in three kernels:
+//   bwd_pre  : per (b, head, 128-row query tile) the float16 copy
+//              doh = dO * dsc (a power of two from the tile's max |dO|),
+//              delta = rowsum(O * doh), the tile's bounds on the dS the other
+//              two kernels form, and the dK/dV kernel's dS scale f of the tile
+//              as lse - log2(f), so that its exp2 yields f P (this file);
+//   bwd_dkdv : one workgroup per 128-key map column of (b, kv head); it walks
+//              the column's present query tiles for every query head of the
+//              GQA group and accumulates dK, dV in registers -- each element
+//              written exactly once, no atomics (bwd_dkdv.hip);
+//   bwd_dq   : one workgroup per 128-query map row; dQ accumulated in
+//              registers (bwd_dq.hip).
 // With P = exp2(scale_log2 * S - lse) and dS = P * (dO V^T - delta):
 //   dV = P^T dO,  dK = scale * dS^T Q,  dQ = scale * dS K.
 // Every product of the 16-bit paths runs on float16 operands (11 significant
@@ -45,117 +43,54 @@ __device__ __forceinline__ void load_vals(const void* base, int64_t off, float* 
     }
   } else {
     const uint16_t* p = (const uint16_t*)base + off;
-    if constexpr (PER % 8 == 0) {
 #pragma unroll
-      for (int i = 0; i < PER; i += 8) {
-        const u32x4 y = *(const u32x4*)(p + i);
+    for (int i = 0; i < PER; i += 8) {
+      const u32x4 y = *(const u32x4*)(p + i);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) g[i + j] = E::to_f32(elt16(y, j));
-      }
-    } else {
-      static_assert(PER == 4, "row slice of 4 or a multiple of 8 values");
-      const u32x2 y = *(const u32x2*)p;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) g[j] = E::to_f32((y[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+      for (int j = 0; j < 8; ++j) g[i + j] = E::to_f32(elt16(y, j));
     }
   }
 }
 
-// Element-wise maximum of x over the 256 threads of a workgroup (red: 4 entries).
-__device__ __forceinline__ f32x2 block_max2_256(f32x2 x, f32x2* red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    x[0] = fmaxf(x[0], __shfl_xor(x[0], o));
-    x[1] = fmaxf(x[1], __shfl_xor(x[1], o));
-  }
-  __syncthreads();  // red may still be read by a previous call
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
-  __syncthreads();
-  f32x2 r = red[0];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    r[0] = fmaxf(r[0], red[w][0]);
-    r[1] = fmaxf(r[1], red[w][1]);
-  }
-  return r;
-}
-
-// Partial maxima of |dO| and |Q| over CHUNK query rows of one (b, head):
-// grid B * Hq * nch, 16 lanes per row, 16 rows per pass.
+// One workgroup of 512 threads per (b, head, 128-row query tile), 4 threads
+// per row.  Rows past Lq (up to the tile's end) are written as zeros.
 template <int D, class Tag, bool O_F32>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
-void bwd_absmax(KArgs a) {
-  constexpr int PER = D / 16;
-  __shared__ f32x2 red[4];
-  const int bh = blockIdx.x / a.nch, ch = blockIdx.x % a.nch;
-  const int h = bh % a.Hq, b = bh / a.Hq;
-  const int sub = threadIdx.x & 15;
-  const int q1 = min(a.Lq, (ch + 1) * CHUNK);
-  f32x2 mx = {0.f, 0.f};
-  const int64_t dbase = (int64_t)b * a.dos[0] + (int64_t)h * a.dos[2] + sub * PER;
-  const int64_t qbase = (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2] + sub * PER;
-#pragma unroll 4
-  for (int q = ch * CHUNK + (threadIdx.x >> 4); q < q1; q += 16) {
-    float g[PER], x[PER];
-    load_vals<PER, Tag, O_F32>(a.dO, dbase + (int64_t)q * a.dos[1], g);
-    load_vals<PER, Tag, false>(a.q, qbase + (int64_t)q * a.qs[1], x);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      mx[0] = fmaxf(mx[0], fabsf(g[i]));
-      mx[1] = fmaxf(mx[1], fabsf(x[i]));
-    }
-  }
-  mx = block_max2_256(mx, red);
-  if (threadIdx.x == 0) {
-    a.part[blockIdx.x] = float2{mx[0], mx[1]};
-    if (ch == 0) a.hst[bh] = float2{0.f, 0.f};  // bwd_pre raises it
-  }
-}
-
-// One workgroup per (b, head, 64-row sub-block), 4 threads per row.  Rows past
-// Lq (up to the 128-row padding of the copies) are written as zeros.
-template <int D, class Tag, bool O_F32>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_pre(KArgs a) {
   using H = Elt<f16_tag>;
   constexpr int PER = D / 4;
-  __shared__ f32x2 red[4];
-  const int nsb = 2 * a.nqt;
-  const int bh = blockIdx.x / nsb, sb = blockIdx.x % nsb;
+  __shared__ f32x2 red[8];
+  const int tile = blockIdx.x;  // (b * Hq + h) * nqt + qt
+  const int qt = tile % a.nqt, bh = tile / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq;
   const int tid = threadIdx.x, part = tid & 3;
-  const int q = sb * SUB_ROWS + (tid >> 2);
+  const int q = qt * TILE + (tid >> 2);
   const bool live = q < a.Lq;
 
-  // the head's scales from its partial maxima (every workgroup of the head
-  // computes the same values)
-  f32x2 hm = {0.f, 0.f};
-  for (int i = tid; i < a.nch; i += 256) {
-    const float2 p = a.part[bh * a.nch + i];
-    hm[0] = fmaxf(hm[0], p.x);
-    hm[1] = fmaxf(hm[1], p.y);
-  }
-  hm = block_max2_256(hm, red);
-  const float s = pow2_scale(hm[0], 14), r = pow2_scale(hm[1], 14);
-  if (sb == 0 && tid == 0) a.hsc[bh] = float2{s, r};
-
-  float o[PER], g[PER], x[PER];
+  float o[PER], g[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) o[i] = g[i] = x[i] = 0.f;
+  for (int i = 0; i < PER; ++i) o[i] = g[i] = 0.f;
   if (live) {
     load_vals<PER, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * PER, o);
     load_vals<PER, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + part * PER, g);
-    load_vals<PER, Tag, false>(a.q, (int64_t)b * a.qs[0] + (int64_t)q * a.qs[1] + (int64_t)h * a.qs[2] + part * PER, x);
   }
-  // float16 copies; delta and the row's L1 norm from dOh exactly as rounded,
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) mx = fmaxf(mx, fabsf(g[i]));
+  // max |V| of the kv head (the forward's per-tile maxima)
+  float vm = 0.f;
+  const int tb = (b * a.Hkv + h / a.G) * a.nkt;
+  for (int t = tid; t < a.nkt; t += 512) vm = fmaxf(vm, a.vmax[tb + t]);
+  const f32x2 m1 = block_max2_512(f32x2{mx, vm}, red);
+  const float s = copy_scale(m1[0]);
+  // the float16 copy; delta and the row's L1 norm from doh exactly as rounded,
   // so that dS = P (dP - delta) cancels exactly where the exact dS is zero
-  // (a row with a single allowed key) and its rounding error scales with V - O.
-  uint32_t hp[PER / 2], qp[PER / 2];
+  // (a row with a single allowed key) and its rounding error scales with V - O
+  uint32_t hp[PER / 2];
   float dl = 0.f, l1 = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; i += 2) {
     hp[i / 2] = H::pack2(g[i] * s, g[i + 1] * s);
-    qp[i / 2] = H::pack2(x[i] * r, x[i + 1] * r);
     const float h0 = H::to_f32(hp[i / 2] & 0xffffu), h1 = H::to_f32(hp[i / 2] >> 16);
     dl = fmaf(o[i], h0, fmaf(o[i + 1], h1, dl));
     l1 += fabsf(h0) + fabsf(h1);
@@ -165,19 +100,22 @@ void bwd_pre(KArgs a) {
     dl += __shfl_xor(dl, m);
     l1 += __shfl_xor(l1, m);
   }
-  const int64_t row = (int64_t)bh * (a.nqt * TILE) + q;
-  uint16_t* wd = a.doh + row * D + part * PER;
-  uint16_t* wq = a.qh + row * D + part * PER;
+  uint16_t* wd = a.doh + ((int64_t)bh * (a.nqt * TILE) + q) * D + part * PER;
 #pragma unroll
-  for (int i = 0; i < PER; i += 8) {
+  for (int i = 0; i < PER; i += 8)
     *(u32x4*)(wd + i) = u32x4{hp[i / 2], hp[i / 2 + 1], hp[i / 2 + 2], hp[i / 2 + 3]};
-    *(u32x4*)(wq + i) = u32x4{qp[i / 2], qp[i / 2 + 1], qp[i / 2 + 2], qp[i / 2 + 3]};
+  const f32x2 st = block_max2_512(f32x2{l1, fabsf(dl)}, red);
+  // |dS s| <= |dP s| + |delta s| <= max_q |doh_q|_1 max |V| + max |delta s|
+  const float f = ds_scale(fmaf(st[0], m1[1], st[1]));
+  if (live && part == 0) {
+    const int64_t rr = (int64_t)bh * a.Lq + q;
+    a.delta[rr] = dl;
+    a.lsf[rr] = a.lse[rr] - (float)((int)(__float_as_uint(f) >> 23) - 127);  // log2 f, exact
   }
-  if (live && part == 0) a.delta[(int64_t)bh * a.Lq + q] = dl;
-  const f32x2 st = block_max2_256(f32x2{l1, fabsf(dl)}, red);
-  if (tid == 0) {  // non-negative floats order like their bit patterns
-    atomicMax((unsigned int*)&a.hst[bh].x, __float_as_uint(st[0]));
-    atomicMax((unsigned int*)&a.hst[bh].y, __float_as_uint(st[1]));
+  if (tid == 0) {
+    a.dsc[tile] = s;
+    a.tst[tile] = float2{st[0], st[1]};
+    a.asc[tile] = f * s;
   }
 }
 
@@ -380,8 +318,7 @@ hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t s
 
 template <int D, class Tag, bool OF32>
 static void launch_pre_16(const KArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((bwd_absmax<D, Tag, OF32>), dim3(a.B * a.Hq * a.nch), dim3(256), 0, st, a);
-  hipLaunchKernelGGL((bwd_pre<D, Tag, OF32>), dim3(a.B * a.Hq * 2 * a.nqt), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((bwd_pre<D, Tag, OF32>), dim3(a.B * a.Hq * a.nqt), dim3(512), 0, st, a);
 }
 
 hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,

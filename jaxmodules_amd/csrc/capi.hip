@@ -15,7 +15,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 
@@ -31,29 +31,34 @@ bool strides_ok(const int64_t s[3], int esz) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Forward workspace (16-bit inputs): V as float16 times a power of two per
-// 128-key tile, [B, Hkv, nkt * 128, D], with each tile's scale and max |V|.
+// Forward residual (16-bit inputs): V as float16 times a power of two per
+// 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
+// [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
+// scale, and each V tile's max |V|.
 struct FwdWs {
-  size_t vh, vsc, vmax, total;
+  size_t vh, qh, vsc, vmax, qsc, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
   FwdWs w{};
   if (p->dtype == MATTN_F32) return w;
-  const size_t tiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
+  const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
+  const size_t qtiles = (size_t)p->B * p->Hq * cdiv(p->Lq, MATTN_TILE_Q);
   w.vh = 0;
-  w.vsc = align256(tiles * MATTN_TILE_K * p->D * 2);
-  w.vmax = w.vsc + align256(tiles * sizeof(float));
-  w.total = w.vmax + align256(tiles * sizeof(float));
+  w.qh = align256(ktiles * MATTN_TILE_K * p->D * 2);
+  w.vsc = w.qh + align256(qtiles * MATTN_TILE_Q * p->D * 2);
+  w.vmax = w.vsc + align256(ktiles * sizeof(float));
+  w.qsc = w.vmax + align256(ktiles * sizeof(float));
+  w.total = w.qsc + align256(qtiles * sizeof(float));
   return w;
 }
 
 // Backward workspace: delta (f32 per query row); for 16-bit inputs also the
-// partial maxima of |dO| and |Q|, the per-head scales and dS bounds, the
-// float16 copies dO', Q' ([B, Hq, nqt * 128, D]) and K', V'
-// ([B, Hkv, nkt * 128, D]), and each K' / V' tile's scale and max |V|.
+// shifted lse (f32 per query row), the float16 copies dO' ([B, Hq, nqt * 128,
+// D]) and K' ([B, Hkv, nkt * 128, D]), and per 128-row tile the dO' scale, the
+// dS bounds and scale of the query tiles and the K' scale of the key tiles.
 struct WsLayout {
-  size_t delta, part, hsc, hst, doh, qh, kh, vh, ksc, vsc, vmax, total;
+  size_t delta, lsf, doh, kh, dsc, tst, asc, ksc, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
@@ -62,21 +67,16 @@ WsLayout ws_layout(const mattn_problem* p) {
   w.delta = 0;
   w.total = align256(rows * sizeof(float));
   if (p->dtype == MATTN_F32) return w;
-  const size_t heads = (size_t)p->B * p->Hq;
-  const size_t nch = cdiv(p->Lq, CHUNK);
-  const size_t qrows = heads * cdiv(p->Lq, MATTN_TILE_Q) * MATTN_TILE_Q;
-  const size_t tiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
-  w.part = w.total;
-  w.hsc = w.part + align256(heads * nch * 8);
-  w.hst = w.hsc + align256(heads * 8);
-  w.doh = w.hst + align256(heads * 8);
-  w.qh = w.doh + align256(qrows * p->D * 2);
-  w.kh = w.qh + align256(qrows * p->D * 2);
-  w.vh = w.kh + align256(tiles * MATTN_TILE_K * p->D * 2);
-  w.ksc = w.vh + align256(tiles * MATTN_TILE_K * p->D * 2);
-  w.vsc = w.ksc + align256(tiles * sizeof(float));
-  w.vmax = w.vsc + align256(tiles * sizeof(float));
-  w.total = w.vmax + align256(tiles * sizeof(float));
+  const size_t qtiles = (size_t)p->B * p->Hq * cdiv(p->Lq, MATTN_TILE_Q);
+  const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
+  w.lsf = w.total;
+  w.doh = w.lsf + align256(rows * sizeof(float));
+  w.kh = w.doh + align256(qtiles * MATTN_TILE_Q * p->D * 2);
+  w.dsc = w.kh + align256(ktiles * MATTN_TILE_K * p->D * 2);
+  w.tst = w.dsc + align256(qtiles * sizeof(float));
+  w.asc = w.tst + align256(qtiles * 8);
+  w.ksc = w.asc + align256(qtiles * sizeof(float));
+  w.total = w.ksc + align256(ktiles * sizeof(float));
   return w;
 }
 
@@ -98,7 +98,6 @@ KArgs make_args(const mattn_problem* p, const mattn_blockmap* bm) {
   a.Hq = p->Hq;
   a.Hkv = p->Hkv;
   a.G = p->Hq / p->Hkv;
-  a.nch = (int)cdiv(p->Lq, CHUNK);
   a.scale = p->scale;
   a.scale_log2 = p->scale * 1.4426950408889634f;
   a.map_b = bm->map_b;
@@ -146,6 +145,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite
+  if (p->flags & ~MATTN_FWD_FOR_BWD) return MATTN_ERR_SHAPE;
   const int es = elem_size(p->dtype), eo = elem_size(p->o_dtype);
   if (!strides_ok(p->q_stride, es) || !strides_ok(p->k_stride, es) || !strides_ok(p->v_stride, es) ||
       !strides_ok(p->dq_stride, es) || !strides_ok(p->dk_stride, es) ||
@@ -209,6 +209,8 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
     a.vh = (uint16_t*)(ws + w.vh);
     a.vsc = (float*)(ws + w.vsc);
     a.vmax = (float*)(ws + w.vmax);
+    a.qsc = (float*)(ws + w.qsc);
+    a.qh = (p->flags & MATTN_FWD_FOR_BWD) ? (uint16_t*)(ws + w.qh) : nullptr;
   }
   hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
@@ -216,14 +218,16 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
 
 int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage, const void* q,
                     const void* k, const void* v, const void* o, const void* do_, const float* lse,
-                    void* workspace, void* dq, void* dk, void* dv, void* stream) {
+                    const void* residual, void* workspace, void* dq, void* dk, void* dv, void* stream) {
   int rc = mattn_validate(p, bm);
   if (rc != MATTN_OK) return rc;
   if (!bm) return MATTN_ERR_NULL;
   if (stage != MATTN_BWD_PRE && stage != MATTN_BWD_DKDV && stage != MATTN_BWD_DQ) return MATTN_ERR_SHAPE;
   if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
+  if (p->dtype != MATTN_F32 && !residual) return MATTN_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
-      !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u))
+      !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u) ||
+      ((uintptr_t)residual & 255u))
     return MATTN_ERR_STRIDE;
   KArgs a = make_args(p, bm);
   a.q = q;
@@ -239,16 +243,20 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
   if (p->dtype != MATTN_F32) {
-    a.part = (float2*)(ws + w.part);
-    a.hsc = (float2*)(ws + w.hsc);
-    a.hst = (float2*)(ws + w.hst);
+    a.lsf = (float*)(ws + w.lsf);
     a.doh = (uint16_t*)(ws + w.doh);
-    a.qh = (uint16_t*)(ws + w.qh);
     a.kh = (uint16_t*)(ws + w.kh);
-    a.vh = (uint16_t*)(ws + w.vh);
+    a.dsc = (float*)(ws + w.dsc);
+    a.tst = (float2*)(ws + w.tst);
+    a.asc = (float*)(ws + w.asc);
     a.ksc = (float*)(ws + w.ksc);
-    a.vsc = (float*)(ws + w.vsc);
-    a.vmax = (float*)(ws + w.vmax);
+    const FwdWs r = fwd_ws_layout(p);
+    const char* res = (const char*)residual;
+    a.vh = (uint16_t*)(res + r.vh);
+    a.qh = (uint16_t*)(res + r.qh);
+    a.vsc = (float*)(res + r.vsc);
+    a.vmax = (float*)(res + r.vmax);
+    a.qsc = (float*)(res + r.qsc);
   }
   hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
                                   bm->n_kv_order, (hipStream_t)stream);
@@ -256,10 +264,11 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
 }
 
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
-              const void* v, const void* o, const void* do_, const float* lse, void* workspace,
-              void* dq, void* dk, void* dv, void* stream) {
+              const void* v, const void* o, const void* do_, const float* lse, const void* residual,
+              void* workspace, void* dq, void* dk, void* dv, void* stream) {
   for (int stage = MATTN_BWD_PRE; stage <= MATTN_BWD_DQ; ++stage) {
-    const int rc = mattn_bwd_stage(p, bm, stage, q, k, v, o, do_, lse, workspace, dq, dk, dv, stream);
+    const int rc = mattn_bwd_stage(p, bm, stage, q, k, v, o, do_, lse, residual, workspace, dq, dk, dv,
+                                   stream);
     if (rc != MATTN_OK) return rc;
   }
   return MATTN_OK;

@@ -38,19 +38,18 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int TILE = 128;  // map tile edge (MATTN_TILE_Q == MATTN_TILE_K)
-constexpr int SUB_ROWS = 64;  // rows of a backward sub-block (the unit of the per-sub-block bounds)
-constexpr int CHUNK = 256; // query rows per workgroup of the max |dO|, |Q| pass
 constexpr float NEG_INF = -__builtin_inff();
 
 // Arguments of every kernel (passed by value in the kernarg segment).
 //
 // The 16-bit paths multiply float16 operands only.  Every float16 working copy
-// is the input times a power of two (exact for bfloat16 and float16 values in
-// range), written head-major and dense, [B, H, rows padded to 128, D], rows
-// past the sequence end zero:
-//   vh = V * vsc[b, hk, tile], kh = K * ksc[b, hk, tile]  (per 128-key tile)
-//   dOh = dO * hsc[b, h].x,  qh = Q * hsc[b, h].y          (per head)
+// is the input times a power of two per 128-row tile (copy_scale: exact for
+// bfloat16 and float16 values), written head-major and dense,
+// [B, H, rows padded to 128, D], rows past the sequence end zero:
+//   vh = V * vsc[b, hk, key tile]    qh  = Q * qsc[b, h, query tile]   (forward)
+//   kh = K * ksc[b, hk, key tile]    doh = dO * dsc[b, h, query tile]  (backward)
 // so each product's scale is a per-step scalar, undone on the float32 result.
+// The forward leaves vh and qh (with their scales) for the backward.
 struct KArgs {
   const void* q;
   const void* k;
@@ -59,21 +58,22 @@ struct KArgs {
   const void* dO;    // upstream gradient in o_dtype
   void* out;         // forward output O
   float* lse;        // [B, Hq, Lq] base-2 log-sum-exp
-  float* delta;      // [B, Hq, Lq] rowsum(O * dOh): delta in units of hsc.x
+  float* delta;      // [B, Hq, Lq] rowsum(O * doh): delta in units of dsc
   void* dq;
   void* dk;
   void* dv;
-  uint16_t* vh;      // [B, Hkv, nkt*128, D] float16 V * vsc
-  uint16_t* kh;      // [B, Hkv, nkt*128, D] float16 K * ksc (backward)
-  uint16_t* qh;      // [B, Hq, nqt*128, D] float16 Q * hsc.y (backward)
-  uint16_t* doh;     // [B, Hq, nqt*128, D] float16 dO * hsc.x (backward)
+  uint16_t* vh;      // [B, Hkv, nkt*128, D] (forward residual)
+  uint16_t* qh;      // [B, Hq, nqt*128, D] (forward residual; the forward writes it when non-null)
+  uint16_t* kh;      // [B, Hkv, nkt*128, D] (backward)
+  uint16_t* doh;     // [B, Hq, nqt*128, D] (backward)
   float* vsc;        // [B*Hkv*nkt] scale of each V tile
   float* vmax;       // [B*Hkv*nkt] max |V| of each tile
-  float* ksc;        // [B*Hkv*nkt] scale of each K tile (backward)
-  float2* hsc;       // [B*Hq] (dO scale, Q scale) of each head (backward)
-  float2* part;      // [B*Hq*nch] partial (max |dO|, max |Q|) (backward)
-  float2* hst;       // [B*Hq] (max row L1 norm of dOh, max |delta|) of each head (backward)
-  int nch;           // query chunks of CHUNK rows per head
+  float* qsc;        // [B*Hq*nqt] scale of each Q tile
+  float* ksc;        // [B*Hkv*nkt] scale of each K tile
+  float* dsc;        // [B*Hq*nqt] scale of each dO tile
+  float2* tst;       // [B*Hq*nqt] per query tile: (max row L1 norm of doh, max |delta|)
+  float* asc;        // [B*Hq*nqt] per query tile: f * dsc, f the dK/dV kernel's dS scale
+  float* lsf;        // [B, Hq, Lq] lse - log2(f) of the row's tile (the dK/dV kernel's P * f)
   int64_t qs[3], ks[3], vs[3], os[3], dos[3], dqs[3], dks[3], dvs[3];
   int B, Lq, Lk, Hq, Hkv, G;
   float scale;       // softmax scale
@@ -97,11 +97,35 @@ __device__ __forceinline__ float pow2_scale(float m, int top) {
   return ldexpf(1.f, min(126, max(-126, top - e)));
 }
 
-// Scale f of the float16 dS of a sub-block: |dS| <= bound (in the units dS
-// is computed in) keeps |dS * f| < 2^14, and f <= 2^15 keeps f * P (P <= 1)
-// inside float16 too.
+// Scale of a float16 working copy from the largest magnitude m it holds: a
+// power of two s with m * s in [2^10, 2^14), s's exponent a multiple of 4.
+// Copies whose maxima lie within a factor of 16 of each other then mostly get
+// the same s, so the kernels rarely rescale an accumulator between tiles.  A
+// bfloat16 value is exact in float16 down to 2^-17 (and a float32 value keeps
+// 11 significant bits down to 2^-14), i.e. to 2^-27 of the copy's maximum.
+__device__ __forceinline__ float copy_scale(float m) {
+  if (!(m > 0.f) || !(m <= 3.4e38f)) return 1.f;
+  int e;
+  frexpf(m, &e);                           // m in [2^(e-1), 2^e)
+  const int t = (e + 3 + 256) / 4 * 4 - 256;  // e rounded up to a multiple of 4
+  return ldexpf(1.f, min(124, max(-124, 14 - t)));
+}
+
+// Scale f of a query tile's float16 dS in the dK/dV kernel: |dS| <= bound (in
+// the units dS is computed in) keeps |dS * f| < 2^14; f's exponent is a
+// multiple of 4 (tiles then mostly share it, as with copy_scale) and at most
+// 12, so that f * P (P <= 1) stays inside float16 too.
 __device__ __forceinline__ float ds_scale(float bound) {
-  return fminf(pow2_scale(bound, 14), 32768.f);
+  if (!(bound > 0.f) || !(bound <= 3.4e38f)) return 4096.f;
+  int e;
+  frexpf(bound, &e);                          // bound in [2^(e-1), 2^e)
+  const int k = (14 - e + 256) / 4 * 4 - 256;  // floor((14 - e) / 4) * 4
+  return ldexpf(1.f, min(12, max(-124, k)));
+}
+
+// 1 / x for a power of two x = 2^k, |k| <= 126: exact (exponent arithmetic).
+__device__ __forceinline__ float pow2_rcp(float x) {
+  return __uint_as_float(0x7f000000u - __float_as_uint(x));
 }
 
 struct bf16_tag {};
@@ -315,8 +339,13 @@ __device__ __forceinline__ float wave_sum32(float x) {
 // Tile entries of one CSR list [e, e1): lane l holds entry base + l (clamped to
 // e1 - 1), refilled when e leaves the window.  The clamp ties the window to one
 // list: call reset() before reading another list.
+// Two per-tile floats (scales) can ride along: gathered from sa[tile] and
+// sb[tile] when the window is refilled, read back the same way, so that no
+// scalar-memory load sits in the tile loop (its lgkmcnt would add to the
+// hand-counted LDS waits).
 struct EntryCache {
   int tile = 0, mask = 0, base = -(1 << 30);
+  float s0 = 1.f, s1 = 1.f;
   __device__ __forceinline__ void reset() { base = -(1 << 30); }
   __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m) {
     if (e - base >= 64 || e < base) {  // wave-uniform
@@ -327,6 +356,21 @@ struct EntryCache {
     }
     t = __builtin_amdgcn_readlane(tile, e - base);
     m = __builtin_amdgcn_readlane(mask, e - base);
+  }
+  __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m,
+                                      const float* sa, const float* sb, float& a, float& b) {
+    if (e - base >= 64 || e < base) {  // wave-uniform
+      base = e;
+      const int idx = min(e + lane, e1 - 1);
+      tile = ent[2 * idx];
+      mask = ent[2 * idx + 1];
+      s0 = sa[tile];
+      s1 = sb[tile];
+    }
+    t = __builtin_amdgcn_readlane(tile, e - base);
+    m = __builtin_amdgcn_readlane(mask, e - base);
+    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s0), e - base));
+    b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s1), e - base));
   }
 };
 
@@ -428,8 +472,8 @@ __device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int 
 
 // One 128-row tile of a 16-bit [rows, D] tensor held by 512 threads, 4 per row
 // (thread t: row t / 4, 16-byte chunks CPL * (t % 4) .. + CPL - 1), and its
-// conversion to float16 times a power of two: tile_load, then tile_scale
-// (the tile's max |x| and scale, one workgroup barrier), then tile_f16.
+// conversion to float16 times a power of two: tile_load, tile_absmax and
+// block_max2_512 for the tile's max |x|, then chunk_f16 per chunk.
 template <int D>
 struct TileRows {
   static constexpr int CPL = D / 32;  // 16-byte chunks per thread
@@ -449,18 +493,15 @@ __device__ __forceinline__ void tile_load(TileRows<D>& t, const uint16_t* src, i
   }
 }
 
-// max |x| over this thread's values of each of two tiles
+// max |x| over this thread's values of a tile
 template <int D, class Tag>
-__device__ __forceinline__ f32x2 tile_absmax2(const TileRows<D>& t0, const TileRows<D>& t1) {
+__device__ __forceinline__ float tile_absmax(const TileRows<D>& t) {
   using E = Elt<Tag>;
-  f32x2 m = {0.f, 0.f};
+  float m = 0.f;
 #pragma unroll
   for (int j = 0; j < TileRows<D>::CPL; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      m[0] = fmaxf(m[0], fabsf(E::to_f32(elt16(t0.x[j], e))));
-      m[1] = fmaxf(m[1], fabsf(E::to_f32(elt16(t1.x[j], e))));
-    }
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(E::to_f32(elt16(t.x[j], e))));
   return m;
 }
 

@@ -13,7 +13,11 @@
 // P enters the product rounded to float16 (11 significant bits; bfloat16's 8
 // leave O and the backward's delta = rowsum(dO * O) outside the 2e-3 gate on
 // unit-variance inputs), and the row sum adds up exactly those rounded values,
-// so that O is the exact attention output for the weights P / sum(P).
+// so that O is the exact attention output for the weights P / sum(P): then
+// dP - delta = sum_j w_j (dP - dP_j) in the backward, without the rounding of
+// the normaliser, which rows dominated by one key would carry into dS.
+// When the backward will run, the workgroup also writes its 128 Q rows as
+// float16 times a power of two (qh, qsc): they are in registers here anyway.
 // K and V' are double-buffered in LDS; the next sub-block's global loads are
 // in flight while the current one is computed.  K and V' tiles are moved by
 // direct global->LDS loads into swizzled row-major tiles; V'^T operands are
@@ -39,8 +43,8 @@ void cvt_v(KArgs a) {
   TileRows<D> t;
   tile_load<D>(t, (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)(kt * TILE) * a.vs[1] +
                       (int64_t)hk * a.vs[2], a.vs[1], a.Lk - kt * TILE);
-  const f32x2 m = block_max2_512(tile_absmax2<D, Tag>(t, t), red);
-  const float s = pow2_scale(m[0], 14);
+  const f32x2 m = block_max2_512(f32x2{tile_absmax<D, Tag>(t), 0.f}, red);
+  const float s = copy_scale(m[0]);
   uint16_t* dst = a.vh + ((int64_t)bh * a.nkt * TILE + kt * TILE + r) * D + 8 * TileRows<D>::CPL * part;
 #pragma unroll
   for (int j = 0; j < TileRows<D>::CPL; ++j) *(u32x4*)(dst + 8 * j) = chunk_f16<Tag>(t.x[j], s);
@@ -69,6 +73,7 @@ void fwd_mfma(KArgs a) {
   // loads landing in one buffer cannot alias the reads of the other
   __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
+  __shared__ float QM[4];  // per-wave max |Q| (the float16 Q copy's scale)
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
@@ -94,6 +99,24 @@ void fwd_mfma(KArgs a) {
                          (int64_t)h * a.qs[2] + 8 * hi;
 #pragma unroll
     for (int kd = 0; kd < NKD; ++kd) qf[kd] = *(const u32x4*)(qp + 16 * kd);
+  }
+  if (a.qh != nullptr) {
+    // float16 copy of the tile's Q rows for the backward (rows past Lq zero)
+    float m = 0.f;
+#pragma unroll
+    for (int kd = 0; kd < NKD; ++kd)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(E::to_f32(elt16(qf[kd], e))));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) QM[wave] = m;
+    __syncthreads();
+    const float r = copy_scale(fmaxf(fmaxf(QM[0], QM[1]), fmaxf(QM[2], QM[3])));
+    uint16_t* qd = a.qh + ((int64_t)bh * a.nqt * TILE + q) * D + 8 * hi;
+#pragma unroll
+    for (int kd = 0; kd < NKD; ++kd)
+      *(u32x4*)(qd + 16 * kd) = q < a.Lq ? chunk_f16<Tag>(qf[kd], r) : u32x4{0u, 0u, 0u, 0u};
+    if (tid == 0) a.qsc[item] = r;
   }
 
   const uint16_t* kb = (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
@@ -139,9 +162,9 @@ void fwd_mfma(KArgs a) {
   };
   auto prep = [&](int s) {
     int kt;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask);
+    float unused;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask, vsc, vsc, nnu, unused);
     nkey0 = kt * TILE + (s & 1) * BN;
-    nnu = vsc[kt];
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
     constexpr int BUF = decltype(bufc)::value;

@@ -124,32 +124,40 @@ def test_validate_blockmap(lib):
 
 
 def test_workspace_bytes(lib):
-    """The documented layouts: backward = delta, then (16-bit inputs) the
-    partial maxima, per-head scales and bounds, float16 dO' and Q' padded to
-    whole 128-row tiles per head, float16 K' and V' per kv-head tile, and
-    three per-tile float arrays; forward = V' and two per-tile float arrays."""
+    """The documented layouts.  Backward workspace: delta, then (16-bit
+    inputs) the shifted lse, float16 dO' padded to whole 128-row tiles per
+    head, float16 K' per kv-head tile, and per tile the dO' scale, dS bounds
+    (2 floats), dS scale and K' scale.  Forward residual: float16 V' and Q', then V' scales and maxima and
+    Q' scales."""
     align = lambda x: (x + 255) // 256 * 256
     B, L, Hq, Hkv, D = 2, 300, 8, 2, 128
-    heads, nch, nqt, tiles = B * Hq, -(-L // 256), -(-L // 128), B * Hkv * -(-L // 128)
-    want = (align(heads * L * 4) + align(heads * nch * 8) + 2 * align(heads * 8)
-            + 2 * align(heads * nqt * 128 * D * 2) + 2 * align(tiles * 128 * D * 2)
-            + 3 * align(tiles * 4))
+    nqt = -(-L // 128)
+    qtiles, ktiles = B * Hq * nqt, B * Hkv * nqt
+    want = (2 * align(B * Hq * L * 4) + align(qtiles * 128 * D * 2) + align(ktiles * 128 * D * 2)
+            + align(qtiles * 4) + align(qtiles * 8) + align(qtiles * 4) + align(ktiles * 4))
     p = _problem()
     assert lib.mattn_workspace_bytes(ctypes.byref(p)) == want
     p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
     assert lib.mattn_workspace_bytes(ctypes.byref(p16)) == want
     p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
-    assert lib.mattn_workspace_bytes(ctypes.byref(p32)) == align(heads * L * 4)
-    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == align(tiles * 128 * D * 2) + 2 * align(tiles * 4)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p32)) == align(B * Hq * L * 4)
+    res = (align(ktiles * 128 * D * 2) + align(qtiles * 128 * D * 2) + 2 * align(ktiles * 4)
+           + align(qtiles * 4))
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == res
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p32)) == 0
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
 
 
+def test_flags_validated(lib):
+    assert _validate(lib, _problem(flags=_lib.MATTN_FWD_FOR_BWD)) == 0
+    assert _validate(lib, _problem(flags=2)) == -2
+
+
 def test_heads_major_long_sequences_validate(lib):
     """Heads-major views (flex_attention's layout) with Hq * Lq * D >= 2^31: the
-    float16 dO' and Q' copies are head-major with one buffer resource per head,
-    so only one head's copy must fit 32-bit byte offsets."""
+    float16 dO' and Q' copies the dK/dV kernel reads are head-major, one buffer
+    resource per head, so only one head's copy must fit 32-bit byte offsets."""
     Hq, L, D = 128, 262144, 128
     p = _problem(B=1, Lq=L, Lk=L, Hq=Hq, Hkv=Hq)
     hm = (ctypes.c_int64 * 3)(Hq * L * D, D, L * D)          # [B, H, L, D] memory, BLHD view
@@ -175,7 +183,7 @@ def test_entry_points_reject_before_launch(lib):
     p = _problem()
     rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None, None)
     assert rc == -1
-    rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 11))
+    rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 12))
     assert rc == -1
 
 

@@ -87,7 +87,7 @@ def test_hip_path_matches_fixture(name):
     assert_close(o.detach().float().cpu().numpy(), f["O"], dt, f"{name} O", "float32")
 
     plan, tm = at.trace_call(tuple(q.shape), tuple(k.shape), tuple(v.shape), **kw)
-    _, lse2 = at.mattn_forward(q.detach(), k.detach(), v.detach(), tm, 1.0 / math.sqrt(c["shape"][-1]))
+    _, lse2, _ = at.mattn_forward(q.detach(), k.detach(), v.detach(), tm, 1.0 / math.sqrt(c["shape"][-1]))
     lse = lse2.cpu().numpy().astype(np.float64) * math.log(2.0)
     fin = np.isfinite(f["lse"])
     assert np.array_equal(np.isfinite(lse), fin)

@@ -132,7 +132,7 @@ def test_fullsize_configs(cfg):
     trace of the configs' lambdas (the ones bench.py and the full-size tests use)."""
     import bench
 
-    B, L, H, d, kw, _ = bench.workload(cfg)
+    B, L, H, _, d, kw, _ = bench.workload(cfg)
     shape = (B, L, H, d)
     plan = bmap.make_plan(shape, shape, shape, **kw)
     t0 = time.perf_counter()
