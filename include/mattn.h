@@ -55,7 +55,9 @@ enum mattn_status {
   MATTN_ERR_STRIDE = -5,        /* misaligned pointer or stride                */
   MATTN_ERR_BLOCKMAP = -6,      /* tile map inconsistent with the problem      */
   MATTN_ERR_LAUNCH = -7,        /* the HIP runtime rejected a launch           */
-  MATTN_ERR_TOO_LARGE = -8      /* a size exceeds 32-bit index ranges          */
+  MATTN_ERR_TOO_LARGE = -8,     /* a size exceeds 32-bit index ranges          */
+  MATTN_ERR_SCRATCH = -9,       /* mattn_bwd_noalloc: workspace > scratch      */
+  MATTN_ERR_DEVICE = -10        /* mattn_bwd_noalloc: no current device/scratch */
 };
 
 /* mattn_problem.flags: the forward also leaves in its residual the float16
@@ -163,6 +165,25 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     const void* q, const void* k, const void* v,
                     const void* o, const void* do_, const float* lse, const void* residual,
                     void* workspace, void* dq, void* dk, void* dv, void* stream);
+
+/* Size of the library's static device scratch used by mattn_bwd_noalloc. */
+#define MATTN_SCRATCH_BYTES (256u << 20)
+
+/* mattn_bwd without a workspace argument: the backward's workspace is a
+ * static device array of MATTN_SCRATCH_BYTES (256 MiB) inside the library, one
+ * per device, so the call makes no allocation of any kind (B=1 L=8192 H=32
+ * D=128 needs 130 MiB).  It has no
+ * counterpart in the reference (whose backward is a jax custom_vjp rule); it
+ * is for callers that cannot allocate: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Problems whose
+ * mattn_workspace_bytes(p) exceeds MATTN_SCRATCH_BYTES return
+ * MATTN_ERR_SCRATCH.  Every call on one device shares that device's scratch:
+ * calls that overlap on one device (other streams, other threads) race.  No
+ * scratch content carries over between calls (each call writes all it reads). */
+int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm,
+                      const void* q, const void* k, const void* v,
+                      const void* o, const void* do_, const float* lse, const void* residual,
+                      void* dq, void* dk, void* dv, void* stream);
 
 /*
  * Device tile-map classifier, for masks given in closed form.  It replaces the

@@ -30,12 +30,15 @@ STATUS = {
     -6: "MATTN_ERR_BLOCKMAP",
     -7: "MATTN_ERR_LAUNCH",
     -8: "MATTN_ERR_TOO_LARGE",
+    -9: "MATTN_ERR_SCRATCH",
+    -10: "MATTN_ERR_DEVICE",
 }
 
 # every symbol include/mattn.h declares
 EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_fwd_workspace_bytes", "mattn_fwd", "mattn_bwd",
            "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version", "mattn_maskspec_validate",
-           "mattn_tilemap_classify", "mattn_tilemap_bits")
+           "mattn_tilemap_classify", "mattn_tilemap_bits", "mattn_bwd_noalloc")
+SCRATCH_BYTES = 256 << 20  # MATTN_SCRATCH_BYTES
 BWD_PRE, BWD_DKDV, BWD_DQ = 0, 1, 2
 
 _I64x3 = ctypes.c_int64 * 3
@@ -113,6 +116,8 @@ def load():
         lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_bwd.restype = ctypes.c_int
         lib.mattn_bwd_stage.argtypes = [P, M, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.mattn_bwd_noalloc.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.mattn_bwd_noalloc.restype = ctypes.c_int
         lib.mattn_bwd_stage.restype = ctypes.c_int
         lib.mattn_strerror.argtypes = [ctypes.c_int]
         lib.mattn_strerror.restype = ctypes.c_char_p

@@ -3,6 +3,8 @@
 // only; the kernels live in fwd.hip, bwd_pre.hip, bwd_dkdv.hip and bwd_dq.hip.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.hpp"
 
 namespace mattn {
@@ -132,6 +134,8 @@ const char* mattn_strerror(int status) {
     case MATTN_ERR_BLOCKMAP: return "block map inconsistent with the problem";
     case MATTN_ERR_LAUNCH: return "kernel launch failed";
     case MATTN_ERR_TOO_LARGE: return "problem exceeds 32-bit index ranges";
+    case MATTN_ERR_SCRATCH: return "backward workspace exceeds the library's static scratch (MATTN_SCRATCH_BYTES)";
+    case MATTN_ERR_DEVICE: return "the HIP runtime could not resolve the device or its scratch";
     default: return "unknown status";
   }
 }
@@ -272,6 +276,46 @@ int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
     if (rc != MATTN_OK) return rc;
   }
   return MATTN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free backward
+// ---------------------------------------------------------------------------
+// The workspace of mattn_bwd_noalloc: one array per device, held from module
+// load to process end.  Host code must not pass `scratch` itself to a kernel
+// (in host code it names a host-side stand-in): the device address comes
+// from hipGetSymbolAddress, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[MATTN_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// The device address of this device's scratch (nullptr on failure); the
+// lookup runs once per device, with that device current.
+void* device_scratch(int dev) {
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+  });
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
+                      const void* v, const void* o, const void* do_, const float* lse,
+                      const void* residual, void* dq, void* dk, void* dv, void* stream) {
+  const int rc = mattn_validate(p, bm);
+  if (rc != MATTN_OK) return rc;
+  if (ws_layout(p).total > (size_t)MATTN_SCRATCH_BYTES) return MATTN_ERR_SCRATCH;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MATTN_ERR_DEVICE;
+  void* ws = device_scratch(dev);
+  if (!ws) return MATTN_ERR_DEVICE;
+  return mattn_bwd(p, bm, q, k, v, o, do_, lse, residual, ws, dq, dk, dv, stream);
 }
 
 }  // extern "C"

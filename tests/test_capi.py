@@ -97,7 +97,7 @@ def test_validate_codes(lib):
     p.q_stride = (ctypes.c_int64 * 3)(300 * 8 * 128, 8 * 128 + 3, 128)
     assert _validate(lib, p) == -5
     assert lib.mattn_validate(None, None) == -1
-    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, 123):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, 123):
         assert isinstance(lib.mattn_strerror(code), bytes)
 
 
@@ -192,3 +192,18 @@ def test_library_missing_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(ImportError):
         _lib.load()
+
+
+def test_noalloc_rejects_before_any_device_call(lib):
+    """mattn_bwd_noalloc checks the problem and its workspace size against the
+    static scratch on the host, before it touches a device."""
+    n, h = 32768, 32                     # dO' and K' copies: 2 x 256 MiB
+    p = _problem(B=1, Lq=n, Lk=n, Hq=h, Hkv=h)
+    for name in ("q", "k", "v", "dq", "dk", "dv", "o", "do"):
+        setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(n * h * 128, h * 128, 128))
+    assert lib.mattn_workspace_bytes(ctypes.byref(p)) > _lib.SCRATCH_BYTES
+    args = [None] * 11
+    assert lib.mattn_bwd_noalloc(ctypes.byref(p), None, *args) == -9
+    assert lib.mattn_bwd_noalloc(ctypes.byref(_problem(D=96)), None, *args) == -3
+    small = _problem()
+    assert lib.mattn_workspace_bytes(ctypes.byref(small)) <= _lib.SCRATCH_BYTES

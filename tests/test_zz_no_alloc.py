@@ -1,0 +1,62 @@
+"""mattn_bwd_noalloc (GPU): the allocation-free backward, whose workspace is
+the library's static per-device scratch, against mattn_bwd with a
+caller-allocated workspace on the same inputs -- bitwise, since both run the
+same kernels in the same order.  Two calls in a row, the second on a smaller
+problem (the scratch keeps the first call's contents), then the first problem
+again; bf16 and fp16; plus the oracle gate on the first call."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from tests.helpers import assert_close, oracle, seeded_inputs
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(B, N, Hq, Hkv, d, dtype, seed, kw):
+    from jaxmodules_amd import _lib
+    from jaxmodules_amd import attention as A
+
+    lib = _lib.load()
+    Q, K, V, dO = seeded_inputs(B, N, N, Hq, Hkv, d, seed)
+    td = getattr(torch, dtype)
+    q, k, v = (torch.from_numpy(x).to("cuda", td).contiguous() for x in (Q, K, V))
+    do = torch.from_numpy(dO).to("cuda").contiguous()
+    plan, tm = A.trace_call(tuple(q.shape), tuple(k.shape), tuple(v.shape), device=q.device, **kw)
+    scale = 1.0 / math.sqrt(d)
+    o, lse, res = A.mattn_forward(q, k, v, tm, scale, torch.float32, for_backward=True)
+    ref = A.mattn_backward(q, k, v, o, lse, do, tm, scale, res)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    p = A._problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
+    assert lib.mattn_workspace_bytes(ctypes.byref(p)) <= _lib.SCRATCH_BYTES
+    bm = A.device_blockmap(tm, q.device)
+    rc = lib.mattn_bwd_noalloc(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
+                               v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                               A._aligned(res), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                               A._stream(q.device))
+    _lib.check(rc, "mattn_bwd_noalloc")
+    torch.cuda.synchronize()
+    for name, a, b in (("dQ", dq, ref[0]), ("dK", dk, ref[1]), ("dV", dv, ref[2])):
+        assert torch.equal(a, b), f"{name}: mattn_bwd_noalloc differs from mattn_bwd"
+    return (Q, K, V, dO, q, k, v, kw, dq, dk, dv)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_noalloc_matches_mattn_bwd_twice(dtype):
+    print(f"[noalloc] {dtype} first call", flush=True)
+    first = _run(2, 700, 4, 2, 128, dtype, 11, dict(is_causal=True, block_size=128))
+    # the first call against the oracle too (the gate of the other parity tests)
+    Q, K, V, dO, q, k, v, kw, dq, dk, dv = first
+    Qr, Kr, Vr = (x.float().cpu().numpy() for x in (q, k, v))
+    _, _, g_ref, _ = oracle(Qr, Kr, Vr, dO, kw)
+    for name, t, r in (("dQ", dq, g_ref[0]), ("dK", dk, g_ref[1]), ("dV", dv, g_ref[2])):
+        assert_close(t.float().cpu().numpy(), r, dtype, name)
+    print(f"[noalloc] {dtype} second, smaller call", flush=True)
+    _run(1, 200, 2, 1, 64, dtype, 12, dict(block_size=64))
+    print(f"[noalloc] {dtype} first problem again", flush=True)
+    _run(2, 700, 4, 2, 128, dtype, 11, dict(is_causal=True, block_size=128))
+
