@@ -373,12 +373,13 @@ void bwd_dkdv_mfma(KArgs a) {
     constexpr int CPL = TileRows<D>::CPL;
     const float kscl = copy_scale(block_max2_512(f32x2{tile_absmax<D, Tag>(tkr), 0.f}, red)[0]);
     const int r = tid >> 2, part = tid & 3;
-    uint16_t* kd = a.kh + ((int64_t)col * TILE + r) * D + 8 * CPL * part;
+    uint16_t* kd = a.kh + ((int64_t)col * TILE + r) * D;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
+      const int c = TileRows<D>::chunk(part, j);
       const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl);
-      *(u32x4*)&Ks[sw_off<D>(r, CPL * part + j)] = yk;
-      *(u32x4*)(kd + 8 * j) = yk;
+      *(u32x4*)&Ks[sw_off<D>(r, c)] = yk;
+      *(u32x4*)(kd + 8 * c) = yk;
     }
     if (tid == 0) a.ksc[col] = kscl;
     ksc = kscl;

@@ -52,6 +52,17 @@ __device__ __forceinline__ void load_vals(const void* base, int64_t off, float* 
   }
 }
 
+// A row's values held by its 4 threads in 16-byte chunks: thread p holds
+// chunks p + 4 j (CS values each: 4 float32 or 8 16-bit values), so that the
+// row's 4 threads read 64 contiguous bytes per access.  g[CS j + e] is value
+// CS (p + 4 j) + e of the row.
+template <int D, class Tag, bool F32>
+__device__ __forceinline__ void load_row(const void* base, int64_t row_off, int part, float* g) {
+  constexpr int CS = F32 ? 4 : 8, NJ = D / 4 / CS;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) load_vals<CS, Tag, F32>(base, row_off + CS * (part + 4 * j), g + CS * j);
+}
+
 // One workgroup of 512 threads per (b, head, 128-row query tile), 4 threads
 // per row.  Rows past Lq (up to the tile's end) are written as zeros.
 template <int D, class Tag, bool O_F32>
@@ -59,6 +70,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_pre(KArgs a) {
   using H = Elt<f16_tag>;
   constexpr int PER = D / 4;
+  constexpr int CS = O_F32 ? 4 : 8;  // values per 16-byte input chunk
   __shared__ f32x2 red[8];
   const int tile = blockIdx.x;  // (b * Hq + h) * nqt + qt
   const int qt = tile % a.nqt, bh = tile / a.nqt;
@@ -71,8 +83,8 @@ void bwd_pre(KArgs a) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) o[i] = g[i] = 0.f;
   if (live) {
-    load_vals<PER, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * PER, o);
-    load_vals<PER, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + part * PER, g);
+    load_row<D, Tag, O_F32>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2], part, o);
+    load_row<D, Tag, O_F32>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2], part, g);
   }
   float mx = 0.f;
 #pragma unroll
@@ -100,10 +112,29 @@ void bwd_pre(KArgs a) {
     dl += __shfl_xor(dl, m);
     l1 += __shfl_xor(l1, m);
   }
-  uint16_t* wd = a.doh + ((int64_t)bh * (a.nqt * TILE) + q) * D + part * PER;
+  // doh row: 16-byte stores, the row's 4 threads covering 64 contiguous bytes each time
+  uint16_t* wd = a.doh + ((int64_t)bh * (a.nqt * TILE) + q) * D;
+  if constexpr (CS == 8) {
+    // chunk j (8 values) -> 8 halves at 8 (part + 4 j)
 #pragma unroll
-  for (int i = 0; i < PER; i += 8)
-    *(u32x4*)(wd + i) = u32x4{hp[i / 2], hp[i / 2 + 1], hp[i / 2 + 2], hp[i / 2 + 3]};
+    for (int j = 0; j < PER / 8; ++j)
+      *(u32x4*)(wd + 8 * (part + 4 * j)) = u32x4{hp[4 * j], hp[4 * j + 1], hp[4 * j + 2], hp[4 * j + 3]};
+  } else {
+    // chunk j (4 values) -> 4 halves at 4 (part + 4 j).  Threads p and p ^ 1
+    // swap one chunk of each pair (2k, 2k + 1): the even thread then holds the
+    // 8 halves at 16 (2k) + 4 p, the odd thread those at 16 (2k + 1) + 4 (p - 1).
+    const bool odd = part & 1;
+#pragma unroll
+    for (int k = 0; k < PER / 8; ++k) {
+      const u32x2 c0 = {hp[4 * k], hp[4 * k + 1]};        // chunk 2k
+      const u32x2 c1 = {hp[4 * k + 2], hp[4 * k + 3]};    // chunk 2k + 1
+      const u32x2 send = odd ? c0 : c1;
+      const u32x2 recv = {(uint32_t)__shfl_xor((int)send[0], 1), (uint32_t)__shfl_xor((int)send[1], 1)};
+      const u32x4 w = odd ? u32x4{recv[0], recv[1], c1[0], c1[1]} : u32x4{c0[0], c0[1], recv[0], recv[1]};
+      const int h0 = odd ? 16 * (2 * k + 1) + 4 * (part - 1) : 16 * (2 * k) + 4 * part;
+      *(u32x4*)(wd + h0) = w;
+    }
+  }
   const f32x2 st = block_max2_512(f32x2{l1, fabsf(dl)}, red);
   // |dS s| <= |dP s| + |delta s| <= max_q |doh_q|_1 max |V| + max |delta s|
   const float f = ds_scale(fmaf(st[0], m1[1], st[1]));

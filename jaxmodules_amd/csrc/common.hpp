@@ -471,13 +471,16 @@ __device__ __forceinline__ int map_row(const KArgs& a, int b, int h, int n, int 
 }
 
 // One 128-row tile of a 16-bit [rows, D] tensor held by 512 threads, 4 per row
-// (thread t: row t / 4, 16-byte chunks CPL * (t % 4) .. + CPL - 1), and its
-// conversion to float16 times a power of two: tile_load, tile_absmax and
-// block_max2_512 for the tile's max |x|, then chunk_f16 per chunk.
+// (thread t: row t / 4, 16-byte chunks t % 4 + 4 j, j < CPL: the 4 threads of a
+// row cover 64 contiguous bytes per access), and its conversion to float16
+// times a power of two: tile_load, tile_absmax and block_max2_512 for the
+// tile's max |x|, then chunk_f16 per chunk.
 template <int D>
 struct TileRows {
   static constexpr int CPL = D / 32;  // 16-byte chunks per thread
   u32x4 x[CPL];
+  // chunk index within the row of this thread's chunk j
+  static __device__ __forceinline__ int chunk(int part, int j) { return part + 4 * j; }
 };
 
 // Rows r >= n are zero.  src points at row 0; rs is the row stride in elements.
@@ -487,9 +490,9 @@ __device__ __forceinline__ void tile_load(TileRows<D>& t, const uint16_t* src, i
 #pragma unroll
   for (int j = 0; j < TileRows<D>::CPL; ++j) t.x[j] = u32x4{0u, 0u, 0u, 0u};
   if (r < n) {
-    const uint16_t* p = src + (int64_t)r * rs + 8 * TileRows<D>::CPL * part;
+    const uint16_t* p = src + (int64_t)r * rs;
 #pragma unroll
-    for (int j = 0; j < TileRows<D>::CPL; ++j) t.x[j] = *(const u32x4*)(p + 8 * j);
+    for (int j = 0; j < TileRows<D>::CPL; ++j) t.x[j] = *(const u32x4*)(p + 8 * TileRows<D>::chunk(part, j));
   }
 }
 

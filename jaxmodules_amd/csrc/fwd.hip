@@ -45,9 +45,10 @@ void cvt_v(KArgs a) {
                       (int64_t)hk * a.vs[2], a.vs[1], a.Lk - kt * TILE);
   const f32x2 m = block_max2_512(f32x2{tile_absmax<D, Tag>(t), 0.f}, red);
   const float s = copy_scale(m[0]);
-  uint16_t* dst = a.vh + ((int64_t)bh * a.nkt * TILE + kt * TILE + r) * D + 8 * TileRows<D>::CPL * part;
+  uint16_t* dst = a.vh + ((int64_t)bh * a.nkt * TILE + kt * TILE + r) * D;
 #pragma unroll
-  for (int j = 0; j < TileRows<D>::CPL; ++j) *(u32x4*)(dst + 8 * j) = chunk_f16<Tag>(t.x[j], s);
+  for (int j = 0; j < TileRows<D>::CPL; ++j)
+    *(u32x4*)(dst + 8 * TileRows<D>::chunk(part, j)) = chunk_f16<Tag>(t.x[j], s);
   if (threadIdx.x == 0) {
     a.vsc[blockIdx.x] = s;
     a.vmax[blockIdx.x] = m[0];
