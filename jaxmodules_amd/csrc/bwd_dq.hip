@@ -17,8 +17,11 @@ namespace mattn {
 // for each 128-key tile -- per 64-key sub-block:
 //   S'^T  = K' Q'^T       (A: K' rows from LDS, B: Q'^T in registers)
 //   dP'^T = V' dO'^T      (A: V' rows from LDS, B: dO'^T in registers)
-//   P     = exp2(S' c2 / (k_t r) - lse)       (each lane owns one query)
-//   dS~^T = P^T * (dP'^T t / v_t - delta s t) = t s dS^T
+//   P~    = exp2(S' c2 / (k_t r) - lse + log2(t / v_t)) = P t / v_t   (each lane owns one query)
+//   dS~^T = P~^T * (dP'^T - delta s v_t) = t s dS^T
+// The dP' accumulator starts at -delta s v_t instead of zero (a constant per
+// lane, i.e. per query), and t / v_t is a power of two folded into P's
+// exponent, so dS~ is one multiply per element.
 //   dQ^T += K'^T dS~^T    (A: K'^T by transposed reads of the same K' tile)
 // t is a power of two that keeps |dS~| < 2^14 (the tile bounds bwd_pre left
 // in tst and the kv head's max |V|); the accumulator is in units of t s k_t,
@@ -86,8 +89,11 @@ void bwd_dq_mfma(KArgs a) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
   const float tds = pow2_scale(fmaf(ts.x, vm, ts.y), 14);
-  const float bq = -a.delta[rs] * tds;  // delta is stored in units of s
+  const float ndl = -a.delta[rs];  // -delta s (delta is stored in units of s)
   const float c2r = c2 * pow2_rcp(qs_r);
+  // exponent of a power of two, exactly
+  auto log2p = [](float x) { return (float)((int)(__float_as_uint(x) >> 23) - 127); };
+  const float nlse_t = nlse + log2p(tds);
 
   // float16 K' / V' rows of this kv head: dense, row stride D, padded to whole tiles
   const uint16_t* kb = a.kh + (int64_t)tb * TILE * D;
@@ -144,6 +150,11 @@ void bwd_dq_mfma(KArgs a) {
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
   float kcur = 1.f;  // K' tile scale the accumulator is in
+  // for the V' tile scale vcur: the dP' accumulators' start value -delta s
+  // v_t and P~'s exponent offset -lse + log2(t / v_t); rebuilt when a tile
+  // with another V' scale comes (rare)
+  float vcur = 0.f, nlv = 0.f;
+  f32x16 cvec = f32x16{};
 
   auto step = [&](auto bufc, bool masked, float sks, float svs) {
     constexpr int BUF = decltype(bufc)::value;
@@ -154,7 +165,13 @@ void bwd_dq_mfma(KArgs a) {
       kcur = sks;
     }
     const float mq = c2r * pow2_rcp(sks);   // S = S' / (k_t r)
-    const float adp = tds * pow2_rcp(svs);  // dS~ = P (dP' t / v_t - delta s t)
+    if (svs != vcur) {  // uniform
+      vcur = svs;
+      nlv = nlse_t - log2p(svs);
+      const float c0 = ndl * svs;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) cvec[r] = c0;
+    }
     const uint64_t mw = masked ? (BUF ? M1 : M0)[qloc] : 0;
     // operand reads pipelined by hand (asm LDS reads issued PS / PQ k-steps
     // ahead of their MFMAs, counted lgkmcnt waits); the V tile sits BN * D
@@ -168,7 +185,7 @@ void bwd_dq_mfma(KArgs a) {
     // its two dQ k-steps before the next half starts (halves the live state).
     static_for<2>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
-      f32x16 st = f32x16{}, dp = f32x16{};
+      f32x16 st = f32x16{}, dp = cvec;
       u32x4 ka[PS + 1], va[PS + 1];
       auto rd = [&](auto kc) {
         constexpr int kd = decltype(kc)::value, sl = kd % (PS + 1);
@@ -189,7 +206,7 @@ void bwd_dq_mfma(KArgs a) {
         hold(dp);
       });
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], mq, nlse));
+      for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], mq, nlv));
       if (masked) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
 #pragma unroll
@@ -199,8 +216,8 @@ void bwd_dq_mfma(KArgs a) {
       u32x4 pk[2];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float d0 = st[r] * fmaf(dp[r], adp, bq);
-        const float d1 = st[r + 1] * fmaf(dp[r + 1], adp, bq);
+        const float d0 = st[r] * dp[r];
+        const float d1 = st[r + 1] * dp[r + 1];
         pk[r >> 3][(r & 7) >> 1] = H::pack2(d0, d1);
       }
       // dQ^T += K^T dS^T over the half's two k-steps, K^T by transposed reads
