@@ -11,8 +11,12 @@ L=8192, H=32, d=128, block 128; the 40% bar is quoted on it); the other
 BASELINE configurations are measured the same way in the same run and
 reported under "configs": cfg2 (B=4 L=4096 H=32), cfg3 (sliding window),
 cfg4 (block-sparse, its tile map built by create_block_mask and
-BlockMask.tile_map as BASELINE words it), cfg5 (packed documents) and the
-target shape with 8 KV heads (GQA).
+BlockMask.tile_map as BASELINE words it), cfg5 (packed documents), the
+target shape with 8 KV heads (GQA), and the regime of the reference's own
+benchmark script (check_attn.py: float16, one head, d=64, L=131072, block
+8192, mask k % 2048 == q % 2048 and k <= q; its present tiles hold one
+allowed key per row, so its unmasked-FLOP rate is small by construction and
+its ms_per_step is the figure to read).
 
 Each kernel's time is measured with HIP events on the stream the kernels run
 on (torch's current stream, which the C ABI launches on).  The CPU baseline
@@ -50,7 +54,7 @@ PEAK_HBM_GBS = 8000.0
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: one int64 device copy of this size (PMC calibration)
 # kernel symbol of each timed stage (for the rocprofv3 counter summaries)
 SYMBOL = {"fwd": "fwd_mfma", "bwd_dkdv": "bwd_dkdv_mfma", "bwd_dq": "bwd_dq_mfma"}
-EXTRA = ["cfg2", "cfg3", "cfg4", "cfg5", "target_gqa"]
+EXTRA = ["cfg2", "cfg3", "cfg4", "cfg5", "target_gqa", "check_attn"]
 
 
 def measured_traffic(config, stage):
@@ -143,6 +147,13 @@ def workload(name):
         mask = lambda b, h, q, k: tbl[h, q // 128, k // 128] & ((q // 128 != k // 128) | (q >= k))
         return 1, 8192, H, H, 64, dict(mask_fn=mask, block_size=128), \
             "cfg4: per-head random 128x128 tiles at 25% (full grid), diagonal causal, bf16 B=1 L=8192 H=32 d=64"
+    if name == "check_attn":
+        from jaxmodules_amd import masks
+
+        mask = masks.intersect(masks.same_residue(2048), masks.causal())
+        return 1, 131072, 1, 1, 64, dict(mask_fn=mask, block_size=8192), \
+            ("check_attn: the reference benchmark's regime (check_attn.py:177-327), fp16 B=1 L=131072 H=1 "
+             "d=64 block 8192, mask k%2048==q%2048 & k<=q, N(0,1) inputs")
     if name == "cfg5":
         doc = _cfg5_docs()
         mask = lambda b, h, q, k: (doc[q] == doc[k]) & (q >= k)
@@ -173,6 +184,13 @@ def tile_map_of(name):
     return tm, time.perf_counter() - t0, how
 
 
+def inputs_of(name):
+    """(torch dtype name, input scale) of a workload's synthetic Q, K, V: bf16
+    times d^-0.25 for the BASELINE configs, float16 N(0, 1) for check_attn
+    (check_attn.py:205-207)."""
+    return ("float16", False) if name == "check_attn" else ("bfloat16", True)
+
+
 class Runner:
     """Preallocated buffers and direct C ABI calls for one configuration."""
 
@@ -191,8 +209,10 @@ class Runner:
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
-        f = d ** -0.25
-        bf = torch.bfloat16
+        dt_name, scaled = inputs_of(name)
+        self.dtype = dt_name
+        f = d ** -0.25 if scaled else 1.0
+        bf = getattr(torch, dt_name)
         self.q = (torch.randn((B, L, Hq, d), generator=g, device=dev) * f).to(bf)
         self.k = (torch.randn((B, L, Hkv, d), generator=g, device=dev) * f).to(bf)
         self.v = (torch.randn((B, L, Hkv, d), generator=g, device=dev) * f).to(bf)
@@ -345,7 +365,8 @@ def tilemap_build_times(repeats=5):
 def summary(r, ms, kern):
     total = r.fwd_flop + r.bwd_flop
     value = total / (ms * 1e-3) / 1e12
-    return value, {"workload": r.desc, "value": round(value, 2), "unit": "TFLOP/s",
+    return value, {"workload": r.desc, "dtype": {"bfloat16": "bf16", "float16": "fp16"}[r.dtype],
+                   "value": round(value, 2), "unit": "TFLOP/s",
                    "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
                    "pairs": r.pairs, "flop_per_step": total,
                    "kernel_ms": {k: round(v, 4) for k, v in kern.items()},

@@ -200,7 +200,8 @@ int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm,
  *     element, 2 the element predicates below
  *   - the element predicates: k <= q when causal; q - k <= win_left and
  *     k - q <= win_right where those are >= 0; doc_q[b][q] == doc_k[b][k]
- *     when doc_b > 0 (b = 0 when doc_b == 1).
+ *     when doc_b > 0 (b = 0 when doc_b == 1); (q - k) % res_period == 0 when
+ *     res_period > 1 (the strided mask k % P == q % P of check_attn.py:9-32).
  * Every pointer is device memory.
  */
 typedef struct mattn_maskspec {
@@ -214,6 +215,7 @@ typedef struct mattn_maskspec {
   int32_t blk_size;              /* 0: no visited-block window                   */
   int32_t blk_left, blk_right;   /* blocks before / from the query's block        */
   int32_t blk_nk;                /* key blocks of the padded key length          */
+  int32_t res_period;            /* 0 or 1: none; P > 1: (q - k) % P == 0        */
 } mattn_maskspec;
 
 /* Host-only check of a mask spec for a map_b x map_h map of Lq x Lk. */

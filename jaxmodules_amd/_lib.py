@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 MATTN_FWD_FOR_BWD = 1
 TILE_Q = TILE_K = 128
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 STATUS = {
     0: "MATTN_OK",
@@ -74,7 +74,7 @@ class MattnMaskspec(ctypes.Structure):
         ("doc_b", ctypes.c_int32), ("doc_q", ctypes.c_void_p), ("doc_k", ctypes.c_void_p),
         ("tab_b", ctypes.c_int32), ("tab_h", ctypes.c_int32), ("tiles", ctypes.c_void_p),
         ("blk_size", ctypes.c_int32), ("blk_left", ctypes.c_int32), ("blk_right", ctypes.c_int32),
-        ("blk_nk", ctypes.c_int32),
+        ("blk_nk", ctypes.c_int32), ("res_period", ctypes.c_int32),
     ]
 
 

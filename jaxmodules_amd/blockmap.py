@@ -251,9 +251,20 @@ def _lpt_xcd_order(weights: np.ndarray, groups: np.ndarray) -> np.ndarray:
     that die's L2).  An XCD takes its groups HEADS_AT_ONCE at a time -- group g
     is the (g // 8)-th of its XCD, in block (g // 8) // HEADS_AT_ONCE -- and
     inside a block the heaviest items go first (longest processing time
-    first).  Idle slots are -1."""
+    first).  With fewer groups than XCDs (a single head, say), each group is
+    split round-robin over NUM_XCD // groups XCDs instead, so that every die
+    has work.  Idle slots are -1."""
+    groups = np.asarray(groups)
+    ngroups = int(groups.max()) + 1 if groups.size else 0
+    if 0 < ngroups < NUM_XCD:
+        spread = NUM_XCD // ngroups
+        by_group = np.argsort(groups, kind="stable")
+        first = np.searchsorted(groups[by_group], np.arange(ngroups))
+        rank = np.empty(groups.size, np.int64)
+        rank[by_group] = np.arange(groups.size) - first[groups[by_group]]   # index within the group
+        groups = groups * spread + rank % spread
     bins = [[] for _ in range(NUM_XCD)]
-    block = (np.asarray(groups) // NUM_XCD) // HEADS_AT_ONCE
+    block = (groups // NUM_XCD) // HEADS_AT_ONCE
     order = np.lexsort((np.arange(len(weights)), -np.asarray(weights), block))  # block, heavy first, stable
     for it in order:
         bins[int(groups[it]) % NUM_XCD].append(int(it))
@@ -431,6 +442,8 @@ def device_trace(plan: Plan, device) -> TileMap:
     if plan.window is not None:
         ms.blk_size, ms.blk_left, ms.blk_right = plan.bs, plan.window[0], plan.window[1]
         ms.blk_nk = plan.Lpad // plan.bs
+    if spec.period is not None and spec.period > 1:
+        ms.res_period = spec.period
     nt = nmap * nqt * nkt
     state = torch.empty(nt, dtype=torch.int8, device=dev)
     count = torch.empty(nt, dtype=torch.int32, device=dev)

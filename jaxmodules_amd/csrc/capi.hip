@@ -17,7 +17,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 

@@ -1,13 +1,16 @@
 // Device tile-map classifier: the tile classification of create_block_mask
 // (/root/reference/jaxmodules/block_mask.py:454-498, get_partial_block
 // :381-408) and of the host tracer, done on the GPU for masks given in closed
-// form (causal, element window, document ids, a per-tile table, and the
-// reference's visited-key-block window, attention.py:161-167,199-204).
+// form (causal, element window, document ids, a per-tile table, keys in the
+// query's residue class modulo a period, and the reference's visited-key-block
+// window, attention.py:161-167,199-204).
 //
 // One wave per 128 x 128 tile.  Lane l owns query rows l and l + 64 of the
 // tile and builds their key bitmasks (two 64-bit words each, the row_bits
-// layout of mattn_blockmap).  Every predicate except document equality is an
-// interval of keys per query row, so a row's words come from two shifts; the
+// layout of mattn_blockmap).  Every predicate except document equality and
+// the residue class is an interval of keys per query row, so a row's words
+// come from two shifts; the residue class keeps every P-th key of the row from
+// its first one in the tile; the
 // document predicate is applied row by row with a ballot over the tile's
 // keys, and only in tiles whose document ids neither all agree nor are
 // disjoint.  The classifier writes per tile its state (absent / full /
@@ -34,6 +37,7 @@ struct TMArgs {
   const uint8_t* tiles;
   int bs, lwb, rwb, bnk;
   int Lq, Lk, map_b, map_h, nqt, nkt;
+  int period;  // > 1: keys with (q - k) % period == 0 only
 };
 
 // keys [a, e) of a 64-key word (a and e relative to the word's first key)
@@ -106,6 +110,18 @@ __device__ int tile_words(const TMArgs& a, int mb, int mh, int qt, int kt, int l
     if (tv != 0) row_span(a, qt * TILE + lane + 64 * s, tv, lo, hi);
     w[s][0] = span_bits(lo - k0, hi - k0);
     w[s][1] = span_bits(lo - k0 - 64, hi - k0 - 64);
+    if (a.period > 1 && tv == 2) {
+      // keys k0 + j with j = (q - k0) mod period + m period
+      const int q = qt * TILE + lane + 64 * s;
+      const int j0 = ((q - k0) % a.period + a.period) % a.period;
+      uint64_t r0 = 0, r1 = 0;
+      for (int j = j0; j < TILE; j += a.period) {
+        if (j < 64) r0 |= 1ull << j;
+        else r1 |= 1ull << (j - 64);
+      }
+      w[s][0] &= r0;
+      w[s][1] &= r1;
+    }
   }
   if (a.doc_b > 0 && tv == 2 && __ballot((w[0][0] | w[0][1] | w[1][0] | w[1][1]) != 0) != 0) {
     const int bd = a.doc_b == 1 ? 0 : mb;
@@ -243,7 +259,7 @@ int check_spec(const mattn_maskspec* ms, int32_t Lq, int32_t Lk, int32_t map_b, 
     if (ms->tab_h != 1 && ms->tab_h != map_h) return MATTN_ERR_SHAPE;
     if (!ms->tiles) return MATTN_ERR_NULL;
   }
-  if (ms->blk_size < 0) return MATTN_ERR_SHAPE;
+  if (ms->blk_size < 0 || ms->res_period < 0) return MATTN_ERR_SHAPE;
   if (ms->blk_size > 0) {
     if (ms->blk_left < 0 || ms->blk_right < 0 || ms->blk_left + ms->blk_right <= 0 ||
         ms->blk_nk < ms->blk_left + ms->blk_right)
@@ -251,7 +267,7 @@ int check_spec(const mattn_maskspec* ms, int32_t Lq, int32_t Lk, int32_t map_b, 
   }
   a = TMArgs{ms->causal, ms->win_left, ms->win_right, ms->doc_b, ms->doc_q, ms->doc_k,
              ms->tab_b, ms->tab_b ? ms->tab_h : 0, ms->tiles, ms->blk_size, ms->blk_left,
-             ms->blk_right, ms->blk_nk, Lq, Lk, map_b, map_h, (int)nqt, (int)nkt};
+             ms->blk_right, ms->blk_nk, Lq, Lk, map_b, map_h, (int)nqt, (int)nkt, ms->res_period};
   return MATTN_OK;
 }
 

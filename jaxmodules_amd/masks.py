@@ -17,6 +17,8 @@ Families, combined with :func:`intersect`:
   in the reference tests' sliding-window masks, ``test_mapped_attention.py:1552``);
 * :func:`documents` -- ``doc[q] == doc[k]`` for packed sequences, one id array
   for every batch or one per batch;
+* :func:`same_residue` -- ``k % period == q % period``, the strided mask of the
+  reference's benchmark (``check_attn.py:9-32``, with ``causal``);
 * :func:`tile_table` -- a per-128x128-tile table (shared, per head or per batch
   and head): 0 masks the tile, 1 allows every element of it, 2 applies the
   element predicates above (a BlockMask's full and partial tiles,
@@ -31,7 +33,8 @@ import numpy as np
 
 TILE = 128
 
-__all__ = ["MaskSpec", "causal", "window", "documents", "tile_table", "intersect", "spec_of"]
+__all__ = ["MaskSpec", "causal", "window", "documents", "same_residue", "tile_table", "intersect",
+           "spec_of"]
 
 
 @dataclass(frozen=True, eq=False)
@@ -42,6 +45,7 @@ class MaskSpec:
     doc_q: Optional[np.ndarray] = None   # int32 [1 or B, Lq]
     doc_k: Optional[np.ndarray] = None   # int32 [1 or B, Lk]
     table: Optional[np.ndarray] = None   # uint8 [1 or B, 1 or H, ceil(Lq/128), ceil(Lk/128)]
+    period: Optional[int] = None         # (q - k) % period == 0
 
     def evaluate(self, b, h, q, k):
         """The mask at broadcast index arrays (or scalars)."""
@@ -56,6 +60,8 @@ class MaskSpec:
         if self.doc_q is not None:
             bd = b if self.doc_q.shape[0] > 1 else 0
             m = m & (self.doc_q[bd, q] == self.doc_k[bd, k])
+        if self.period is not None:
+            m = m & ((q - k) % self.period == 0)
         if self.table is not None:
             tb = b if self.table.shape[0] > 1 else 0
             th = h if self.table.shape[1] > 1 else 0
@@ -139,6 +145,14 @@ def documents(doc_ids, doc_ids_k=None):
     return _fn(MaskSpec(doc_q=_frozen(dq, np.int32), doc_k=_frozen(dk, np.int32)))
 
 
+def same_residue(period: int):
+    """k % period == q % period, i.e. (q - k) % period == 0: every period-th
+    key (with :func:`causal`, the mask of ``check_attn.py:9-32``)."""
+    if int(period) != period or period < 1 or period > 2**31 - 1:
+        raise ValueError(f"period must be a positive int32, got {period}")
+    return _fn(MaskSpec(period=int(period)))
+
+
 def tile_table(table):
     """Per-128x128-tile table of shape [nqt, nkt], [H, nqt, nkt] or [B, H, nqt, nkt]:
     0 = no element, 1 = every element, 2 = the other predicates of the mask
@@ -169,6 +183,12 @@ def intersect(*mask_fns):
             if v is not None:
                 cur = getattr(out, side)
                 kw[side] = v if cur is None else min(cur, v)
+        if s.period is not None:
+            # both residue classes: modulo the least common multiple
+            p = s.period if out.period is None else int(np.lcm(out.period, s.period))
+            if p > 2**31 - 1:
+                raise ValueError("the combined period exceeds int32")
+            kw["period"] = p
         for name in ("doc_q", "table"):
             if getattr(s, name) is not None:
                 if getattr(out, name) is not None:

@@ -93,3 +93,35 @@ def kernel_model(Q, K, V, dO, allowed, scale, dtype, design="float16"):
     dK = dKx.reshape(B, L, Hkv, G, d).sum(3)
     dV = dVx.reshape(B, L, Hkv, G, d).sum(3)
     return O, round_to(dQ, dtype), round_to(dK, dtype), round_to(dV, dtype)
+
+
+# log2(1 + 2^-11): how far a sum of float16-rounded positive terms moves log2 of the sum
+LSE_ROUNDING = float(np.log2(1.0 + 2.0 ** -11))
+
+
+def residue_dv_model(Q, K, dO, period, key, col, scale, lse2=None):
+    """dV[key, col] of one head under the strided causal mask k % P == q % P,
+    k <= q (check_attn.py:9-32), as the float16 design rounds it: the sum over
+    the queries of the key's residue class of sig11(P) sig11(dO).  P is
+    exp2(s log2(e) - lse2[q]) with ``lse2`` the forward's base-2 log-sum-exp
+    per row -- the log of the sum of the forward's float16-rounded weights
+    (the self-consistent normaliser), checked here to lie within LSE_ROUNDING
+    of the exact one -- or the exact softmax when ``lse2`` is None.
+    Q, K: [L, d], dO: [L, d] (float64-exact copies of the kernel's inputs).
+    Returns (value, sum of the terms' magnitudes)."""
+    L = Q.shape[0]
+    total, mag = 0.0, 0.0
+    for q in range(key, L, period):
+        ks = np.arange(q % period, q + 1, period)
+        s = (K[ks] @ Q[q]) * scale
+        m = s.max()
+        exact2 = float((m + np.log(np.exp(s - m).sum())) / np.log(2.0))
+        if lse2 is None:
+            p = np.exp(s - m) / np.exp(s - m).sum()
+        else:
+            assert abs(float(lse2[q]) - exact2) <= LSE_ROUNDING + 1e-6, (q, float(lse2[q]), exact2)
+            p = np.exp2(s / np.log(2.0) - float(lse2[q]))
+        t = float(sig11(p[ks == key])[0] * sig11(dO[q, col]))
+        total += t
+        mag += abs(t)
+    return total, mag

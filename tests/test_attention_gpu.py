@@ -10,7 +10,7 @@ import math
 import numpy as np
 import pytest
 
-from tests.helpers import assert_close, oracle, seeded_inputs
+from tests.helpers import assert_close, assert_close_or_floor, oracle, seeded_inputs
 
 torch = pytest.importorskip("torch")
 
@@ -121,6 +121,47 @@ def test_packed_documents_cfg5_small():
 
 def test_gqa():
     run_case((2, 256, 256, 4, 2, 128), dict(is_causal=True, block_size=64), "bfloat16")
+
+
+@pytest.mark.parametrize("closed_form", [True, False])
+def test_reference_benchmark_regime_small(closed_form):
+    """check_attn.py's regime scaled down (its L >= 32768, period 2048, block
+    8192): float16, one head, d = 64, unit-variance inputs, mask
+    k % P == q % P and k <= q (check_attn.py:9-32), here P = 512, L = 4096,
+    block 1024; the closed form (GPU tile map) and the plain lambda (host tracer).
+    A key is attended by at most L / P queries, each with at most L / P keys,
+    so a dV element is a sum of a few terms of size ~0.5 that often cancel: one
+    element (key 890, a sum of 7 terms of up to 1.9 cancelling to 0.017) misses
+    the 2e-3 absolute tolerance by 1.12x.  The float64 model of the design's
+    roundings (tests/rounding_model.py: P from the forward's log-sum-exp of its
+    float16-rounded weights, then P and dO rounded to float16) gives the
+    kernel's value to the output ulp."""
+    import jaxmodules_amd as jm
+    from jaxmodules_amd import masks
+    from tests.rounding_model import residue_dv_model
+
+    P, L, d = 512, 4096, 64
+    mf = (masks.intersect(masks.same_residue(P), masks.causal()) if closed_form
+          else (lambda b, h, q, k: (k <= q) & (k % P == q % P)))
+    kw = dict(mask_fn=mf, block_size=1024)
+    Q, K, V, dO = seeded_inputs(1, L, L, 1, 1, d, 21, scaled=False)
+    q, k, v = (torch.from_numpy(x).to("cuda", torch.float16).requires_grad_() for x in (Q, K, V))
+    o = jm.masked_attention_via_map(q, k, v, **kw)
+    # the forward's base-2 log-sum-exp, as the backward reads it (the same call)
+    from jaxmodules_amd import attention as A
+
+    _, tm = A.trace_call(tuple(q.shape), tuple(k.shape), tuple(v.shape), device=q.device, **kw)
+    lse2 = A.mattn_forward(q.detach(), k.detach(), v.detach(), tm, 1.0 / math.sqrt(d))[1][0, 0].cpu().numpy()
+    Qr, Kr, Vr = (x.detach().double().cpu().numpy() for x in (q, k, v))
+    O_ref, _, g_ref, _ = oracle(Qr, Kr, Vr, dO, kw)
+    assert_close(o.detach().double().cpu().numpy(), O_ref, "float16", "O", "float32")
+    o.backward(torch.from_numpy(dO).cuda())
+    dO64 = dO.astype(np.float64)
+    model = lambda idx: residue_dv_model(Qr[0, :, 0], Kr[0, :, 0], dO64[0, :, 0], P, idx[1], idx[3],  # noqa: E731
+                                         1.0 / math.sqrt(d), lse2)
+    for name, t, r, floor in (("dQ", q, g_ref[0], 0), ("dK", k, g_ref[1], 0), ("dV", v, g_ref[2], 1)):
+        assert_close_or_floor(t.grad.double().cpu().numpy(), r, "float16", name, floor, model)
+    torch.cuda.synchronize()
 
 
 def test_gqa_head_specific_mask():

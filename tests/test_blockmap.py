@@ -117,6 +117,27 @@ def test_lpt_xcd_order():
         assert list(w[col]) == sorted(w[col], reverse=True)
 
 
+@pytest.mark.parametrize("ngroups", [1, 2, 3])
+def test_lpt_xcd_order_few_groups(ngroups):
+    """Fewer groups than XCDs: each group's items go round-robin (by their
+    index within the group) over NUM_XCD // ngroups XCDs of their own, so that
+    every die has work; heaviest first on each XCD."""
+    per = 40
+    g = np.repeat(np.arange(ngroups), per)
+    w = np.tile(np.arange(per), ngroups) + 1       # causal-like: later items heavier
+    o = bm._lpt_xcd_order(w, g)
+    assert sorted(o[o >= 0].tolist()) == list(range(g.size))
+    slots = o.reshape(-1, bm.NUM_XCD)
+    spread = bm.NUM_XCD // ngroups
+    used = [x for x in range(bm.NUM_XCD) if (slots[:, x] >= 0).any()]
+    assert len(used) == ngroups * spread
+    for x in used:
+        col = [int(i) for i in slots[:, x] if i >= 0]
+        assert len({int(g[i]) for i in col}) == 1               # one group per XCD
+        assert len(col) == per // spread or len(col) == per // spread + 1
+        assert list(w[col]) == sorted(w[col], reverse=True)
+
+
 def test_lpt_xcd_order_blocks_of_groups():
     """An XCD with more than HEADS_AT_ONCE groups takes them block by block,
     heaviest first inside a block."""

@@ -35,9 +35,23 @@ def test_scalar_calls_follow_the_definitions():
         assert bool(m(0, 0, q, k)) == want, (q, k)
     w = masks.window(None, 2)
     assert bool(w(0, 0, 0, 2)) and not bool(w(0, 0, 0, 3)) and bool(w(0, 0, 900, 0))
+    r = masks.intersect(masks.same_residue(5), masks.causal())
+    for q, k in [(7, 2), (7, 7), (2, 7), (7, 3), (1000, 0), (1001, 1), (1001, 0)]:
+        assert bool(r(0, 0, q, k)) == ((k % 5 == q % 5) and k <= q), (q, k)
 
 
-@pytest.mark.parametrize("case", ["causal_window", "docs", "docs_batch", "table", "cross"])
+def test_same_residue_is_the_benchmark_mask():
+    """same_residue(P) & causal is check_attn.py:9-32's get_block_causal_mask
+    (k <= q and k % P == q % P), written out here on a grid."""
+    P, N = 16, 200
+    q, k = np.arange(N)[:, None], np.arange(N)[None, :]
+    want = (k <= q) & (k % P == q % P)
+    got = masks.intersect(masks.same_residue(P), masks.causal())(0, 0, q, k)
+    assert np.array_equal(np.broadcast_to(got, want.shape), want)
+
+
+@pytest.mark.parametrize("case", ["causal_window", "docs", "docs_batch", "table", "cross", "residue",
+                                  "residue_small", "residue_docs"])
 def test_host_trace_equals_lambda(case):
     rng = np.random.default_rng(1)
     if case == "causal_window":
@@ -62,6 +76,21 @@ def test_host_trace_equals_lambda(case):
         mf = masks.intersect(masks.tile_table(t), masks.causal())
         lam = lambda b, h, q, k: (t[h, q // 128, k // 128] == 1) | (       # noqa: E731
             (t[h, q // 128, k // 128] == 2) & (q >= k))
+        kw = dict(block_size=100)
+    elif case == "residue":
+        sq = sk = (1, 1000, 2, 16)
+        mf = masks.intersect(masks.same_residue(160), masks.causal())
+        lam = lambda b, h, q, k: ((q - k) % 160 == 0) & (q >= k)          # noqa: E731
+        kw = dict(block_size=100)
+    elif case == "residue_small":
+        sq, sk = (1, 300, 2, 16), (1, 700, 2, 16)
+        mf = masks.same_residue(7)
+        lam = lambda b, h, q, k: k % 7 == q % 7                             # noqa: E731
+        kw = dict(block_size=100)
+    elif case == "residue_docs":
+        sq = sk = (2, 1000, 2, 16)
+        mf = masks.intersect(masks.same_residue(3), masks.documents(DOC), masks.window(200, 0))
+        lam = lambda b, h, q, k: ((q - k) % 3 == 0) & (DOC[q] == DOC[k]) & (q - k <= 200) & (k <= q)  # noqa: E731
         kw = dict(block_size=100)
     else:
         sq, sk = (1, 300, 2, 16), (1, 700, 2, 16)
@@ -89,6 +118,8 @@ def test_intersect_rules():
         masks.intersect(masks.causal(), lambda b, h, q, k: q >= k)
     with pytest.raises(ValueError):
         masks.intersect()
+    # two residue classes: the least common multiple
+    assert masks.spec_of(masks.intersect(masks.same_residue(4), masks.same_residue(6))).period == 12
 
 
 def test_argument_errors():
@@ -100,6 +131,9 @@ def test_argument_errors():
         masks.documents(np.zeros(10, np.float32))
     with pytest.raises(ValueError):
         masks.tile_table(np.full((2, 2), 3))
+    for bad in (0, -3, 2.5, 2**31):
+        with pytest.raises(ValueError):
+            masks.same_residue(bad)
     spec = masks.spec_of(masks.documents(np.zeros(100, int)))
     with pytest.raises(ValueError):
         spec.check(1, 1, 99, 100)                       # ids of the wrong length
@@ -162,6 +196,8 @@ def test_maskspec_validate_codes(lib):
     assert v(_spec(blk_size=128, blk_left=4, blk_right=1, blk_nk=4)) == -2
     assert v(_spec(blk_size=128, blk_left=3, blk_right=1, blk_nk=4)) == 0
     assert v(_spec(), Lq=2**30, Lk=2**30) == -8                     # tile index beyond int32
+    assert v(_spec(res_period=-1)) == -2
+    assert v(_spec(res_period=2048)) == 0
 
 
 def test_tilemap_entry_points_reject_before_launch(lib):

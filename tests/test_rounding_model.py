@@ -65,3 +65,25 @@ def test_float16_floor_unit_normal_causal():
     assert max(_ratios(Q, K, V, dO, kw, "bfloat16", 1 / 8, "bfloat16")) > 2
     r = _ratios(Q, K, V, dO, kw, "bfloat16", 1 / 8, "float16")
     assert r[0] < 1 and r[1] < 1 and r[2] == pytest.approx(1.10, abs=0.02), r
+
+
+def test_residue_dv_model_without_roundings_is_exact(monkeypatch):
+    """residue_dv_model with the roundings switched off equals dV of the dense
+    float64 attention under the strided causal mask (k % P == q % P, k <= q)."""
+    import math
+
+    from tests import rounding_model as rm
+
+    rng = np.random.default_rng(0)
+    L, d, P = 600, 16, 64
+    Q, K, dO = rng.standard_normal((L, d)), rng.standard_normal((L, d)), rng.standard_normal((L, d))
+    q, k = np.arange(L)[:, None], np.arange(L)[None, :]
+    allowed = (k <= q) & ((q - k) % P == 0)
+    s = np.where(allowed, Q @ K.T / math.sqrt(d), -np.inf)
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    dV = p.T @ dO
+    monkeypatch.setattr(rm, "sig11", lambda x: np.asarray(x, np.float64))
+    for key, col in [(0, 3), (70, 5), (599, 0), (64, 15)]:
+        assert math.isclose(rm.residue_dv_model(Q, K, dO, P, key, col, 1 / math.sqrt(d))[0], dV[key, col],
+                            rel_tol=1e-12, abs_tol=1e-14)

@@ -74,6 +74,18 @@ CASES = {
     "cross_docs": (((2, 300, 2, 64), (2, 1000, 2, 64)),
                    dict(mask_fn=masks.documents(np.arange(300) // 40, np.arange(1000) // 133),
                         block_size=100)),
+    # the reference benchmark's strided mask (check_attn.py:9-32), scaled down
+    "residue_causal": (((1, 8192, 1, 64), (1, 8192, 1, 64)),
+                       dict(mask_fn=masks.intersect(masks.same_residue(1024), masks.causal()),
+                            block_size=1024)),
+    "residue_period_96": (((1, 1000, 2, 64), (1, 1000, 2, 64)),
+                          dict(mask_fn=masks.intersect(masks.same_residue(96), masks.window(500, 30)),
+                               block_size=100)),
+    "residue_period_3_docs": (((2, 900, 2, 64), (2, 900, 2, 64)),
+                              dict(mask_fn=masks.intersect(masks.same_residue(3),
+                                                           masks.documents(_docs(900, 4)),
+                                                           masks.causal()),
+                                   block_size=90)),
 }
 
 
