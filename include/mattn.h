@@ -50,7 +50,7 @@ enum mattn_status {
   MATTN_OK = 0,
   MATTN_ERR_NULL = -1,          /* a required pointer is NULL                  */
   MATTN_ERR_SHAPE = -2,         /* non-positive size or Hq % Hkv != 0          */
-  MATTN_ERR_HEAD_DIM = -3,      /* D not in {64, 128}                          */
+  MATTN_ERR_HEAD_DIM = -3,      /* D not in {64, 128, 256}                     */
   MATTN_ERR_DTYPE = -4,         /* unsupported dtype / o_dtype combination     */
   MATTN_ERR_STRIDE = -5,        /* misaligned pointer or stride                */
   MATTN_ERR_BLOCKMAP = -6,      /* tile map inconsistent with the problem      */
@@ -123,11 +123,15 @@ typedef struct mattn_blockmap {
  * No GPU call; usable without a device. */
 int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
 
-/* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer). */
+/* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer).
+ * Head dimensions 64 and 128 with 16-bit inputs run on the MFMA kernels;
+ * float32 inputs, and D = 256 for every dtype (the host pads d in (128, 256]
+ * with zeros), run on float32 SIMT kernels, whose workspace is delta alone. */
 size_t mattn_workspace_bytes(const mattn_problem* p);
 
 /* Bytes of the forward's residual buffer (256-byte aligned pointer; 0 for
- * float32 inputs): float16 copies of V and (with MATTN_FWD_FOR_BWD) Q, each
+ * float32 inputs and for D = 256): float16 copies of V and (with
+ * MATTN_FWD_FOR_BWD) Q, each
  * times a power of two per 128-row tile, which the forward's P V product and
  * the backward read. */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
@@ -145,8 +149,9 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
 /* Backward (replaces the custom_vjp bwd rule, attention.py:266-342).
  *   do_       : upstream gradient, [B, Lq, Hq, D] of o_dtype
  *   o, lse    : the forward's outputs
- *   residual  : the forward's residual buffer (16-bit inputs; that forward
- *               ran with MATTN_FWD_FOR_BWD), read only
+ *   residual  : the forward's residual buffer (16-bit inputs at D <= 128;
+ *               that forward ran with MATTN_FWD_FOR_BWD), read only; may be
+ *               NULL when mattn_fwd_workspace_bytes(p) == 0
  *   workspace : mattn_workspace_bytes(p) bytes (scratch)
  *   dq, dk, dv: gradients of dtype, every element written (no pre-zeroing). */
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,

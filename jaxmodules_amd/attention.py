@@ -13,10 +13,12 @@ Mirrors the public interface of ``/root/reference/jaxmodules/attention.py``:
   enable_gqa, return_lse)`` (attention.py:456-692) on the same kernels, its
   ``BlockMask`` handed over as a tile map (``BlockMask.tile_map``).
 
-The kernels are built for head dimensions 64 and 128; other head dimensions
-up to 128 are zero-padded on the GPU to the next of the two (zero columns of
-Q and K leave every score unchanged, zero columns of V give zero output
-columns, which are sliced off; the scale stays 1/sqrt(true d)).
+The kernels are built for head dimensions 64, 128 and 256; other head
+dimensions up to 256 are zero-padded on the GPU to the next of the three (zero
+columns of Q and K leave every score unchanged, zero columns of V give zero
+output columns, which are sliced off; the scale stays 1/sqrt(true d)).  16-bit
+inputs at 64 and 128 run on the MFMA kernels; float32 inputs, and every dtype
+at 256, on float32 SIMT kernels.
 
 Arrays are torch tensors on the GPU (jax is not available in this image; the
 jax.ffi binding a jax user would register is described with the C ABI).  The
@@ -260,8 +262,9 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
     """(O [B, N, Hq, d] in out_dtype, base-2 LSE [B, Hq, N], residual) via
     mattn_fwd.  ``heads_major`` lays O out in memory as [B, Hq, N, d] (the
     returned tensor is the [B, N, Hq, d] view of it).  The residual (a uint8
-    tensor, None for float32 inputs) holds the float16 V copy and, with
-    ``for_backward``, the float16 Q copy that mattn_backward reads."""
+    tensor; None for float32 inputs and at d = 256, which the SIMT kernels
+    serve) holds the float16 V copy and, with ``for_backward``, the float16 Q
+    copy that mattn_backward reads."""
     lib = _lib.load()
     B, N, Hq, d = q.shape
     if heads_major:
@@ -340,12 +343,11 @@ class _MaskedAttention(torch.autograd.Function):
 
 
 def _kernel_dim(d: int) -> int:
-    """Head dimension the kernels run at: 64 or 128 (d zero-padded up to it)."""
-    if d <= 64:
-        return 64
-    if d <= 128:
-        return 128
-    raise NotImplementedError(f"head dimension {d} > 128 is not supported by the HIP kernels")
+    """Head dimension the kernels run at: 64, 128 or 256 (d zero-padded up to it)."""
+    for D in (64, 128, 256):
+        if d <= D:
+            return D
+    raise NotImplementedError(f"head dimension {d} > 256 is not supported by the HIP kernels")
 
 
 def _pad_dim(x: torch.Tensor, D: int) -> torch.Tensor:

@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libmattn.so")
-SOURCES = ["fwd.hip", "bwd_pre.hip", "bwd_dq.hip", "bwd_dkdv.hip", "tilemap.hip", "capi.hip"]
+SOURCES = ["fwd.hip", "bwd_pre.hip", "bwd_dq.hip", "bwd_dkdv.hip", "simt.hip", "tilemap.hip", "capi.hip"]
 # machine-scheduler strategy per source: the ILP-oriented ones hoist LDS operand
 # reads ahead of the MFMA chains; each file uses the one measured fastest
 # without register spills for its kernels (bwd_dkdv.hip orders its operand reads

@@ -150,196 +150,6 @@ void bwd_pre(KArgs a) {
   }
 }
 
-// float32 inputs: delta = rowsum(dO * O) only (the SIMT kernels read dO
-// directly).  16 lanes per (b, q, h) row, 16 rows per workgroup.
-template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
-void bwd_pre_f32(KArgs a) {
-  constexpr int PER = D / 16;
-  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
-  const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
-  const int h = (int)(row % (uint32_t)a.Hq);
-  const uint32_t bq = row / (uint32_t)a.Hq;
-  const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
-  float x[PER], g[PER];
-  load_vals<PER, bf16_tag, true>(a.o, (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + sub * PER, x);
-  load_vals<PER, bf16_tag, true>(a.dO, (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + sub * PER, g);
-  float acc = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) acc = fmaf(x[i], g[i], acc);
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 16);
-  if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
-}
-
-// ---------------------------------------------------------------------------
-// float32 SIMT backward
-// ---------------------------------------------------------------------------
-
-template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
-void bwd_dq_simt(KArgs a) {
-  constexpr int SB = 32;
-  constexpr int DP = D / 4;
-  __shared__ __attribute__((aligned(16))) float Ks[SB * D];
-  __shared__ __attribute__((aligned(16))) float Vs[SB * D];
-
-  const int item = a.q_order[blockIdx.x];
-  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
-  const int qt = item % a.nqt;
-  const int bh = item / a.nqt;
-  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
-  const int mrow = map_row(a, b, h, a.nqt, qt);
-  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
-  const int tid = threadIdx.x, row = tid >> 2, part = tid & 3;
-  const int q = qt * TILE + row;
-  const int qc = min(q, a.Lq - 1);
-
-  float qv[DP], gv[DP], dq[DP];
-  {
-    const float* qp = (const float*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
-                      (int64_t)h * a.qs[2] + part * DP;
-    const float* gp = (const float*)a.dO + (int64_t)b * a.dos[0] + (int64_t)qc * a.dos[1] +
-                      (int64_t)h * a.dos[2] + part * DP;
-#pragma unroll
-    for (int i = 0; i < DP; ++i) { qv[i] = qp[i]; gv[i] = gp[i]; dq[i] = 0.f; }
-  }
-  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
-  const float lse = a.lse[rs], dl = a.delta[rs];
-  const float* kb = (const float*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-  const float* vb = (const float*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-
-  for (int e = e0; e < e1; ++e) {
-    const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
-    for (int sb = 0; sb < TILE / SB; ++sb) {
-      const int key0 = kt * TILE + sb * SB;
-      if (key0 >= a.Lk) break;
-      __syncthreads();
-      for (int c = tid; c < SB * D / 4; c += 512) {
-        const int r = c / (D / 4), col = 4 * (c % (D / 4));
-        const int key = min(key0 + r, a.Lk - 1);
-        *(f32x4*)&Ks[r * D + col] = *(const f32x4*)(kb + (int64_t)key * a.ks[1] + col);
-        *(f32x4*)&Vs[r * D + col] = *(const f32x4*)(vb + (int64_t)key * a.vs[1] + col);
-      }
-      __syncthreads();
-      uint32_t bits = 0xffffffffu;
-      if (mask >= 0)
-        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
-      for (int j = 0; j < SB; ++j) {
-        float s = 0.f, g = 0.f;
-#pragma unroll
-        for (int i = 0; i < DP; ++i) {
-          s = fmaf(qv[i], Ks[j * D + part * DP + i], s);
-          g = fmaf(gv[i], Vs[j * D + part * DP + i], g);
-        }
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        g += __shfl_xor(g, 1);
-        g += __shfl_xor(g, 2);
-        float p = exp2f(s * a.scale_log2 - lse);
-        if (!((bits >> j) & 1u)) p = 0.f;
-        const float ds = p * (g - dl);
-#pragma unroll
-        for (int i = 0; i < DP; ++i) dq[i] = fmaf(ds, Ks[j * D + part * DP + i], dq[i]);
-      }
-    }
-  }
-  if (q >= a.Lq) return;
-  float* op = (float*)a.dq + (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2] +
-              part * DP;
-#pragma unroll
-  for (int i = 0; i < DP; ++i) op[i] = dq[i] * a.scale;
-}
-
-template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
-void bwd_dkdv_simt(KArgs a) {
-  constexpr int SB = 32;
-  constexpr int DP = D / 4;
-  __shared__ __attribute__((aligned(16))) float Qs[SB * D];
-  __shared__ __attribute__((aligned(16))) float Gs[SB * D];
-  __shared__ float Ls[SB], Dl[SB];
-
-  const int item = a.kv_order[blockIdx.x];
-  if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
-  const int kt = item % a.nkt;
-  const int bh = item / a.nkt;
-  const int hk = bh % a.Hkv, b = bh / a.Hkv;
-  const int tid = threadIdx.x, row = tid >> 2, part = tid & 3;
-  const int key = kt * TILE + row;
-  const int kcl = min(key, a.Lk - 1);
-
-  float kv[DP], vv[DP], dk[DP], dv[DP];
-  {
-    const float* kp = (const float*)a.k + (int64_t)b * a.ks[0] + (int64_t)kcl * a.ks[1] +
-                      (int64_t)hk * a.ks[2] + part * DP;
-    const float* vp = (const float*)a.v + (int64_t)b * a.vs[0] + (int64_t)kcl * a.vs[1] +
-                      (int64_t)hk * a.vs[2] + part * DP;
-#pragma unroll
-    for (int i = 0; i < DP; ++i) { kv[i] = kp[i]; vv[i] = vp[i]; dk[i] = 0.f; dv[i] = 0.f; }
-  }
-  for (int g = 0; g < a.G; ++g) {
-    const int h = hk * a.G + g;
-    const int mc = map_row(a, b, h, a.nkt, kt);
-    const int e0 = a.col_ptr[mc], e1 = a.col_ptr[mc + 1];
-    const float* qb = (const float*)a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
-    const float* gb = (const float*)a.dO + (int64_t)b * a.dos[0] + (int64_t)h * a.dos[2];
-    for (int e = e0; e < e1; ++e) {
-      const int qt = a.col_ent[2 * e], mask = a.col_ent[2 * e + 1];
-      for (int sb = 0; sb < TILE / SB; ++sb) {
-        const int q0 = qt * TILE + sb * SB;
-        if (q0 >= a.Lq) break;
-        __syncthreads();
-        for (int c = tid; c < SB * D / 4; c += 512) {
-          const int r = c / (D / 4), col = 4 * (c % (D / 4));
-          const int qq = min(q0 + r, a.Lq - 1);
-          *(f32x4*)&Qs[r * D + col] = *(const f32x4*)(qb + (int64_t)qq * a.qs[1] + col);
-          *(f32x4*)&Gs[r * D + col] = *(const f32x4*)(gb + (int64_t)qq * a.dos[1] + col);
-        }
-        if (tid < 2 * SB) {
-          const int qq = min(q0 + (tid & (SB - 1)), a.Lq - 1);
-          const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qq;
-          if (tid < SB) Ls[tid] = a.lse[rs];
-          else Dl[tid - SB] = a.delta[rs];
-        }
-        __syncthreads();
-        uint32_t bits = 0xffffffffu;
-        if (mask >= 0)
-          bits = (uint32_t)(a.col_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
-        for (int j = 0; j < SB; ++j) {
-          float s = 0.f, gd = 0.f;
-#pragma unroll
-          for (int i = 0; i < DP; ++i) {
-            s = fmaf(kv[i], Qs[j * D + part * DP + i], s);
-            gd = fmaf(vv[i], Gs[j * D + part * DP + i], gd);
-          }
-          s += __shfl_xor(s, 1);
-          s += __shfl_xor(s, 2);
-          gd += __shfl_xor(gd, 1);
-          gd += __shfl_xor(gd, 2);
-          float p = exp2f(s * a.scale_log2 - Ls[j]);
-          if (!((bits >> j) & 1u)) p = 0.f;
-          const float ds = p * (gd - Dl[j]);
-#pragma unroll
-          for (int i = 0; i < DP; ++i) {
-            dv[i] = fmaf(p, Gs[j * D + part * DP + i], dv[i]);
-            dk[i] = fmaf(ds, Qs[j * D + part * DP + i], dk[i]);
-          }
-        }
-      }
-    }
-  }
-  if (key >= a.Lk) return;
-  float* kp = (float*)a.dk + (int64_t)b * a.dks[0] + (int64_t)key * a.dks[1] + (int64_t)hk * a.dks[2] +
-              part * DP;
-  float* vp = (float*)a.dv + (int64_t)b * a.dvs[0] + (int64_t)key * a.dvs[1] + (int64_t)hk * a.dvs[2] +
-              part * DP;
-#pragma unroll
-  for (int i = 0; i < DP; ++i) { kp[i] = dk[i] * a.scale; vp[i] = dv[i]; }
-}
-
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -352,24 +162,13 @@ static void launch_pre_16(const KArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((bwd_pre<D, Tag, OF32>), dim3(a.B * a.Hq * a.nqt), dim3(512), 0, st, a);
 }
 
+hipError_t launch_bwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid, int kv_grid,
+                           hipStream_t st);
+
 hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,
                             int kv_grid, hipStream_t st) {
   const bool of32 = (o_dtype == MATTN_F32);
-  if (dtype == MATTN_F32) {
-    if (stage == MATTN_BWD_PRE) {
-      const int64_t rows = (int64_t)a.B * a.Lq * a.Hq;
-      const int pre_grid = (int)((rows + 15) / 16);
-      if (D == 64) hipLaunchKernelGGL((bwd_pre_f32<64>), dim3(pre_grid), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((bwd_pre_f32<128>), dim3(pre_grid), dim3(256), 0, st, a);
-    } else if (stage == MATTN_BWD_DKDV) {
-      if (D == 64) hipLaunchKernelGGL((bwd_dkdv_simt<64>), dim3(kv_grid), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((bwd_dkdv_simt<128>), dim3(kv_grid), dim3(512), 0, st, a);
-    } else {
-      if (D == 64) hipLaunchKernelGGL((bwd_dq_simt<64>), dim3(q_grid), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((bwd_dq_simt<128>), dim3(q_grid), dim3(512), 0, st, a);
-    }
-    return hipGetLastError();
-  }
+  if (dtype == MATTN_F32 || D > 128) return launch_bwd_simt(a, D, dtype, o_dtype, stage, q_grid, kv_grid, st);
   if (stage == MATTN_BWD_DKDV) return launch_dkdv(a, D, dtype, kv_grid, st);
   if (stage == MATTN_BWD_DQ) return launch_dq(a, D, dtype, q_grid, st);
   if (dtype == MATTN_BF16) {

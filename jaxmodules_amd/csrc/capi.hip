@@ -1,6 +1,8 @@
 // C ABI of the library (declared in include/mattn.h): argument validation,
 // workspace layouts, kernel-argument packing and launch selection.  Host code
-// only; the kernels live in fwd.hip, bwd_pre.hip, bwd_dkdv.hip and bwd_dq.hip.
+// only; the kernels live in fwd.hip, bwd_pre.hip, bwd_dkdv.hip, bwd_dq.hip
+// (16-bit inputs, D = 64 and 128: MFMA) and simt.hip (float32 inputs, and
+// every input dtype at D = 256: float32 SIMT arithmetic).
 #include <math.h>
 
 #include <mutex>
@@ -33,7 +35,11 @@ bool strides_ok(const int64_t s[3], int esz) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Forward residual (16-bit inputs): V as float16 times a power of two per
+// problems served by the SIMT kernels, which need no residual and no
+// backward workspace beyond delta
+bool simt_path(const mattn_problem* p) { return p->dtype == MATTN_F32 || p->D > 128; }
+
+// Forward residual (16-bit inputs, D <= 128): V as float16 times a power of two per
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
 // [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
 // scale, and each V tile's max |V|.
@@ -43,7 +49,7 @@ struct FwdWs {
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
   FwdWs w{};
-  if (p->dtype == MATTN_F32) return w;
+  if (simt_path(p)) return w;
   const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
   const size_t qtiles = (size_t)p->B * p->Hq * cdiv(p->Lq, MATTN_TILE_Q);
   w.vh = 0;
@@ -55,7 +61,8 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
   return w;
 }
 
-// Backward workspace: delta (f32 per query row); for 16-bit inputs also the
+// Backward workspace: delta (f32 per query row); for 16-bit inputs at D <= 128
+// (the MFMA kernels) also the
 // shifted lse (f32 per query row), the float16 copies dO' ([B, Hq, nqt * 128,
 // D]) and K' ([B, Hkv, nkt * 128, D]), and per 128-row tile the dO' scale, the
 // dS bounds and scale of the query tiles and the K' scale of the key tiles.
@@ -68,7 +75,7 @@ WsLayout ws_layout(const mattn_problem* p) {
   WsLayout w{};
   w.delta = 0;
   w.total = align256(rows * sizeof(float));
-  if (p->dtype == MATTN_F32) return w;
+  if (simt_path(p)) return w;
   const size_t qtiles = (size_t)p->B * p->Hq * cdiv(p->Lq, MATTN_TILE_Q);
   const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
   w.lsf = w.total;
@@ -128,7 +135,7 @@ const char* mattn_strerror(int status) {
     case MATTN_OK: return "success";
     case MATTN_ERR_NULL: return "a required pointer is NULL";
     case MATTN_ERR_SHAPE: return "invalid shape (sizes must be positive and Hq divisible by Hkv)";
-    case MATTN_ERR_HEAD_DIM: return "unsupported head dimension (supported: 64, 128)";
+    case MATTN_ERR_HEAD_DIM: return "unsupported head dimension (supported: 64, 128, 256)";
     case MATTN_ERR_DTYPE: return "unsupported dtype combination";
     case MATTN_ERR_STRIDE: return "pointer or stride not 16-byte aligned";
     case MATTN_ERR_BLOCKMAP: return "block map inconsistent with the problem";
@@ -145,7 +152,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->B <= 0 || p->Lq <= 0 || p->Lk <= 0 || p->Hq <= 0 || p->Hkv <= 0 || p->D <= 0)
     return MATTN_ERR_SHAPE;
   if (p->Hq % p->Hkv != 0) return MATTN_ERR_SHAPE;
-  if (p->D != 64 && p->D != 128) return MATTN_ERR_HEAD_DIM;
+  if (p->D != 64 && p->D != 128 && p->D != 256) return MATTN_ERR_HEAD_DIM;
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite
@@ -228,7 +235,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   if (!bm) return MATTN_ERR_NULL;
   if (stage != MATTN_BWD_PRE && stage != MATTN_BWD_DKDV && stage != MATTN_BWD_DQ) return MATTN_ERR_SHAPE;
   if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
-  if (p->dtype != MATTN_F32 && !residual) return MATTN_ERR_NULL;
+  if (!simt_path(p) && !residual) return MATTN_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
       !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u) ||
       ((uintptr_t)residual & 255u))
@@ -246,7 +253,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
-  if (p->dtype != MATTN_F32) {
+  if (!simt_path(p)) {
     a.lsf = (float*)(ws + w.lsf);
     a.doh = (uint16_t*)(ws + w.doh);
     a.kh = (uint16_t*)(ws + w.kh);

@@ -335,99 +335,6 @@ void fwd_mfma(KArgs a) {
                                  min(32, a.Lq - r0), lane, E::pack2);
 }
 
-// float32 forward (SIMT, no MFMA): 512 threads own the 128 queries of a map
-// row, 4 threads per query, each holding D/4 head dims.  Used for float32
-// inputs, whose tolerance (1e-5) rules out 16-bit operands.
-template <int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
-void fwd_simt(KArgs a) {
-  constexpr int SB = 32;     // keys per sub-block
-  constexpr int DP = D / 4;  // dims per thread
-  __shared__ __attribute__((aligned(16))) float Ks[SB * D];
-  __shared__ __attribute__((aligned(16))) float Vs[SB * D];
-
-  const int item = a.q_order[blockIdx.x];
-  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
-  const int qt = item % a.nqt;
-  const int bh = item / a.nqt;
-  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
-  const int mrow = map_row(a, b, h, a.nqt, qt);
-  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
-  const int tid = threadIdx.x, row = tid >> 2, part = tid & 3;
-  const int q = qt * TILE + row;
-  const int qc = min(q, a.Lq - 1);
-
-  float qv[DP], ov[DP];
-  {
-    const float* qp = (const float*)a.q + (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] +
-                      (int64_t)h * a.qs[2] + part * DP;
-#pragma unroll
-    for (int i = 0; i < DP; i += 4) {
-      const f32x4 x = *(const f32x4*)(qp + i);
-      qv[i] = x[0]; qv[i + 1] = x[1]; qv[i + 2] = x[2]; qv[i + 3] = x[3];
-      ov[i] = ov[i + 1] = ov[i + 2] = ov[i + 3] = 0.f;
-    }
-  }
-  const float* kb = (const float*)a.k + (int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2];
-  const float* vb = (const float*)a.v + (int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2];
-  float m = NEG_INF, l = 0.f;
-
-  for (int e = e0; e < e1; ++e) {
-    const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
-    for (int sb = 0; sb < TILE / SB; ++sb) {
-      const int key0 = kt * TILE + sb * SB;
-      if (key0 >= a.Lk) break;
-      __syncthreads();
-      for (int c = tid; c < SB * D / 4; c += 512) {
-        const int r = c / (D / 4), col = 4 * (c % (D / 4));
-        const int key = min(key0 + r, a.Lk - 1);
-        *(f32x4*)&Ks[r * D + col] = *(const f32x4*)(kb + (int64_t)key * a.ks[1] + col);
-        *(f32x4*)&Vs[r * D + col] = *(const f32x4*)(vb + (int64_t)key * a.vs[1] + col);
-      }
-      __syncthreads();
-      uint32_t bits = 0xffffffffu;
-      if (mask >= 0)
-        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
-      float sc[SB];
-      float mx = NEG_INF;
-#pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        float p = 0.f;
-#pragma unroll
-        for (int i = 0; i < DP; ++i) p = fmaf(qv[i], Ks[j * D + part * DP + i], p);
-        p += __shfl_xor(p, 1);
-        p += __shfl_xor(p, 2);
-        float x = p * a.scale_log2;
-        if (!((bits >> j) & 1u)) x = NEG_INF;
-        sc[j] = x;
-        mx = fmaxf(mx, x);
-      }
-      const float mn = fmaxf(m, mx);
-      const float mu = (mn == NEG_INF) ? 0.f : mn;
-      const float alpha = exp2f(m - mu);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < DP; ++i) ov[i] *= alpha;
-#pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        const float p = exp2f(sc[j] - mu);
-        l += p;
-#pragma unroll
-        for (int i = 0; i < DP; ++i) ov[i] = fmaf(p, Vs[j * D + part * DP + i], ov[i]);
-      }
-    }
-  }
-  if (q >= a.Lq) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (part == 0) a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + log2f(l) : NEG_INF;
-  float* op = (float*)a.out + (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] +
-              part * DP;
-#pragma unroll
-  for (int i = 0; i < DP; i += 4)
-    *(f32x4*)(op + i) = f32x4{ov[i] * inv, ov[i + 1] * inv, ov[i + 2] * inv, ov[i + 3] * inv};
-}
-
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -442,13 +349,11 @@ static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStr
   return hipGetLastError();
 }
 
+hipError_t launch_fwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st);
+
 hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st) {
   const bool of32 = (o_dtype == MATTN_F32);
-  if (dtype == MATTN_F32) {
-    if (D == 64) hipLaunchKernelGGL((fwd_simt<64>), dim3(grid), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((fwd_simt<128>), dim3(grid), dim3(512), 0, st, a);
-    return hipGetLastError();
-  }
+  if (dtype == MATTN_F32 || D > 128) return launch_fwd_simt(a, D, dtype, o_dtype, grid, st);
   if (dtype == MATTN_BF16)
     return D == 64 ? launch_fwd_mfma<64, bf16_tag>(a, grid, of32, st)
                    : launch_fwd_mfma<128, bf16_tag>(a, grid, of32, st);

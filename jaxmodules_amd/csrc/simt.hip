@@ -1,0 +1,385 @@
+// SIMT (no MFMA) masked-attention kernels: the forward and the three backward
+// stages in float32 arithmetic, for
+//   * float32 inputs, whose 1e-5 tolerance rules out 16-bit operands, at head
+//     dimensions 64, 128 and 256;
+//   * 16-bit inputs at head dimension 256 (any d in (128, 256], zero-padded by
+//     the host), which the MFMA kernels' register and LDS tiling does not hold.
+// Same maths and tile walk as the MFMA path (/root/reference/jaxmodules/
+// attention.py:52-105 forward, :266-342 backward): per 32-key (or 32-query)
+// sub-block an online softmax, P = exp2(scale_log2 S - lse) in the backward,
+// dS = P (dP - delta), dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO.
+// TPR threads share a row (query or key), each holding D / TPR head dims; a
+// workgroup of 512 threads owns 512 / TPR rows of a 128-row map tile, so a
+// tile takes 128 TPR / 512 workgroups (one for TPR = 4, two for TPR = 8).
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace mattn {
+namespace {
+
+// float element access to tensors of float32 or a 16-bit Tag
+template <class T>
+struct Mem {
+  static __device__ __forceinline__ float get(const void* p, int64_t i) { return ((const float*)p)[i]; }
+  // 4 consecutive values (i a multiple of 4: 16-byte aligned)
+  static __device__ __forceinline__ void get4(const void* p, int64_t i, float* x) {
+    const f32x4 y = *(const f32x4*)((const float*)p + i);
+    x[0] = y[0]; x[1] = y[1]; x[2] = y[2]; x[3] = y[3];
+  }
+  static __device__ __forceinline__ void put(void* p, int64_t i, float x) { ((float*)p)[i] = x; }
+};
+template <class Tag>
+struct Mem16 {
+  using E = Elt<Tag>;
+  static __device__ __forceinline__ float get(const void* p, int64_t i) {
+    return E::to_f32(((const uint16_t*)p)[i]);
+  }
+  // 4 consecutive values (i a multiple of 4: 8-byte aligned)
+  static __device__ __forceinline__ void get4(const void* p, int64_t i, float* x) {
+    const u32x2 y = *(const u32x2*)((const uint16_t*)p + i);
+    x[0] = E::to_f32(y[0] & 0xffffu); x[1] = E::to_f32(y[0] >> 16);
+    x[2] = E::to_f32(y[1] & 0xffffu); x[3] = E::to_f32(y[1] >> 16);
+  }
+  static __device__ __forceinline__ void put(void* p, int64_t i, float x) {
+    ((uint16_t*)p)[i] = (uint16_t)(E::pack2(x, 0.f) & 0xffffu);  // round to nearest even
+  }
+};
+template <>
+struct Mem<bf16_tag> : Mem16<bf16_tag> {};
+template <>
+struct Mem<f16_tag> : Mem16<f16_tag> {};
+
+constexpr int SB = 32;  // keys (forward, dQ) or queries (dK/dV) per sub-block
+
+// sum over the TPR lanes of a row (consecutive lanes)
+template <int TPR>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// rows [r0, r0 + SB) of a [rows, D] tensor slice (row stride rs) as floats in
+// LDS; rows past n - 1 re-read row n - 1 (their scores are masked)
+template <int D, class T>
+__device__ __forceinline__ void stage_rows(float* dst, const void* base, int64_t rs, int r0, int n) {
+  for (int c = threadIdx.x; c < SB * D / 4; c += 512) {
+    const int r = c / (D / 4), col = 4 * (c % (D / 4));
+    Mem<T>::get4(base, (int64_t)min(r0 + r, n - 1) * rs + col, dst + r * D + col);
+  }
+}
+
+template <int D, int TPR, class IT, class OT>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
+void fwd_simt(KArgs a) {
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
+  __shared__ __attribute__((aligned(16))) float Ks[SB * D];
+  __shared__ __attribute__((aligned(16))) float Vs[SB * D];
+
+  const int item = a.q_order[blockIdx.x / SPLIT];
+  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int tid = threadIdx.x, part = tid % TPR;
+  const int row = (blockIdx.x % SPLIT) * RPW + tid / TPR;  // row within the tile
+  const int q = qt * TILE + row;
+  const int qc = min(q, a.Lq - 1);
+
+  float qv[DP], ov[DP];
+  const int64_t qo = (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] + (int64_t)h * a.qs[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; i += 4) {
+    Mem<IT>::get4(a.q, qo + i, qv + i);
+    ov[i] = ov[i + 1] = ov[i + 2] = ov[i + 3] = 0.f;
+  }
+  const char* kb = (const char*)a.k + ES * ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2]);
+  const char* vb = (const char*)a.v + ES * ((int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2]);
+  float m = NEG_INF, l = 0.f;
+
+  for (int e = e0; e < e1; ++e) {
+    const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
+    for (int sb = 0; sb < TILE / SB; ++sb) {
+      const int key0 = kt * TILE + sb * SB;
+      if (key0 >= a.Lk) break;
+      __syncthreads();
+      stage_rows<D, IT>(Ks, kb, a.ks[1], key0, a.Lk);
+      stage_rows<D, IT>(Vs, vb, a.vs[1], key0, a.Lk);
+      __syncthreads();
+      uint32_t bits = 0xffffffffu;
+      if (mask >= 0)
+        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+      float sc[SB];
+      float mx = NEG_INF;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        float p = 0.f;
+#pragma unroll
+        for (int i = 0; i < DP; ++i) p = fmaf(qv[i], Ks[j * D + part * DP + i], p);
+        float x = row_sum<TPR>(p) * a.scale_log2;
+        if (!((bits >> j) & 1u)) x = NEG_INF;
+        sc[j] = x;
+        mx = fmaxf(mx, x);
+      }
+      const float mn = fmaxf(m, mx);
+      const float mu = (mn == NEG_INF) ? 0.f : mn;
+      const float alpha = exp2f(m - mu);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < DP; ++i) ov[i] *= alpha;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float p = exp2f(sc[j] - mu);
+        l += p;
+#pragma unroll
+        for (int i = 0; i < DP; ++i) ov[i] = fmaf(p, Vs[j * D + part * DP + i], ov[i]);
+      }
+    }
+  }
+  if (q >= a.Lq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (part == 0) a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + log2f(l) : NEG_INF;
+  const int64_t oo = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; ++i) Mem<OT>::put(a.out, oo + i, ov[i] * inv);
+}
+
+// delta = rowsum(dO * O), O and dO in OT: 16 lanes per (b, q, h) row, 16 rows
+// per workgroup of 256 threads
+template <int D, class OT>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
+void bwd_delta_simt(KArgs a) {
+  constexpr int PER = D / 16;
+  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
+  const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
+  const int h = (int)(row % (uint32_t)a.Hq);
+  const uint32_t bq = row / (uint32_t)a.Hq;
+  const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
+  const int64_t oo = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + sub * PER;
+  const int64_t go = (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + sub * PER;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; i += 4) {
+    float x[4], g[4];
+    Mem<OT>::get4(a.o, oo + i, x);
+    Mem<OT>::get4(a.dO, go + i, g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(x[j], g[j], acc);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 16);
+  if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
+}
+
+template <int D, int TPR, class IT, class OT>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
+void bwd_dq_simt(KArgs a) {
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
+  __shared__ __attribute__((aligned(16))) float Ks[SB * D];
+  __shared__ __attribute__((aligned(16))) float Vs[SB * D];
+
+  const int item = a.q_order[blockIdx.x / SPLIT];
+  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int tid = threadIdx.x, part = tid % TPR;
+  const int row = (blockIdx.x % SPLIT) * RPW + tid / TPR;
+  const int q = qt * TILE + row;
+  const int qc = min(q, a.Lq - 1);
+
+  float qv[DP], gv[DP], dq[DP];
+  const int64_t qo = (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] + (int64_t)h * a.qs[2] + part * DP;
+  const int64_t go = (int64_t)b * a.dos[0] + (int64_t)qc * a.dos[1] + (int64_t)h * a.dos[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; i += 4) {
+    Mem<IT>::get4(a.q, qo + i, qv + i);
+    Mem<OT>::get4(a.dO, go + i, gv + i);
+    dq[i] = dq[i + 1] = dq[i + 2] = dq[i + 3] = 0.f;
+  }
+  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
+  const float lse = a.lse[rs], dl = a.delta[rs];
+  const char* kb = (const char*)a.k + ES * ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2]);
+  const char* vb = (const char*)a.v + ES * ((int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2]);
+
+  for (int e = e0; e < e1; ++e) {
+    const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
+    for (int sb = 0; sb < TILE / SB; ++sb) {
+      const int key0 = kt * TILE + sb * SB;
+      if (key0 >= a.Lk) break;
+      __syncthreads();
+      stage_rows<D, IT>(Ks, kb, a.ks[1], key0, a.Lk);
+      stage_rows<D, IT>(Vs, vb, a.vs[1], key0, a.Lk);
+      __syncthreads();
+      uint32_t bits = 0xffffffffu;
+      if (mask >= 0)
+        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+      for (int j = 0; j < SB; ++j) {
+        float s = 0.f, g = 0.f;
+#pragma unroll
+        for (int i = 0; i < DP; ++i) {
+          s = fmaf(qv[i], Ks[j * D + part * DP + i], s);
+          g = fmaf(gv[i], Vs[j * D + part * DP + i], g);
+        }
+        s = row_sum<TPR>(s);
+        g = row_sum<TPR>(g);
+        float p = exp2f(s * a.scale_log2 - lse);
+        if (!((bits >> j) & 1u)) p = 0.f;
+        const float ds = p * (g - dl);
+#pragma unroll
+        for (int i = 0; i < DP; ++i) dq[i] = fmaf(ds, Ks[j * D + part * DP + i], dq[i]);
+      }
+    }
+  }
+  if (q >= a.Lq) return;
+  const int64_t oo = (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; ++i) Mem<IT>::put(a.dq, oo + i, dq[i] * a.scale);
+}
+
+template <int D, int TPR, class IT, class OT>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
+void bwd_dkdv_simt(KArgs a) {
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
+  constexpr int EO = std::is_same<OT, float>::value ? 4 : 2;
+  __shared__ __attribute__((aligned(16))) float Qs[SB * D];
+  __shared__ __attribute__((aligned(16))) float Gs[SB * D];
+  __shared__ float Ls[SB], Dl[SB];
+
+  const int item = a.kv_order[blockIdx.x / SPLIT];
+  if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
+  const int kt = item % a.nkt;
+  const int bh = item / a.nkt;
+  const int hk = bh % a.Hkv, b = bh / a.Hkv;
+  const int tid = threadIdx.x, part = tid % TPR;
+  const int row = (blockIdx.x % SPLIT) * RPW + tid / TPR;  // key within the tile
+  const int key = kt * TILE + row;
+  const int kcl = min(key, a.Lk - 1);
+
+  float kv[DP], vv[DP], dk[DP], dv[DP];
+  const int64_t ko = (int64_t)b * a.ks[0] + (int64_t)kcl * a.ks[1] + (int64_t)hk * a.ks[2] + part * DP;
+  const int64_t vo = (int64_t)b * a.vs[0] + (int64_t)kcl * a.vs[1] + (int64_t)hk * a.vs[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; i += 4) {
+    Mem<IT>::get4(a.k, ko + i, kv + i);
+    Mem<IT>::get4(a.v, vo + i, vv + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dk[i + j] = dv[i + j] = 0.f;
+  }
+  for (int g = 0; g < a.G; ++g) {
+    const int h = hk * a.G + g;
+    const int mc = map_row(a, b, h, a.nkt, kt);
+    const int e0 = a.col_ptr[mc], e1 = a.col_ptr[mc + 1];
+    const char* qb = (const char*)a.q + ES * ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[2]);
+    const char* gb = (const char*)a.dO + EO * ((int64_t)b * a.dos[0] + (int64_t)h * a.dos[2]);
+    for (int e = e0; e < e1; ++e) {
+      const int qt = a.col_ent[2 * e], mask = a.col_ent[2 * e + 1];
+      for (int sb = 0; sb < TILE / SB; ++sb) {
+        const int q0 = qt * TILE + sb * SB;
+        if (q0 >= a.Lq) break;
+        __syncthreads();
+        stage_rows<D, IT>(Qs, qb, a.qs[1], q0, a.Lq);
+        stage_rows<D, OT>(Gs, gb, a.dos[1], q0, a.Lq);
+        if (tid < 2 * SB) {
+          const int qq = min(q0 + (tid & (SB - 1)), a.Lq - 1);
+          const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qq;
+          if (tid < SB) Ls[tid] = a.lse[rs];
+          else Dl[tid - SB] = a.delta[rs];
+        }
+        __syncthreads();
+        uint32_t bits = 0xffffffffu;
+        if (mask >= 0)
+          bits = (uint32_t)(a.col_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+        for (int j = 0; j < SB; ++j) {
+          float s = 0.f, gd = 0.f;
+#pragma unroll
+          for (int i = 0; i < DP; ++i) {
+            s = fmaf(kv[i], Qs[j * D + part * DP + i], s);
+            gd = fmaf(vv[i], Gs[j * D + part * DP + i], gd);
+          }
+          s = row_sum<TPR>(s);
+          gd = row_sum<TPR>(gd);
+          float p = exp2f(s * a.scale_log2 - Ls[j]);
+          if (!((bits >> j) & 1u)) p = 0.f;
+          const float ds = p * (gd - Dl[j]);
+#pragma unroll
+          for (int i = 0; i < DP; ++i) {
+            dv[i] = fmaf(p, Gs[j * D + part * DP + i], dv[i]);
+            dk[i] = fmaf(ds, Qs[j * D + part * DP + i], dk[i]);
+          }
+        }
+      }
+    }
+  }
+  if (key >= a.Lk) return;
+  const int64_t dko = (int64_t)b * a.dks[0] + (int64_t)key * a.dks[1] + (int64_t)hk * a.dks[2] + part * DP;
+  const int64_t dvo = (int64_t)b * a.dvs[0] + (int64_t)key * a.dvs[1] + (int64_t)hk * a.dvs[2] + part * DP;
+#pragma unroll
+  for (int i = 0; i < DP; ++i) {
+    Mem<IT>::put(a.dk, dko + i, dk[i] * a.scale);
+    Mem<IT>::put(a.dv, dvo + i, dv[i]);
+  }
+}
+
+// the stages of one (D, TPR, input, output) combination
+template <int D, int TPR, class IT, class OT>
+struct Simt {
+  static constexpr int SPLIT = TILE * TPR / 512;
+  static void fwd(const KArgs& a, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((fwd_simt<D, TPR, IT, OT>), dim3(grid * SPLIT), dim3(512), 0, st, a);
+  }
+  static void bwd(const KArgs& a, int stage, int q_grid, int kv_grid, hipStream_t st) {
+    if (stage == MATTN_BWD_PRE) {
+      const int64_t rows = (int64_t)a.B * a.Lq * a.Hq;
+      hipLaunchKernelGGL((bwd_delta_simt<D, OT>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, a);
+    } else if (stage == MATTN_BWD_DKDV) {
+      hipLaunchKernelGGL((bwd_dkdv_simt<D, TPR, IT, OT>), dim3(kv_grid * SPLIT), dim3(512), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_simt<D, TPR, IT, OT>), dim3(q_grid * SPLIT), dim3(512), 0, st, a);
+    }
+  }
+};
+
+// f(Simt<...>{}) for the problem's combination: float32 at D = 64, 128 (4
+// threads per row) or 256 (8); 16-bit inputs at D = 256 with a float32 or
+// same-dtype output
+template <class F>
+hipError_t dispatch(int D, int dtype, int o_dtype, F&& f) {
+  const bool of32 = o_dtype == MATTN_F32;
+  if (dtype == MATTN_F32) {
+    if (D == 64) f(Simt<64, 4, float, float>{});
+    else if (D == 128) f(Simt<128, 4, float, float>{});
+    else f(Simt<256, 8, float, float>{});
+  } else if (dtype == MATTN_BF16) {
+    if (of32) f(Simt<256, 8, bf16_tag, float>{});
+    else f(Simt<256, 8, bf16_tag, bf16_tag>{});
+  } else {
+    if (of32) f(Simt<256, 8, f16_tag, float>{});
+    else f(Simt<256, 8, f16_tag, f16_tag>{});
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st) {
+  return dispatch(D, dtype, o_dtype, [&](auto s) { decltype(s)::fwd(a, grid, st); });
+}
+
+hipError_t launch_bwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid, int kv_grid,
+                           hipStream_t st) {
+  return dispatch(D, dtype, o_dtype, [&](auto s) { decltype(s)::bwd(a, stage, q_grid, kv_grid, st); });
+}
+
+}  // namespace mattn

@@ -88,6 +88,20 @@ def test_causal_fwd_bwd(dtype, d):
     run_case((2, 384, 384, 2, 2, d), dict(is_causal=True, block_size=128), dtype)
 
 
+# head dimension 256: the float32 SIMT kernels for every input dtype (ragged
+# lengths, grouped heads, a partial-tile mask, both output dtypes)
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_d256_causal_gqa_fwd_bwd(dtype):
+    run_case((2, 300, 300, 4, 2, 256), dict(is_causal=True, block_size=128), dtype,
+             scaled=dtype != "float32")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_d256_masked_16bit_output(dtype):
+    run_case((1, 200, 330, 2, 1, 256), dict(mask_fn=lambda h, q, k: (q + 3 * h - k) % 7 != 0,
+                                            block_size=64), dtype, out_dtype=dtype, seed=3)
+
+
 def test_full_attention_no_block_size():
     run_case((1, 256, 256, 2, 2, 128), {}, "bfloat16")
 

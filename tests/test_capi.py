@@ -90,6 +90,8 @@ def test_validate_codes(lib):
     assert _validate(lib, _problem(Hkv=3)) == -2          # Hq % Hkv
     assert _validate(lib, _problem(B=0)) == -2
     assert _validate(lib, _problem(D=96)) == -3
+    assert _validate(lib, _problem(D=256)) == 0
+    assert _validate(lib, _problem(D=512)) == -3
     assert _validate(lib, _problem(dtype=7)) == -4
     assert _validate(lib, _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_BF16)) == -4
     assert _validate(lib, _problem(o_dtype=_lib.MATTN_F16)) == -4   # bf16 in, fp16 out
@@ -147,6 +149,11 @@ def test_workspace_bytes(lib):
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p32)) == 0
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
+    # D = 256 runs on the float32 SIMT kernels for every dtype: delta only, no residual
+    for dt in (_lib.MATTN_BF16, _lib.MATTN_F16, _lib.MATTN_F32):
+        p256 = _problem(D=256, dtype=dt, o_dtype=dt)
+        assert lib.mattn_workspace_bytes(ctypes.byref(p256)) == align(B * Hq * L * 4)
+        assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p256)) == 0
 
 
 def test_flags_validated(lib):

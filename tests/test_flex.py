@@ -1,5 +1,5 @@
 """flex_attention over BlockMask (attention.py:456-692) and head dimensions
-other than 64/128.
+other than 64, 128 and 256.
 
 CPU: the reference's argument checks and exception types.
 GPU: the HIP path against the fp64 oracle on the mask the block mask stands
@@ -236,9 +236,10 @@ def test_flex_slow_evaluates_elements_with_query_head():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d", [16, 32, 96])
+@pytest.mark.parametrize("d", [16, 32, 96, 160, 200])
 def test_masked_attention_padded_head_dim(d):
-    """Head dimensions other than 64/128 (zero-padded on the GPU), fwd + bwd."""
+    """Head dimensions other than 64/128/256 (zero-padded on the GPU to the
+    next of the three), fwd + bwd."""
     import jaxmodules_amd as jm
     from tests.helpers import oracle, seeded_inputs
 
