@@ -225,13 +225,17 @@ class Runner:
         self.p = A._problem(self.q, self.k, self.v, self.o, 1.0 / d ** 0.5, do=self.do, dq=self.dq,
                             dk=self.dk, dv=self.dv)
         self.p.flags = _lib.MATTN_FWD_FOR_BWD
-        nws = int(self.lib.mattn_workspace_bytes(ctypes.byref(self.p)))
+        self.bm = A.device_blockmap(tm, dev)
+        # the backward's flags as the autograd path picks them (stored dS at D = 128)
+        self.p.flags = _lib.MATTN_FWD_FOR_BWD | A.bwd_flags(self.p, self.bm)
+        self.stored_ds = bool(self.p.flags & _lib.MATTN_BWD_DS)
+        nws = int(self.lib.mattn_bwd_workspace_bytes(ctypes.byref(self.p), ctypes.byref(self.bm)))
         self.ws = torch.empty(nws + 256, dtype=torch.uint8, device=dev)
         self.wptr = (self.ws.data_ptr() + 255) & ~255
+        self.ws_bytes = nws
         nres = int(self.lib.mattn_fwd_workspace_bytes(ctypes.byref(self.p)))
         self.res = torch.empty(nres + 256, dtype=torch.uint8, device=dev)
         self.rptr = (self.res.data_ptr() + 255) & ~255
-        self.bm = A.device_blockmap(tm, dev)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.pairs = tm.pairs
         self.fwd_flop = 4 * d * tm.pairs
@@ -353,7 +357,7 @@ def tilemap_build_times(repeats=5):
             dev = bmap.device_trace(plan, "cuda:0")
             ts.append(time.perf_counter() - t0)
         same = all(np.array_equal(getattr(host, f), getattr(dev, f))
-                   for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "row_bits", "col_bits",
+                   for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
                              "q_order", "kv_order")) and host.pairs == dev.pairs
         out["configs"][name] = {"workload": desc, "host_s": round(th, 4),
                                 "device_s": round(float(np.median(ts)), 5),
@@ -375,7 +379,9 @@ def summary(r, ms, kern):
                                                       kern["bwd_dq"]) * 1e-3) / 1e12, 2),
                    "tile_map": {"nnz": r.tm.nnz, "full": r.tm.n_full, "partial": r.tm.n_partial,
                                 "masks": r.tm.n_masks, "built_by": r.trace_how,
-                                "build_s": round(r.trace_s, 3)}}
+                                "build_s": round(r.trace_s, 3)},
+                   "bwd_dq": "from stored dS" if r.stored_ds else "recomputes S and dP",
+                   "bwd_workspace_bytes": r.ws_bytes}
 
 
 def main():
@@ -389,6 +395,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed region, copy 1 GiB once (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--recompute-dq", action="store_true",
+                    help="run dQ by recomputing S and dP (no stored dS) everywhere")
     ap.add_argument("--tilemap", action="store_true",
                     help="instead: time the tile-map build of configs 3-5, host tracer vs GPU classifier")
     args = ap.parse_args()
@@ -402,6 +410,10 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.recompute_dq:
+        from jaxmodules_amd import attention as A
+
+        A.STORE_DS = False
     if args.tilemap:
         print(json.dumps(tilemap_build_times()), flush=True)
         return

@@ -63,6 +63,13 @@ enum mattn_status {
 /* mattn_problem.flags: the forward also leaves in its residual the float16
  * copy of Q that mattn_bwd reads (set it for a forward whose backward runs). */
 #define MATTN_FWD_FOR_BWD 1
+/* mattn_problem.flags: the backward keeps dS: the dK/dV stage stores dS of
+ * every present tile (float16, 32 KiB per 128 x 128 tile) in the workspace and
+ * the dQ stage computes dQ = dS K from it instead of recomputing S and dP.
+ * The workspace then takes mattn_bwd_workspace_bytes(p, bm) bytes.  For
+ * 16-bit inputs at D <= 128 (ignored on the SIMT path).  Faster at D = 128,
+ * where recomputing costs more than streaming 2 bytes per allowed pair. */
+#define MATTN_BWD_DS 2
 
 /* Tile size of the block map, in queries x keys. */
 #define MATTN_TILE_Q 128
@@ -117,17 +124,28 @@ typedef struct mattn_blockmap {
   const int32_t* q_order;
   const int32_t* kv_order;
   int32_t n_q_order, n_kv_order;
+  /* [nnz]: for each col_ent entry, the index in row_ent of the same tile (the
+   * slot of its dS under MATTN_BWD_DS; may be NULL without that flag).     */
+  const int32_t* col_row;
 } mattn_blockmap;
 
 /* Host-only check of a problem (and, when bm != NULL, of the map's sizes).
  * No GPU call; usable without a device. */
 int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
 
-/* Bytes of device workspace mattn_bwd needs (256-byte aligned pointer).
+/* Bytes of device workspace mattn_bwd needs without MATTN_BWD_DS (256-byte
+ * aligned pointer); with it, mattn_bwd_workspace_bytes(p, bm).  0 for an
+ * invalid problem.
  * Head dimensions 64 and 128 with 16-bit inputs run on the MFMA kernels;
  * float32 inputs, and D = 256 for every dtype (the host pads d in (128, 256]
  * with zeros), run on float32 SIMT kernels, whose workspace is delta alone. */
 size_t mattn_workspace_bytes(const mattn_problem* p);
+
+/* Bytes of device workspace mattn_bwd needs for this map, MATTN_BWD_DS
+ * included: mattn_workspace_bytes(p) plus, with that flag on the MFMA path,
+ * 32 KiB per present tile of every (batch, head) -- nnz * (B / map_b) *
+ * (Hq / map_h) tiles.  Host only; 0 for an invalid problem or map. */
+size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* bm);
 
 /* Bytes of the forward's residual buffer (256-byte aligned pointer; 0 for
  * float32 inputs and for D = 256): float16 copies of V and (with
@@ -152,7 +170,7 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
  *   residual  : the forward's residual buffer (16-bit inputs at D <= 128;
  *               that forward ran with MATTN_FWD_FOR_BWD), read only; may be
  *               NULL when mattn_fwd_workspace_bytes(p) == 0
- *   workspace : mattn_workspace_bytes(p) bytes (scratch)
+ *   workspace : mattn_bwd_workspace_bytes(p, bm) bytes (scratch)
  *   dq, dk, dv: gradients of dtype, every element written (no pre-zeroing). */
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* q, const void* k, const void* v,
@@ -161,8 +179,9 @@ int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
 
 /* The three stages of mattn_bwd, in the order they must run on one stream:
  * MATTN_BWD_PRE (delta = rowsum(dO * O) and the float16 copy of dO, into the
- * workspace), MATTN_BWD_DKDV (also writes the float16 copy of K into the
- * workspace), then MATTN_BWD_DQ (reads both).  mattn_bwd == the three stages
+ * workspace), MATTN_BWD_DKDV (also writes the float16 copy of K, and with
+ * MATTN_BWD_DS every tile's dS, into the workspace), then MATTN_BWD_DQ (reads
+ * them).  mattn_bwd == the three stages
  * in order.  Same arguments as mattn_bwd; exposed so a caller can time the
  * stages. */
 enum mattn_bwd_stage { MATTN_BWD_PRE = 0, MATTN_BWD_DKDV = 1, MATTN_BWD_DQ = 2 };
@@ -181,8 +200,8 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
  * counterpart in the reference (whose backward is a jax custom_vjp rule); it
  * is for callers that cannot allocate: code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Problems whose
- * mattn_workspace_bytes(p) exceeds MATTN_SCRATCH_BYTES return
- * MATTN_ERR_SCRATCH.  Every call on one device shares that device's scratch:
+ * mattn_bwd_workspace_bytes(p, bm) exceeds MATTN_SCRATCH_BYTES return
+ * MATTN_ERR_SCRATCH (clear MATTN_BWD_DS to run a larger one here).  Every call on one device shares that device's scratch:
  * calls that overlap on one device (other streams, other threads) race.  No
  * scratch content carries over between calls (each call writes all it reads). */
 int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm,

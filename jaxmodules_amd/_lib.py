@@ -17,8 +17,9 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
 
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 MATTN_FWD_FOR_BWD = 1
+MATTN_BWD_DS = 2
 TILE_Q = TILE_K = 128
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 STATUS = {
     0: "MATTN_OK",
@@ -35,7 +36,8 @@ STATUS = {
 }
 
 # every symbol include/mattn.h declares
-EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_fwd_workspace_bytes", "mattn_fwd", "mattn_bwd",
+EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_bwd_workspace_bytes", "mattn_fwd_workspace_bytes",
+           "mattn_fwd", "mattn_bwd",
            "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version", "mattn_maskspec_validate",
            "mattn_tilemap_classify", "mattn_tilemap_bits", "mattn_bwd_noalloc")
 SCRATCH_BYTES = 256 << 20  # MATTN_SCRATCH_BYTES
@@ -65,6 +67,7 @@ class MattnBlockmap(ctypes.Structure):
         ("row_bits", ctypes.c_void_p), ("col_bits", ctypes.c_void_p),
         ("q_order", ctypes.c_void_p), ("kv_order", ctypes.c_void_p),
         ("n_q_order", ctypes.c_int32), ("n_kv_order", ctypes.c_int32),
+        ("col_row", ctypes.c_void_p),
     ]
 
 
@@ -109,6 +112,8 @@ def load():
         lib.mattn_validate.restype = ctypes.c_int
         lib.mattn_workspace_bytes.argtypes = [P]
         lib.mattn_workspace_bytes.restype = ctypes.c_size_t
+        lib.mattn_bwd_workspace_bytes.argtypes = [P, M]
+        lib.mattn_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mattn_fwd_workspace_bytes.argtypes = [P]
         lib.mattn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mattn_fwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp]

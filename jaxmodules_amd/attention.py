@@ -205,7 +205,7 @@ def device_blockmap(tm: bmap.TileMap, device) -> _lib.MattnBlockmap:
 
     bufs = dict(
         row_ptr=up(tm.row_ptr), row_ent=up(tm.row_ent.reshape(-1)),
-        col_ptr=up(tm.col_ptr), col_ent=up(tm.col_ent.reshape(-1)),
+        col_ptr=up(tm.col_ptr), col_ent=up(tm.col_ent.reshape(-1)), col_row=up(tm.col_row),
         row_bits=up(tm.row_bits.view(np.int64).reshape(-1)),
         col_bits=up(tm.col_bits.view(np.int64).reshape(-1)),
         q_order=up(tm.q_order), kv_order=up(tm.kv_order))
@@ -216,7 +216,8 @@ def device_blockmap(tm: bmap.TileMap, device) -> _lib.MattnBlockmap:
         row_bits=bufs["row_bits"].data_ptr() if tm.n_masks else None,
         col_bits=bufs["col_bits"].data_ptr() if tm.n_masks else None,
         q_order=bufs["q_order"].data_ptr(), kv_order=bufs["kv_order"].data_ptr(),
-        n_q_order=int(tm.q_order.size), n_kv_order=int(tm.kv_order.size))
+        n_q_order=int(tm.q_order.size), n_kv_order=int(tm.kv_order.size),
+        col_row=bufs["col_row"].data_ptr() if tm.nnz else None)
     tm.device[key] = (bufs, s)
     return s
 
@@ -297,6 +298,32 @@ def _aligned(t):
     return None if t is None else (t.data_ptr() + 255) & ~255
 
 
+# Whether the backward keeps dS (MATTN_BWD_DS): None = where it pays (16-bit
+# inputs at kernel head dim 128, dS within DS_MAX_BYTES), True = wherever the
+# kernels support it (16-bit inputs, head dim <= 128), False = never.
+STORE_DS: Optional[bool] = None
+DS_MAX_BYTES = 16 << 30
+
+
+def bwd_flags(p, bm) -> int:
+    """mattn_problem.flags for the backward of problem ``p`` on map ``bm``: the
+    forward's flags plus MATTN_BWD_DS where STORE_DS selects it."""
+    lib = _lib.load()
+    flags = p.flags & ~_lib.MATTN_BWD_DS
+    if STORE_DS is False or p.dtype == _lib.MATTN_F32 or p.D > 128:
+        return flags
+    if STORE_DS is None:
+        if p.D != 128:
+            return flags
+        p.flags = flags | _lib.MATTN_BWD_DS
+        extra = int(lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm))) \
+            - int(lib.mattn_workspace_bytes(ctypes.byref(p)))
+        p.flags = flags
+        if extra > DS_MAX_BYTES:
+            return flags
+    return flags | _lib.MATTN_BWD_DS
+
+
 def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None):
     """(dQ, dK, dV) via mattn_bwd; ``res`` is mattn_forward's residual (run
     with for_backward=True)."""
@@ -306,8 +333,12 @@ def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     p = _problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
-    ws, wptr = _workspace(max(int(lib.mattn_workspace_bytes(ctypes.byref(p))), 256), q.device)
     bm = device_blockmap(tm, q.device)
+    p.flags = bwd_flags(p, bm)
+    nws = int(lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)))
+    if nws == 0:
+        _lib.check(lib.mattn_validate(ctypes.byref(p), ctypes.byref(bm)), "mattn_bwd")
+    ws, wptr = _workspace(max(nws, 256), q.device)
     _lib.check(lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
                              v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(), _aligned(res),
                              wptr, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)),

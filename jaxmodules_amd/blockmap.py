@@ -163,6 +163,7 @@ class TileMap:
     row_ent: np.ndarray     # int32 [nnz, 2] (key tile, mask id)
     col_ptr: np.ndarray     # int32 [map_b*map_h*nkt + 1]
     col_ent: np.ndarray     # int32 [nnz, 2] (query tile, mask id)
+    col_row: np.ndarray     # int32 [nnz]: index in row_ent of each col_ent entry (same tile)
     row_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, q] bit j = key 64w + j allowed
     col_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, k] bit j = query 64w + j allowed
     q_order: np.ndarray     # int32 launch order of (b, h, query tile) items
@@ -367,6 +368,7 @@ def _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_f
     col_ptr = np.zeros(nmap * nkt + 1, np.int64)
     np.cumsum(np.bincount(c, minlength=nmap * nkt), out=col_ptr[1:])
     col_ent = np.stack([qt_of[oc], mid[oc]], axis=1).astype(np.int32).reshape(-1, 2)
+    col_row = oc.astype(np.int32)           # the row-ordered index of each column entry
 
     # launch order (weights = present tiles per work item, +1 for the epilogue)
     row_cnt = np.diff(row_ptr).reshape(map_b, map_h, nqt)
@@ -388,7 +390,7 @@ def _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_f
 
     pairs = pairs_map * (B // map_b) * (Hq // map_h)
     return TileMap(B, Hq, Hkv, N, L, map_b, map_h, nqt, nkt,
-                   row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent,
+                   row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent, col_row,
                    np.ascontiguousarray(rb), np.ascontiguousarray(cb), q_order, kv_order, pairs,
                    n_full=n_full, n_partial=n_partial, trace_seconds=time.perf_counter() - t0)
 

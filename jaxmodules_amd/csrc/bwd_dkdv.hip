@@ -35,7 +35,14 @@ namespace mattn {
 // The two query halves' dK/dV partials of a key are summed through LDS at the
 // end, and the rows leave through an LDS-staged tile, 16 bytes per lane along
 // each row.
-template <int D, class Tag>
+// DS (MATTN_BWD_DS): each wave also leaves its 32 x 32 block of dS~ for the
+// dQ kernel, as it holds it for the dK product (lane = key; the DS_TILE layout
+// in common.hpp: the dQ kernel, which streams it from HBM with LDS to spare,
+// does the transposition).  The two 16-byte stores per lane go out
+// (nontemporal: read once, much later) right after the next sub-block's
+// barrier, or after the loop, so that they have a whole step to complete
+// before the wait ahead of the following barrier, which counts stores too.
+template <int D, class Tag, bool DS>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
   using E = Elt<Tag>;
@@ -155,6 +162,11 @@ void bwd_dkdv_mfma(KArgs a) {
   // below test wave-uniform values (scalar registers), not per-lane ones.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   int cur_qt = 0, cur_mid = -1;
+  int cur_ri = 0;                      // row-entry index of the column entry (DS)
+  uint16_t* dsp0 = nullptr;            // DS: dS slot of the sub-block in each buffer
+  uint16_t* dsp1 = nullptr;
+  uint16_t* dpend = nullptr;           // DS: where the chunks in sf go (null: none)
+  u32x4 sf[2];                         // DS: the last sub-block's dS~ chunks (sk)
   const float* lrow = nullptr;  // lse - log2 f (wave 6) or delta (wave 7) row of the current head
 
   // The next sub-block's loads in two parts: prep() advances the cursor
@@ -183,8 +195,13 @@ void bwd_dkdv_mfma(KArgs a) {
         qsc_h = a.qsc + (b * a.Hq + h) * a.nqt;
         asc_h = a.asc + (b * a.Hq + h) * a.nqt;
       }
-      ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s);
+      if constexpr (DS)
+        ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s, a.col_row, cur_ri);
+      else
+        ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s);
     }
+    if constexpr (DS)  // this query half's two dQ waves (2 lhalf, 2 lhalf + 1) of the tile's slot
+      (BUF ? dsp1 : dsp0) = a.ds + (ds_rep(a, b, rh_head) + cur_ri) * DS_TILE + lhalf * (2 * 8 * 512);
     (BUF ? mid1 : mid0) = cur_mid;
     (BUF ? sh1 : sh0) = cur_s;
     (BUF ? rh1 : rh0) = cur_r;
@@ -219,6 +236,12 @@ void bwd_dkdv_mfma(KArgs a) {
   f32x16 dk[NMD], dv[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+
+  const int dsp_l0 = ds_pos(lane, 0) * 8, dsp_l1 = 512 + ds_pos(lane, 1) * 8;  // chunk offsets per t
+  auto store_ds = [&]() {
+    __builtin_nontemporal_store(sf[0], (u32x4*)(dpend + dsp_l0));
+    __builtin_nontemporal_store(sf[1], (u32x4*)(dpend + dsp_l1));
+  };
   // set by the prologue: the column's K' / V' tile scales
   float ksc = 1.f, ivs = 1.f;
   float acc_s = 1.f, acc_r = 1.f;  // scales f s and r the accumulators are in
@@ -275,6 +298,7 @@ void bwd_dkdv_mfma(KArgs a) {
       });
       dma_on = false;
     }
+
     // lse, delta and the mask words read together: one LDS round trip
     const uint64_t mw = (BUF ? M1 : M0)[kloc];
     f32x4 dv4[4];
@@ -305,6 +329,13 @@ void bwd_dkdv_mfma(KArgs a) {
     for (int r = 0; r < 16; r += 2) {
       pk[r >> 3][(r & 7) >> 1] = H::pack2(st[r], st[r + 1]);
       sk[r >> 3][(r & 7) >> 1] = H::pack2(dp[r], dp[r + 1]);
+    }
+    if constexpr (DS) {
+      // sk[t] holds queries 16 t + 4 hi + 8 j + i of key kloc (slots 4 j + i):
+      // the chunk of lane `lane` in block (2 lhalf + qh, kg, t)
+      sf[0] = sk[0];
+      sf[1] = sk[1];
+      dpend = (BUF ? dsp1 : dsp0) + (8 * qh + 2 * kg) * 512;
     }
     {
       // dV^T / dK^T pipelined by hand like S / dP.  Per 16-query k-step ks, the
@@ -359,6 +390,9 @@ void bwd_dkdv_mfma(KArgs a) {
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     const bool masked = (BUF ? mid1 : mid0) >= 0;
     if (s + 1 < tot) launch(std::integral_constant<int, 1 - BUF>{});
+    if constexpr (DS) {
+      if (dpend) store_ds();  // sub-block s - 1's fragments
+    }
     step(bufc, masked);
   };
   if (tot > 0) {
@@ -391,6 +425,9 @@ void bwd_dkdv_mfma(KArgs a) {
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});
+  }
+  if constexpr (DS) {
+    if (dpend) store_ds();  // the last sub-block's fragments
   }
 
   // dK / dV: the second query half's partials join the first's through LDS
@@ -465,14 +502,20 @@ void bwd_dkdv_mfma(KArgs a) {
 // launcher
 // ---------------------------------------------------------------------------
 
-hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
+template <bool DS>
+static void launch_dkdv_t(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
   if (dtype == MATTN_BF16) {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, bf16_tag>), dim3(grid), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, bf16_tag>), dim3(grid), dim3(512), 0, st, a);
+    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, bf16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, bf16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
   } else {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, f16_tag>), dim3(grid), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, f16_tag>), dim3(grid), dim3(512), 0, st, a);
+    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, f16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, f16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
   }
+}
+
+hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
+  if (a.ds) launch_dkdv_t<true>(a, D, dtype, grid, st);
+  else launch_dkdv_t<false>(a, D, dtype, grid, st);
   return hipGetLastError();
 }
 

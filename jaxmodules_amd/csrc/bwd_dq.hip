@@ -272,10 +272,232 @@ void bwd_dq_mfma(KArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// dQ from the stored dS (MATTN_BWD_DS)
+// ---------------------------------------------------------------------------
+// The dK/dV kernel left dS~ = f s dS of every present tile as its waves held
+// it (lane = key; DS_TILE layout in common.hpp), so per 64-key sub-block each
+// wave only streams its four 1 KiB blocks (one nontemporal 16-byte load per
+// lane each, PF sub-blocks ahead of use), turns them into B operands (lane =
+// query) through 4 KiB of LDS of its own -- written as loaded, read back with
+// ds_read_b64_tr_b16, which the blocks' chunk order makes conflict-free -- and
+// runs
+//   dQ^T += K'^T dS~^T    (A: K'^T by transposed reads of the K' tile in LDS)
+// 2 D flop per pair instead of recomputing S and dP (another 4 D); the
+// kernel streams 2 bytes per allowed pair from HBM.  Masked elements of a
+// partial tile hold dS = 0, so no mask is read.  K' sub-blocks are
+// double-buffered in LDS as in bwd_dq_mfma; the accumulator is in units of
+// f s k_t (f s is the tile's asc), rescaled when the K' scale k_t changes.
+template <int D, class Tag>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+void bwd_dq_ds(KArgs a) {
+  using E = Elt<Tag>;
+  using H = Elt<f16_tag>;
+  using TL = TileLoad<D>;
+  constexpr int BN = 64;
+  constexpr int NMD = D / 32;
+  constexpr int NI = D / 32;       // load instructions per wave per 64-row sub-block
+  constexpr int BLK = 512;         // elements one load instruction fills
+  constexpr int PF = 3;            // sub-blocks of fragments in flight ahead of use
+
+  __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t FX[4 * 2048];  // per wave: one sub-block's blocks
+
+  const int item = a.q_order[blockIdx.x];
+  if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  const int qt = item % a.nqt;
+  const int bh = item / a.nqt;
+  const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
+  const int mrow = map_row(a, b, h, a.nqt, qt);
+  const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int nsb = 2 * (e1 - e0);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hi = lane >> 5;
+  // the epilogue's operands, loaded here and pinned (empty asm) rather than
+  // left as scalar loads in flight across the loop's hand-counted LDS waits
+  const int r0 = qt * TILE + 32 * wave;
+  int nrows = min(32, a.Lq - r0);  // this wave's output rows
+  int64_t orow = (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2];
+  int64_t ostr = a.dqs[1];
+  void* odq = a.dq;
+  float osc = a.scale * pow2_rcp(a.asc[item]);
+  asm volatile("" : "+s"(nrows), "+s"(orow), "+s"(ostr), "+s"(odq), "+v"(osc));
+
+  const int tb = (b * a.Hkv + hk) * a.nkt;  // first tile of this kv head in the per-tile arrays
+  const uint16_t* kb = a.kh + (int64_t)tb * TILE * D;
+  const float* ksc = a.ksc + tb;
+  // this wave's fragments of tile e: frag + e * DS_TILE + ks * 512 (ks = 0..7)
+  const uint16_t* frag = a.ds + ds_rep(a, b, h) * DS_TILE + wave * 8 * 512 + lane * 8;
+  uint32_t kld[NI];  // source byte offsets of this lane's load slots
+#pragma unroll
+  for (int i = 0; i < NI; ++i) kld[i] = 2 * TL::src_off(NI * wave + i, lane, D);
+  const int tz = 32 * (swz<D>(4 * hi + ((lane & 15) >> 2)) >> 2);
+  const int tb0 = tr_src<D>(lane, 0, 0) - tz;
+  const int tb1 = tr_src<D>(lane, 0, 1) - tz;
+  const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);
+  EntryCache ec;
+  // The wave's LDS blocks: block b = 2 (kk / 2) + t (32-key group kk / 2 of the
+  // sub-block, 16-query half t) at 1 KiB b, chunk of lane l at 16 l.  B operand
+  // of k-step kk (keys 16 kk + 4 hi + 8 j + i, i = 0..3, in slots 4 j + i) of
+  // lane (query 16 t + i16, half hi): read j supplies, for lane i16 of its
+  // 16-lane group, the 8 bytes of key 16 (kk % 2) + 4 hi + 8 j + i16 / 4 (of
+  // the 32-key group) and queries 16 t + 4 q4 + 0..3, q4 = i16 % 4: chunk of
+  // lane rl = key + 32 (q4 % 2) at position ds_pos(rl, t), bytes 8 (q4 / 2).
+  // With P0 = ds_pos of the j = 0, kk = 0 lane, read (kk, j) sits at
+  // byte 2048 (kk / 2) + 256 (kk % 2) + 128 (j ^ t) past P0's chunk.
+  const uint32_t fxw = lds_addr(FX) + 4096 * wave;
+  uint32_t fb0, fb1;  // read bases for j = 0 and j = 1
+  {
+    const int i16 = lane & 15, t = (lane >> 4) & 1, q4 = i16 & 3;
+    const int rl = 4 * hi + (i16 >> 2) + 32 * (q4 & 1);
+    const uint32_t c = fxw + 1024 * t + 16 * ds_pos(rl, 0) + 8 * (q4 >> 1);
+    fb0 = c + 128 * t;
+    fb1 = c + 128 * (1 - t);
+  }
+
+  // map entry of sub-block s: key tile and K' scale (s / 2 is the tile's entry)
+  auto entry = [&](int s, int& kt, float& ks) {
+    int m;
+    float unused;
+    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, m, ksc, ksc, ks, unused);
+  };
+  auto launch = [&](int s, int kt, auto bufc) {  // global -> LDS loads of sub-block s's K' rows
+    constexpr int BUF = decltype(bufc)::value;
+    const char* kp = (const char*)(kb + (int64_t)(kt * TILE + (s & 1) * BN) * D);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) lds_load16(kp + kld[i], (BUF ? K1 : K0) + wofs + i * BLK);
+  };
+  // fragments of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2)
+  auto fetch = [&](int s, u32x4 (&f)[4]) {
+    const uint16_t* p = frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) f[k] = __builtin_nontemporal_load((const u32x4*)(p + k * 512));
+  };
+
+  f32x16 acc[NMD];
+#pragma unroll
+  for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
+  float kcur = 1.f;  // K' tile scale the accumulator is in
+
+  auto step = [&](auto bufc, const u32x4 (&f)[4], float sks) {
+    constexpr int BUF = decltype(bufc)::value;
+    if (sks != kcur) {  // a tile with another K' scale (uniform; powers of two: exact)
+      const float r = sks / kcur;
+#pragma unroll
+      for (int i = 0; i < NMD; ++i) acc[i] *= r;
+      kcur = sks;
+    }
+    constexpr int PQ = 2, NSTEP = 4 * NMD;  // (k-step, d tile)
+    const uint32_t kb0 = lds_addr(BUF ? K1 : K0);
+    const int tzo = opaque(tz);
+    const uint32_t a0 = kb0 + 2 * (uint32_t)opaque(tb0), a1 = kb0 + 2 * (uint32_t)opaque(tb1);
+    // the sub-block's dS~ blocks into the wave's LDS and back transposed; the
+    // previous sub-block's reads of FX returned before its last MFMA (LDS
+    // serves a wave in order), so these writes cannot overtake them
+    const uint32_t fxo = opaque(fxw) + 16 * lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ds_write128(fxo + 1024 * k, f[k]);
+    u32x2 bq[4][2];
+    static_for<4>([&](auto kc) {
+      constexpr int kk = decltype(kc)::value, off = 2048 * (kk / 2) + 256 * (kk % 2);
+      bq[kk][0] = ds_read_tr8<off>(fb0);
+      bq[kk][1] = ds_read_tr8<off>(fb1);
+    });
+    u32x2 lo[PQ + 1], up[PQ + 1];
+    auto rq = [&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PQ + 1);
+      const uint32_t xm = 2 * (uint32_t)((32 * mt) ^ tzo);
+      lo[sl] = ds_read_tr8<32 * ks * D>(a0 + xm);
+      up[sl] = ds_read_tr8<32 * ks * D>(a1 + xm);
+    };
+    static_for<PQ>(rq);
+    static_for<NSTEP>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PQ + 1);
+      if constexpr (i + PQ < NSTEP) rq(std::integral_constant<int, i + PQ>{});
+      lgkm_wait<2 * (i + PQ < NSTEP ? PQ : NSTEP - 1 - i)>();
+      if constexpr (i == 0) {  // this wait also covered the earlier FX writes and reads
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          hold(bq[kk][0]);
+          hold(bq[kk][1]);
+        }
+      }
+      hold(lo[sl]);
+      hold(up[sl]);
+      acc[mt] = H::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]},
+                        u32x4{bq[ks][0][0], bq[ks][0][1], bq[ks][1][0], bq[ks][1][1]}, acc[mt]);
+      hold(acc[mt]);
+    });
+  };
+
+  // Sub-block s: its K' rows were loaded (into buffer s % 2) one iteration
+  // ahead, its fragments PF iterations ahead into ring slot s % (PF + 1).  The
+  // wait before the barrier covers this wave's K' loads of s; the fragment
+  // loads issued after them (those of s + 1 .. s + PF - 1 that exist: 4 loads
+  // each) may stay outstanding, since vector memory loads return in order.
+  u32x4 fr[PF + 1][4];
+  int nkt_ = 0;
+  float nks = 1.f;  // key tile and K' scale of the prepared sub-block
+  if (nsb > 0) {
+    entry(0, nkt_, nks);
+    launch(0, nkt_, std::integral_constant<int, 0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<PF>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      if (p < nsb) fetch(p, fr[p]);
+    });
+  }
+  auto iter = [&](int s, auto bufc, auto slc) {
+    constexpr int BUF = decltype(bufc)::value, SL = decltype(slc)::value;
+    const float sks = nks;
+    int kt1 = 0;
+    if (s + 1 < nsb) entry(s + 1, kt1, nks);
+    // this wave's K' loads of s landed; younger fragment loads may be in flight
+    static_assert(PF == 3, "the waits below count PF - 1 = 2 younger sub-blocks");
+    if (s + 2 < nsb) __builtin_amdgcn_s_waitcnt(vmcnt_only(8));
+    else if (s + 1 < nsb) __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
+    // wave's operand reads ended with lgkmcnt(0)).  A bare barrier: the fence
+    // of __syncthreads would also wait for the fragment loads in flight.
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < nsb) launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
+    __builtin_amdgcn_sched_barrier(0);  // the fragment loads stay behind the K' loads
+    if (s + PF < nsb) fetch(s + PF, fr[(SL + PF) % (PF + 1)]);
+    step(bufc, fr[SL], sks);
+  };
+  // unrolled by 4 (2 K' buffers, 4 fragment slots): every index static
+  for (int s = 0; s < nsb; s += 4) {
+    iter(s, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if (s + 2 < nsb) iter(s + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{});
+    if (s + 3 < nsb) iter(s + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 3>{});
+  }
+
+  // dQ through LDS (a quarter of the K' buffers per wave, free once every wave is done)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint16_t* stage = (wave < 2 ? K0 : K1) + (wave & 1) * 32 * D;
+  static_assert(2 * 32 * D <= BN * D, "output staging");
+  store_rows<D, 2>(acc, osc * pow2_rcp(kcur), stage, odq, orow, ostr, nrows, lane, E::pack2);
+}
+
+// ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
 
 hipError_t launch_dq(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
+  if (a.ds) {
+    if (dtype == MATTN_BF16) {
+      if (D == 64) hipLaunchKernelGGL((bwd_dq_ds<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((bwd_dq_ds<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+    } else {
+      if (D == 64) hipLaunchKernelGGL((bwd_dq_ds<64, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((bwd_dq_ds<128, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+  }
   if (dtype == MATTN_BF16) {
     if (D == 64) hipLaunchKernelGGL((bwd_dq_mfma<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((bwd_dq_mfma<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);

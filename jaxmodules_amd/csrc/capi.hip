@@ -19,7 +19,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 
@@ -38,6 +38,14 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // problems served by the SIMT kernels, which need no residual and no
 // backward workspace beyond delta
 bool simt_path(const mattn_problem* p) { return p->dtype == MATTN_F32 || p->D > 128; }
+
+// the backward keeps dS (MATTN_BWD_DS on the MFMA path)
+bool ds_path(const mattn_problem* p) { return (p->flags & MATTN_BWD_DS) && !simt_path(p); }
+
+// dS tiles of the whole problem: the map's present tiles once per (b, h) it covers
+size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
+  return (size_t)bm->nnz * (bm->map_b == 1 ? p->B : 1) * (bm->map_h == 1 ? p->Hq : 1);
+}
 
 // Forward residual (16-bit inputs, D <= 128): V as float16 times a power of two per
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
@@ -141,7 +149,7 @@ const char* mattn_strerror(int status) {
     case MATTN_ERR_BLOCKMAP: return "block map inconsistent with the problem";
     case MATTN_ERR_LAUNCH: return "kernel launch failed";
     case MATTN_ERR_TOO_LARGE: return "problem exceeds 32-bit index ranges";
-    case MATTN_ERR_SCRATCH: return "backward workspace exceeds the library's static scratch (MATTN_SCRATCH_BYTES)";
+    case MATTN_ERR_SCRATCH: return "backward workspace exceeds the library's static scratch (MATTN_SCRATCH_BYTES; clear MATTN_BWD_DS)";
     case MATTN_ERR_DEVICE: return "the HIP runtime could not resolve the device or its scratch";
     default: return "unknown status";
   }
@@ -156,7 +164,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite
-  if (p->flags & ~MATTN_FWD_FOR_BWD) return MATTN_ERR_SHAPE;
+  if (p->flags & ~(MATTN_FWD_FOR_BWD | MATTN_BWD_DS)) return MATTN_ERR_SHAPE;
   const int es = elem_size(p->dtype), eo = elem_size(p->o_dtype);
   if (!strides_ok(p->q_stride, es) || !strides_ok(p->k_stride, es) || !strides_ok(p->v_stride, es) ||
       !strides_ok(p->dq_stride, es) || !strides_ok(p->dk_stride, es) ||
@@ -192,6 +200,12 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
 size_t mattn_workspace_bytes(const mattn_problem* p) {
   if (mattn_validate(p, nullptr) != MATTN_OK) return 0;
   return ws_layout(p).total;
+}
+
+size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* bm) {
+  if (!bm || mattn_validate(p, bm) != MATTN_OK) return 0;
+  const size_t base = ws_layout(p).total;
+  return ds_path(p) ? base + ds_slots(p, bm) * DS_TILE * 2 : base;
 }
 
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p) {
@@ -236,6 +250,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   if (stage != MATTN_BWD_PRE && stage != MATTN_BWD_DKDV && stage != MATTN_BWD_DQ) return MATTN_ERR_SHAPE;
   if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
   if (!simt_path(p) && !residual) return MATTN_ERR_NULL;
+  if (ds_path(p) && bm->nnz > 0 && !bm->col_row) return MATTN_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
       !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u) ||
       ((uintptr_t)residual & 255u))
@@ -268,6 +283,11 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.vsc = (float*)(res + r.vsc);
     a.vmax = (float*)(res + r.vmax);
     a.qsc = (float*)(res + r.qsc);
+    if (ds_path(p)) {  // dS after the workspace's other parts (w.total is 256-byte aligned)
+      a.ds = (uint16_t*)(ws + w.total);
+      a.col_row = bm->col_row;
+      a.ds_nnz = bm->nnz;
+    }
   }
   hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
                                   bm->n_kv_order, (hipStream_t)stream);
@@ -317,7 +337,8 @@ int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm, const vo
                       const void* residual, void* dq, void* dk, void* dv, void* stream) {
   const int rc = mattn_validate(p, bm);
   if (rc != MATTN_OK) return rc;
-  if (ws_layout(p).total > (size_t)MATTN_SCRATCH_BYTES) return MATTN_ERR_SCRATCH;
+  const size_t need = bm ? mattn_bwd_workspace_bytes(p, bm) : ws_layout(p).total;
+  if (need > (size_t)MATTN_SCRATCH_BYTES) return MATTN_ERR_SCRATCH;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MATTN_ERR_DEVICE;
   void* ws = device_scratch(dev);

@@ -87,7 +87,30 @@ struct KArgs {
   const uint64_t* col_bits;
   const int* q_order;
   const int* kv_order;
+  // MATTN_BWD_DS: dS fragments of every present tile (null: dQ recomputes dS);
+  // slot of tile e (row-entry index) of (b, h): rep * ds_nnz + e, where rep
+  // counts the (b, h) that share the map's entries
+  uint16_t* ds;
+  const int* col_row;
+  int ds_nnz;
 };
+
+// dS storage slot base of (b, h): the map's entries are shared by the (b, h)
+// it broadcasts over, each of which has slots of its own
+__device__ __forceinline__ int64_t ds_rep(const KArgs& a, int b, int h) {
+  const int rb = a.map_b == 1 ? b : 0, rh = a.map_h == 1 ? h : 0;
+  return ((int64_t)rb * (a.map_h == 1 ? a.Hq : 1) + rh) * a.ds_nnz;
+}
+// Elements of one tile's dS (128 x 128 float16), as the dK/dV kernel's waves
+// hold it (lane = key): per 32-query group w, 32-key group kg and 16-query
+// half t, a 1 KiB block at (8 w + 2 kg + t) * 512 elements of 64 16-byte
+// chunks.  Chunk of lane l (key 32 kg + l % 32, hi = l / 32) = queries
+// 32 w + 16 t + 4 hi + 8 j + i (j = 0, 1; i = 0..3) in slots 4 j + i, stored
+// at position ds_pos(l, t) of the block.  The permutation makes the dQ
+// kernel's transposed 8-byte reads of a block (4 keys x 16 queries per
+// 16 lanes) hit 32 distinct bank pairs per 32 lanes.
+constexpr int DS_TILE = TILE * TILE;
+__device__ __forceinline__ int ds_pos(int l, int t) { return l ^ ((((l >> 5) & 1) << 2) | (t << 3)); }
 
 // Power of two s with m * s in [2^(top-1), 2^top) for finite m > 0 (1 otherwise).
 __device__ __forceinline__ float pow2_scale(float m, int top) {
@@ -357,6 +380,26 @@ struct EntryCache {
     t = __builtin_amdgcn_readlane(tile, e - base);
     m = __builtin_amdgcn_readlane(mask, e - base);
   }
+  // also the row-entry index crow[e] of the entry (the dS slot under MATTN_BWD_DS)
+  int rowi = 0;
+  __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m,
+                                      const float* sa, const float* sb, float& a, float& b,
+                                      const int* crow, int& ri) {
+    if (e - base >= 64 || e < base) {  // wave-uniform
+      base = e;
+      const int idx = min(e + lane, e1 - 1);
+      tile = ent[2 * idx];
+      mask = ent[2 * idx + 1];
+      rowi = crow[idx];
+      s0 = sa[tile];
+      s1 = sb[tile];
+    }
+    t = __builtin_amdgcn_readlane(tile, e - base);
+    m = __builtin_amdgcn_readlane(mask, e - base);
+    ri = __builtin_amdgcn_readlane(rowi, e - base);
+    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s0), e - base));
+    b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s1), e - base));
+  }
   __device__ __forceinline__ void get(const int* ent, int e, int e1, int lane, int& t, int& m,
                                       const float* sa, const float* sb, float& a, float& b) {
     if (e - base >= 64 || e < base) {  // wave-uniform
@@ -446,10 +489,23 @@ __device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return v;
 }
+// 16-byte LDS write issued where it stands, like ds_write64 below.
+__device__ __forceinline__ void ds_write128(uint32_t addr, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+// 8-byte LDS write issued where it stands (asm, like ds_read128: the compiler
+// neither reorders it against the asm reads nor makes it wait for LDS-DMA loads
+// it cannot tell apart from it).
+__device__ __forceinline__ void ds_write64(uint32_t addr, u32x2 v) {
+  asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
 // s_waitcnt lgkmcnt(N) in the asm order; values read by ds_read128 /
 // ds_read_tr8 before it are passed through hold() after it, so that nothing
 // using them is scheduled ahead of the wait.  hold() also pins an MFMA result
 // between two asm statements (the MFMA is then issued where it stands).
+// s_waitcnt immediate that waits for at most n outstanding vector memory
+// operations and leaves the other counters alone (gfx9 encoding)
+constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 template <int N>
 __device__ __forceinline__ void lgkm_wait() {
   asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");

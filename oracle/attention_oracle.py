@@ -190,15 +190,15 @@ def dense_forward(Q, K, V, allowed, scale=None):
     return O, lse
 
 
-def dense_backward(Q, K, V, allowed, dO, scale=None):
-    """Analytic gradients of sum(O * dO) w.r.t. Q, K, V, float64."""
+def dense_probs_ds(Q, K, V, allowed, dO, scale=None):
+    """(P, dS) [B,Hq,N,L] float64: the normalised attention weights and the
+    score gradient dS = P (dP - delta), dP = dO V^T, delta = rowsum(dP * P)
+    (attention.py:266-342's per-tile quantities, over the whole matrix)."""
     Q = np.asarray(Q, np.float64)
     K = np.asarray(K, np.float64)
     V = np.asarray(V, np.float64)
     dO = np.asarray(dO, np.float64)
-    B, N, Hq, d = Q.shape
-    Hkv = K.shape[2]
-    G = Hq // Hkv
+    Hq, d = Q.shape[2], Q.shape[3]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     Kx, Vx = _expand_kv(K, Hq), _expand_kv(V, Hq)
     S = np.einsum("bqhd,bkhd->bhqk", Q, Kx) * scale
@@ -210,7 +210,20 @@ def dense_backward(Q, K, V, allowed, dO, scale=None):
     P = P / np.where(l > 0, l, 1.0)
     dP = np.einsum("bqhd,bkhd->bhqk", dO, Vx)
     delta = (dP * P).sum(axis=-1, keepdims=True)      # == rowsum(dO * O)
-    dS = P * (dP - delta)
+    return P, P * (dP - delta)
+
+
+def dense_backward(Q, K, V, allowed, dO, scale=None):
+    """Analytic gradients of sum(O * dO) w.r.t. Q, K, V, float64."""
+    Q = np.asarray(Q, np.float64)
+    K = np.asarray(K, np.float64)
+    dO = np.asarray(dO, np.float64)
+    B, N, Hq, d = Q.shape
+    Hkv = K.shape[2]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    Kx = _expand_kv(K, Hq)
+    P, dS = dense_probs_ds(Q, K, V, allowed, dO, scale)
     dQ = np.einsum("bhqk,bkhd->bqhd", dS, Kx) * scale
     dKx = np.einsum("bhqk,bqhd->bkhd", dS, Q) * scale
     dVx = np.einsum("bhqk,bqhd->bkhd", P, dO)

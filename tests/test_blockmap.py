@@ -56,6 +56,14 @@ def check_consistency(tm, plan):
     cols = np.repeat(np.arange(nmap * tm.nkt), np.diff(tm.col_ptr))
     bwd = {(c // tm.nkt, int(qt), c % tm.nkt, int(m)) for c, (qt, m) in zip(cols, tm.col_ent)}
     assert fwd == bwd
+    # col_row names, for every column entry, the row entry of the same tile (a permutation)
+    assert tm.col_row.dtype == np.int32 and tm.col_row.shape == (tm.nnz,)
+    assert np.array_equal(np.sort(tm.col_row), np.arange(tm.nnz))
+    r_of = rows[tm.col_row]
+    assert np.array_equal(r_of // tm.nqt, cols // tm.nkt)                 # same map slab
+    assert np.array_equal(r_of % tm.nqt, tm.col_ent[:, 0])                # same query tile
+    assert np.array_equal(tm.row_ent[tm.col_row, 0], cols % tm.nkt)       # same key tile
+    assert np.array_equal(tm.row_ent[tm.col_row, 1], tm.col_ent[:, 1])   # same mask
     # masks are distinct and the column bits are the transposed row bits
     seen = set()
     for m in range(tm.n_masks):

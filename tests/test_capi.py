@@ -158,7 +158,41 @@ def test_workspace_bytes(lib):
 
 def test_flags_validated(lib):
     assert _validate(lib, _problem(flags=_lib.MATTN_FWD_FOR_BWD)) == 0
-    assert _validate(lib, _problem(flags=2)) == -2
+    assert _validate(lib, _problem(flags=_lib.MATTN_BWD_DS)) == 0
+    assert _validate(lib, _problem(flags=_lib.MATTN_FWD_FOR_BWD | _lib.MATTN_BWD_DS)) == 0
+    assert _validate(lib, _problem(flags=4)) == -2
+
+
+def test_bwd_workspace_bytes_with_stored_ds(lib):
+    """mattn_bwd_workspace_bytes: the plain workspace, plus with MATTN_BWD_DS
+    32 KiB per present tile of every (batch, head) the map covers -- the map's
+    nnz tiles once per (b, h) it is broadcast over."""
+    p = _problem()                                   # B=2, Hq=8, L=300: nqt = nkt = 3
+    base = lib.mattn_workspace_bytes(ctypes.byref(p))
+    bm = _lib.MattnBlockmap(map_b=1, map_h=1, nqt=3, nkt=3, n_masks=0, nnz=6, row_ptr=8, col_ptr=8,
+                            row_ent=8, col_ent=8, col_row=8, q_order=8, kv_order=8,
+                            n_q_order=2 * 8 * 3, n_kv_order=2 * 2 * 3)
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == base
+    p.flags = _lib.MATTN_BWD_DS
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == base + 6 * 2 * 8 * 32768
+    bm.map_h = 8                                      # per-head map: its nnz covers every head
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == base + 6 * 2 * 32768
+    bm.map_b = 2
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == base + 6 * 32768
+    # the float32 (SIMT) path ignores the flag
+    p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32, flags=_lib.MATTN_BWD_DS)
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p32), ctypes.byref(bm)) == \
+        lib.mattn_workspace_bytes(ctypes.byref(p32))
+    # an invalid map or problem gives 0
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), None) == 0
+    bm.nqt = 2
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == 0
+    # the stored dS needs the column entries' row indices
+    bm.nqt = 3
+    bm.col_row = None
+    args = [8] * 13
+    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), 1, *args[:3], 8, 8, 8, 256, 256, 8, 8, 8,
+                               None) == -1
 
 
 def test_heads_major_long_sequences_validate(lib):

@@ -43,11 +43,13 @@ def _kernels(asm, stem="13bwd_dkdv_mfma"):
     return sorted(set(re.findall(rf"^(_ZN5mattn{stem}\w+):", asm, re.M)))
 
 
-@pytest.mark.parametrize("which", ["dkdv", "dq", "fwd"])
+@pytest.mark.parametrize("which", ["dkdv", "dq", "dq_ds", "fwd"])
 def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm, fwd_asm):
     asm, stem, least, count = {
-        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 100, 4),   # D = 64 / 128 x bfloat16 / float16
+        # D = 64 / 128 x bfloat16 / float16 x storing dS or not
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 100, 8),
         "dq": (dq_asm, "11bwd_dq_mfma", 60, 4),
+        "dq_ds": (dq_asm, "9bwd_dq_ds", 60, 4),
         "fwd": (fwd_asm, "8fwd_mfma", 50, 8),            # ... x float32 / 16-bit output
     }[which]
     names = _kernels(asm, stem)

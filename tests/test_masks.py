@@ -16,8 +16,8 @@ from jaxmodules_amd import masks
 def assert_same_map(a, b):
     for f in ("map_b", "map_h", "pairs", "n_full", "n_partial"):
         assert getattr(a, f) == getattr(b, f), f
-    for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "row_bits", "col_bits", "q_order",
-              "kv_order"):
+    for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
+              "q_order", "kv_order"):
         assert np.array_equal(getattr(a, f), getattr(b, f)), f
 
 

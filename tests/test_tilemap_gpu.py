@@ -27,8 +27,8 @@ def assert_same_map(a: bmap.TileMap, b: bmap.TileMap):
     for f in ("B", "Hq", "Hkv", "Lq", "Lk", "map_b", "map_h", "nqt", "nkt", "pairs", "n_full",
               "n_partial"):
         assert getattr(a, f) == getattr(b, f), f
-    for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "row_bits", "col_bits", "q_order",
-              "kv_order"):
+    for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
+              "q_order", "kv_order"):
         x, y = getattr(a, f), getattr(b, f)
         assert x.shape == y.shape and x.dtype == y.dtype, (f, x.shape, y.shape, x.dtype, y.dtype)
         assert np.array_equal(x, y), f

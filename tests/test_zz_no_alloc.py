@@ -32,8 +32,9 @@ def _run(B, N, Hq, Hkv, d, dtype, seed, kw):
     ref = A.mattn_backward(q, k, v, o, lse, do, tm, scale, res)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     p = A._problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
-    assert lib.mattn_workspace_bytes(ctypes.byref(p)) <= _lib.SCRATCH_BYTES
     bm = A.device_blockmap(tm, q.device)
+    p.flags = A.bwd_flags(p, bm)  # the flags mattn_backward ran with (stored dS at D = 128)
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) <= _lib.SCRATCH_BYTES
     rc = lib.mattn_bwd_noalloc(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
                                v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
                                A._aligned(res), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
