@@ -459,9 +459,9 @@ void bwd_dq_ds(KArgs a) {
     else if (s + 1 < nsb) __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
     else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
-    // wave's operand reads ended with lgkmcnt(0)).  A bare barrier: the fence
-    // of __syncthreads would also wait for the fragment loads in flight.
-    __builtin_amdgcn_s_barrier();
+    // wave's operand reads ended with lgkmcnt(0)).  No __syncthreads: its
+    // fence would also wait for the fragment loads in flight.
+    barrier_lds();
     if (s + 1 < nsb) launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
     __builtin_amdgcn_sched_barrier(0);  // the fragment loads stay behind the K' loads
     if (s + PF < nsb) fetch(s + PF, fr[(SL + PF) % (PF + 1)]);

@@ -564,6 +564,12 @@ __device__ __forceinline__ float tile_absmax(const TileRows<D>& t) {
   return m;
 }
 
+// Workgroup barrier that waits for this wave's LDS operations (lgkmcnt(0))
+// but not for its vector memory operations, unlike __syncthreads, whose fence
+// also drains loads in flight (and stores); asm, so that the compiler moves no
+// memory operation across it.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // maximum over the 512 threads of a workgroup (red: 8 entries; one barrier
 // before the write guards a previous use of red)
 __device__ __forceinline__ f32x2 block_max2_512(f32x2 x, f32x2* red) {
