@@ -53,7 +53,6 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: one int64 device copy of this size (PMC calibration)
 # kernel symbol of each timed stage (for the rocprofv3 counter summaries)
-SYMBOL = {"fwd": "fwd_mfma", "bwd_dkdv": "bwd_dkdv_mfma", "bwd_dq": "bwd_dq_mfma"}
 EXTRA = ["cfg2", "cfg3", "cfg4", "cfg5", "target_gqa", "check_attn"]
 
 
@@ -71,7 +70,7 @@ def measured_traffic(config, stage):
     commit, val = None, None
     for line in open(path):
         m = pat.match(line.strip())
-        if m and m.group(1) == SYMBOL.get(stage):
+        if m and m.group(1) == stage:
             val = int(m.group(2))
         c = re.match(r"^commit:\s*(\w+)", line.strip())
         if c:
