@@ -356,7 +356,7 @@ def tilemap_build_times(repeats=5):
             dev = bmap.device_trace(plan, "cuda:0")
             ts.append(time.perf_counter() - t0)
         same = all(np.array_equal(getattr(host, f), getattr(dev, f))
-                   for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
+                   for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "kv_desc", "row_bits", "col_bits",
                              "q_order", "kv_order")) and host.pairs == dev.pairs
         out["configs"][name] = {"workload": desc, "host_s": round(th, 4),
                                 "device_s": round(float(np.median(ts)), 5),

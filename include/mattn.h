@@ -127,6 +127,16 @@ typedef struct mattn_blockmap {
   /* [nnz]: for each col_ent entry, the index in row_ent of the same tile (the
    * slot of its dS under MATTN_BWD_DS; may be NULL without that flag).     */
   const int32_t* col_row;
+  /* [n_kv_order][8], read by the dK/dV stage of 16-bit problems at D <= 128:
+   * per kv_order slot p with item = kv_order[p] = (b * Hkv + hk) * nkt + kt,
+   * { item, g, e, e_end, n_sub, qt, mask, row } where g is the first query
+   * head hk * G + g of the group whose column list (map row of (b, hk*G+g),
+   * key tile kt) is not empty, [e, e_end) that list, n_sub twice the total
+   * entry count over the group's heads, and (qt, mask) = col_ent[e],
+   * row = col_row[e] (0 without it); { -1, 0, ... } for idle slots and
+   * { item, 0, ... } for an empty column.  It lets each workgroup issue its
+   * first loads after a single read instead of a chain of dependent ones. */
+  const int32_t* kv_desc;
 } mattn_blockmap;
 
 /* Host-only check of a problem (and, when bm != NULL, of the map's sizes).

@@ -19,7 +19,7 @@ MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 MATTN_FWD_FOR_BWD = 1
 MATTN_BWD_DS = 2
 TILE_Q = TILE_K = 128
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 STATUS = {
     0: "MATTN_OK",
@@ -67,7 +67,7 @@ class MattnBlockmap(ctypes.Structure):
         ("row_bits", ctypes.c_void_p), ("col_bits", ctypes.c_void_p),
         ("q_order", ctypes.c_void_p), ("kv_order", ctypes.c_void_p),
         ("n_q_order", ctypes.c_int32), ("n_kv_order", ctypes.c_int32),
-        ("col_row", ctypes.c_void_p),
+        ("col_row", ctypes.c_void_p), ("kv_desc", ctypes.c_void_p),
     ]
 
 

@@ -206,6 +206,7 @@ def device_blockmap(tm: bmap.TileMap, device) -> _lib.MattnBlockmap:
     bufs = dict(
         row_ptr=up(tm.row_ptr), row_ent=up(tm.row_ent.reshape(-1)),
         col_ptr=up(tm.col_ptr), col_ent=up(tm.col_ent.reshape(-1)), col_row=up(tm.col_row),
+        kv_desc=up(tm.kv_desc.reshape(-1)),
         row_bits=up(tm.row_bits.view(np.int64).reshape(-1)),
         col_bits=up(tm.col_bits.view(np.int64).reshape(-1)),
         q_order=up(tm.q_order), kv_order=up(tm.kv_order))
@@ -217,7 +218,7 @@ def device_blockmap(tm: bmap.TileMap, device) -> _lib.MattnBlockmap:
         col_bits=bufs["col_bits"].data_ptr() if tm.n_masks else None,
         q_order=bufs["q_order"].data_ptr(), kv_order=bufs["kv_order"].data_ptr(),
         n_q_order=int(tm.q_order.size), n_kv_order=int(tm.kv_order.size),
-        col_row=bufs["col_row"].data_ptr() if tm.nnz else None)
+        col_row=bufs["col_row"].data_ptr() if tm.nnz else None, kv_desc=bufs["kv_desc"].data_ptr())
     tm.device[key] = (bufs, s)
     return s
 

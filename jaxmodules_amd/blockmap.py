@@ -164,6 +164,7 @@ class TileMap:
     col_ptr: np.ndarray     # int32 [map_b*map_h*nkt + 1]
     col_ent: np.ndarray     # int32 [nnz, 2] (query tile, mask id)
     col_row: np.ndarray     # int32 [nnz]: index in row_ent of each col_ent entry (same tile)
+    kv_desc: np.ndarray     # int32 [len(kv_order), 8]: per dK/dV launch slot (_kv_desc)
     row_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, q] bit j = key 64w + j allowed
     col_bits: np.ndarray    # uint64 [n_masks, 2, 128]: [m, w, k] bit j = query 64w + j allowed
     q_order: np.ndarray     # int32 launch order of (b, h, query tile) items
@@ -387,12 +388,45 @@ def _assemble(B, Hq, Hkv, N, L, map_b, map_h, r, kt, mid, rb, cb, pairs_map, n_f
     kvgroups = np.repeat(np.arange(B * Hkv), nkt)
     q_order = _lpt_xcd_order(qw, qgroups)
     kv_order = _lpt_xcd_order(kvw, kvgroups)
+    kv_desc = _kv_desc(kv_order, col_ptr, col_ent, col_row, B, Hq, Hkv, nkt, map_b, map_h)
 
     pairs = pairs_map * (B // map_b) * (Hq // map_h)
     return TileMap(B, Hq, Hkv, N, L, map_b, map_h, nqt, nkt,
-                   row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent, col_row,
+                   row_ptr.astype(np.int32), row_ent, col_ptr.astype(np.int32), col_ent, col_row, kv_desc,
                    np.ascontiguousarray(rb), np.ascontiguousarray(cb), q_order, kv_order, pairs,
                    n_full=n_full, n_partial=n_partial, trace_seconds=time.perf_counter() - t0)
+
+
+def _kv_desc(kv_order, col_ptr, col_ent, col_row, B, Hq, Hkv, nkt, map_b, map_h) -> np.ndarray:
+    """Per dK/dV launch slot, what the kernel's first loads need, in one row:
+    (item, first query head g of the GQA group with entries in the column,
+    that head's first column entry e and its end, sub-blocks of the whole
+    column (2 per entry over the group's heads), and entry e's query tile, mask
+    id and row-entry index); (-1, 0, ...) for idle slots and zeros after the
+    item for an empty column."""
+    G = Hq // Hkv
+    it = np.asarray(kv_order, np.int64)
+    valid = it >= 0
+    i = np.where(valid, it, 0)
+    kt, bhk = i % nkt, i // nkt
+    hk, b = bhk % Hkv, bhk // Hkv
+    cp = np.asarray(col_ptr, np.int64)
+    mcs = np.stack([((b % map_b) * map_h + (hk * G + g) % map_h) * nkt + kt for g in range(G)], axis=1)
+    cnt = cp[mcs + 1] - cp[mcs]                                   # [slots, G]
+    tot = 2 * cnt.sum(axis=1)
+    lg0 = np.argmax(cnt > 0, axis=1)                              # 0 when the column is empty
+    mc0 = mcs[np.arange(len(it)), lg0]
+    e0, lend0 = cp[mc0], cp[mc0 + 1]
+    has = valid & (tot > 0)
+    ent = np.asarray(col_ent, np.int64).reshape(-1, 2)
+    crow = np.asarray(col_row, np.int64)
+    ec = np.where(has, e0, 0)
+    qt0 = np.where(has, ent[ec, 0] if len(ent) else 0, 0)
+    m0 = np.where(has, ent[ec, 1] if len(ent) else 0, 0)
+    r0 = np.where(has, crow[ec] if len(crow) else 0, 0)
+    d = np.stack([np.where(valid, it, -1), lg0, e0, lend0, tot, qt0, m0, r0], axis=1)
+    d[~has, 1:] = 0
+    return np.ascontiguousarray(d.astype(np.int32))
 
 
 def device_trace(plan: Plan, device) -> TileMap:

@@ -70,7 +70,12 @@ void bwd_dkdv_mfma(KArgs a) {
   uint16_t* const Vs = KV + TILE * D;
   __shared__ f32x2 red[8];
 
-  const int item = a.kv_order[blockIdx.x];
+  // the slot's descriptor (item, first head / entry / end of its column list,
+  // sub-block count, first entry's query tile, mask and row index): the first
+  // loads need this one read, not a chain of dependent ones
+  const u32x4 dA = ((const u32x4*)a.kv_desc)[2 * blockIdx.x];
+  const u32x4 dB = ((const u32x4*)a.kv_desc)[2 * blockIdx.x + 1];
+  const int item = (int)dA[0];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
   const int kt = item % a.nkt;
   const int bh = item / a.nkt;
@@ -84,8 +89,8 @@ void bwd_dkdv_mfma(KArgs a) {
 
   // the forward's V' tile of the column, by direct loads into LDS, and this
   // thread's share of its K rows (4 threads per key row), converted to
-  // float16 once the tile's max |K| is known; both issued now so that the
-  // column-list reads below overlap their latency
+  // float16 once the tile's max |K| is known; both issued now so that their
+  // latency overlaps the first sub-block's
   const int col = item;  // (b * Hkv + hk) * nkt + kt
   {
     const uint16_t* vsrc = a.vh + (int64_t)col * TILE * D;
@@ -99,19 +104,11 @@ void bwd_dkdv_mfma(KArgs a) {
   tile_load<D>(tkr, (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)(kt * TILE) * a.ks[1] +
                         (int64_t)hk * a.ks[2], a.ks[1], a.Lk - kt * TILE);
 
-  // Flattened walk over (query head g of the group, column entry, half).
-  int tot = 0;
-  for (int g = 0; g < a.G; ++g) {
-    const int mc = map_row(a, b, hk * a.G + g, a.nkt, kt);
-    tot += 2 * (a.col_ptr[mc + 1] - a.col_ptr[mc]);
-  }
-  // cursor of the next sub-block to load
-  int lg = 0, le = 0, lend = 0, lhalf = 0;
-  {
-    const int mc = map_row(a, b, hk * a.G, a.nkt, kt);
-    le = a.col_ptr[mc];
-    lend = a.col_ptr[mc + 1];
-  }
+  // Flattened walk over (query head g of the group, column entry, half):
+  // tot sub-blocks; the cursor of the next sub-block to load starts at the
+  // descriptor's first entry
+  const int tot = (int)dB[0];
+  int lg = (int)dA[1], le = (int)dA[2], lend = (int)dA[3], lhalf = 0;
 
   // loop-invariant source byte offsets of this lane's load slots (Q' and dO'
   // rows are dense: row stride D in both copies)
@@ -175,10 +172,15 @@ void bwd_dkdv_mfma(KArgs a) {
   // 600 cycles when all eight waves ran it right after the barrier); launch()
   // issues the loads after the barrier, once the buffer they fill is free.
   int nq0 = 0;  // first query row of the prepared sub-block
-  auto prep = [&](auto bufc) {
+  // FIRST (the first sub-block): its entry comes from the descriptor, and the
+  // query tile's scales are read back after the K' tile (first_r, first_s),
+  // so that its loads are issued without waiting for any list read
+  float first_r = 1.f, first_s = 1.f;
+  auto prep = [&](auto bufc, auto firstc) {
     constexpr int BUF = decltype(bufc)::value;
+    constexpr bool FIRST = decltype(firstc)::value;
     if (lhalf == 0) {
-      while (le >= lend) {  // next query head of the group: another column list
+      while (!FIRST && le >= lend) {  // next query head of the group: another column list
         ++lg;
         const int mc = map_row(a, b, hk * a.G + lg, a.nkt, kt);
         le = a.col_ptr[mc];
@@ -195,7 +197,13 @@ void bwd_dkdv_mfma(KArgs a) {
         qsc_h = a.qsc + (b * a.Hq + h) * a.nqt;
         asc_h = a.asc + (b * a.Hq + h) * a.nqt;
       }
-      if constexpr (DS)
+      if constexpr (FIRST) {
+        cur_qt = (int)dB[1];
+        cur_mid = (int)dB[2];
+        cur_ri = (int)dB[3];
+        first_r = qsc_h[cur_qt];
+        first_s = asc_h[cur_qt];
+      } else if constexpr (DS)
         ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s, a.col_row, cur_ri);
       else
         ec.get(a.col_ent, le, lend, lane, cur_qt, cur_mid, qsc_h, asc_h, cur_r, cur_s);
@@ -385,7 +393,7 @@ void bwd_dkdv_mfma(KArgs a) {
   // the loop is unrolled by two so that every buffer index is static
   auto iter = [&](int s, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
-    if (s + 1 < tot) prep(std::integral_constant<int, 1 - BUF>{});
+    if (s + 1 < tot) prep(std::integral_constant<int, 1 - BUF>{}, std::false_type{});
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     const bool masked = (BUF ? mid1 : mid0) >= 0;
@@ -396,7 +404,7 @@ void bwd_dkdv_mfma(KArgs a) {
     step(bufc, masked);
   };
   if (tot > 0) {
-    prep(std::integral_constant<int, 0>{});
+    prep(std::integral_constant<int, 0>{}, std::true_type{});
     launch(std::integral_constant<int, 0>{});
     static_for<2 * NS>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
     dma_on = false;
@@ -421,6 +429,10 @@ void bwd_dkdv_mfma(KArgs a) {
     m2c = c2 * pow2_rcp(acc_r * ksc);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's V' loads have landed
     __syncthreads();                // the K' / V' tiles are complete
+  }
+  if (tot > 0) {  // the first sub-block's scales, loaded with its entry
+    cur_r = rh0 = first_r;
+    cur_s = sh0 = first_s;
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});

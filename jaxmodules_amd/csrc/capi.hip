@@ -19,7 +19,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 
@@ -129,6 +129,7 @@ KArgs make_args(const mattn_problem* p, const mattn_blockmap* bm) {
   a.col_bits = bm->col_bits;
   a.q_order = bm->q_order;
   a.kv_order = bm->kv_order;
+  a.kv_desc = bm->kv_desc;
   return a;
 }
 
@@ -251,6 +252,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
   if (!simt_path(p) && !residual) return MATTN_ERR_NULL;
   if (ds_path(p) && bm->nnz > 0 && !bm->col_row) return MATTN_ERR_NULL;
+  if (!simt_path(p) && stage == MATTN_BWD_DKDV && !bm->kv_desc) return MATTN_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
       !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u) ||
       ((uintptr_t)residual & 255u))

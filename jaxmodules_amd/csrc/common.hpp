@@ -93,6 +93,7 @@ struct KArgs {
   uint16_t* ds;
   const int* col_row;
   int ds_nnz;
+  const int* kv_desc;  // per dK/dV launch slot: { item, g, e, e_end, n_sub, qt, mask, row }
 };
 
 // dS storage slot base of (b, h): the map's entries are shared by the (b, h)

@@ -64,6 +64,29 @@ def check_consistency(tm, plan):
     assert np.array_equal(r_of % tm.nqt, tm.col_ent[:, 0])                # same query tile
     assert np.array_equal(tm.row_ent[tm.col_row, 0], cols % tm.nkt)       # same key tile
     assert np.array_equal(tm.row_ent[tm.col_row, 1], tm.col_ent[:, 1])   # same mask
+    # kv_desc: per launch slot, the column's first entry, recomputed by plain loops
+    G = plan.Hq // plan.Hkv
+    assert tm.kv_desc.dtype == np.int32 and tm.kv_desc.shape == (len(tm.kv_order), 8)
+    for slot, item in enumerate(tm.kv_order):
+        d = tm.kv_desc[slot]
+        if item < 0:
+            assert d[0] == -1 and not d[1:].any()
+            continue
+        kt, bhk = item % tm.nkt, item // tm.nkt
+        hk, b = bhk % plan.Hkv, bhk // plan.Hkv
+        ranges = []
+        for g in range(G):
+            mc = ((b % tm.map_b) * tm.map_h + (hk * G + g) % tm.map_h) * tm.nkt + kt
+            ranges.append((g, tm.col_ptr[mc], tm.col_ptr[mc + 1]))
+        tot = 2 * sum(e1 - e0 for _, e0, e1 in ranges)
+        assert d[0] == item and d[4] == tot
+        nonempty = [r for r in ranges if r[2] > r[1]]
+        if not nonempty:
+            assert not d[1:].any()
+            continue
+        g, e0, e1 = nonempty[0]
+        assert tuple(d[1:4]) == (g, e0, e1)
+        assert tuple(d[5:8]) == (tm.col_ent[e0, 0], tm.col_ent[e0, 1], tm.col_row[e0])
     # masks are distinct and the column bits are the transposed row bits
     seen = set()
     for m in range(tm.n_masks):

@@ -195,6 +195,17 @@ def test_bwd_workspace_bytes_with_stored_ds(lib):
                                None) == -1
 
 
+def test_dkdv_stage_needs_the_launch_descriptors(lib):
+    """The MFMA dK/dV stage reads kv_desc (one row per launch slot); without it
+    the call returns MATTN_ERR_NULL before any launch.  The float32 (SIMT)
+    path does not read it."""
+    p = _problem()
+    bm = _lib.MattnBlockmap(map_b=1, map_h=1, nqt=3, nkt=3, n_masks=0, nnz=0, row_ptr=8, col_ptr=8,
+                            q_order=8, kv_order=8, n_q_order=2 * 8 * 3, n_kv_order=2 * 2 * 3, kv_desc=None)
+    ptrs = [8, 8, 8, 8, 8, 8, 256, 256, 8, 8, 8]
+    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), _lib.BWD_DKDV, *ptrs, None) == -1
+
+
 def test_heads_major_long_sequences_validate(lib):
     """Heads-major views (flex_attention's layout) with Hq * Lq * D >= 2^31: the
     float16 dO' and Q' copies the dK/dV kernel reads are head-major, one buffer

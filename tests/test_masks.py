@@ -17,7 +17,7 @@ def assert_same_map(a, b):
     for f in ("map_b", "map_h", "pairs", "n_full", "n_partial"):
         assert getattr(a, f) == getattr(b, f), f
     for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
-              "q_order", "kv_order"):
+              "q_order", "kv_order", "kv_desc"):
         assert np.array_equal(getattr(a, f), getattr(b, f)), f
 
 

@@ -28,7 +28,7 @@ def assert_same_map(a: bmap.TileMap, b: bmap.TileMap):
               "n_partial"):
         assert getattr(a, f) == getattr(b, f), f
     for f in ("row_ptr", "row_ent", "col_ptr", "col_ent", "col_row", "row_bits", "col_bits",
-              "q_order", "kv_order"):
+              "q_order", "kv_order", "kv_desc"):
         x, y = getattr(a, f), getattr(b, f)
         assert x.shape == y.shape and x.dtype == y.dtype, (f, x.shape, y.shape, x.dtype, y.dtype)
         assert np.array_equal(x, y), f
