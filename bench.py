@@ -396,6 +396,8 @@ def main():
                     help="after the timed region, copy 1 GiB once (calibrates rocprofv3 byte counters)")
     ap.add_argument("--recompute-dq", action="store_true",
                     help="run dQ by recomputing S and dP (no stored dS) everywhere")
+    ap.add_argument("--stored-ds", action="store_true",
+                    help="run dQ from the stored dS wherever the kernels allow it (head dim <= 128)")
     ap.add_argument("--tilemap", action="store_true",
                     help="instead: time the tile-map build of configs 3-5, host tracer vs GPU classifier")
     args = ap.parse_args()
@@ -409,10 +411,10 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    if args.recompute_dq:
+    if args.recompute_dq or args.stored_ds:
         from jaxmodules_amd import attention as A
 
-        A.STORE_DS = False
+        A.STORE_DS = bool(args.stored_ds)
     if args.tilemap:
         print(json.dumps(tilemap_build_times()), flush=True)
         return

@@ -453,11 +453,13 @@ void bwd_dq_ds(KArgs a) {
     const float sks = nks;
     int kt1 = 0;
     if (s + 1 < nsb) entry(s + 1, kt1, nks);
-    // this wave's K' loads of s landed; younger fragment loads may be in flight
-    static_assert(PF == 3, "the waits below count PF - 1 = 2 younger sub-blocks");
-    if (s + 2 < nsb) __builtin_amdgcn_s_waitcnt(vmcnt_only(8));
-    else if (s + 1 < nsb) __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    // this wave's K' loads of s landed; the fragment loads of the n = min(PF -
+    // 1, nsb - 1 - s) later sub-blocks, issued after them, may stay in flight
+    const int n = min(PF - 1, nsb - 1 - s);
+    static_for<PF>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if (n == j) __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * j));
+    });
     // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
     // wave's operand reads ended with lgkmcnt(0)).  No __syncthreads: its
     // fence would also wait for the fragment loads in flight.
@@ -467,12 +469,13 @@ void bwd_dq_ds(KArgs a) {
     if (s + PF < nsb) fetch(s + PF, fr[(SL + PF) % (PF + 1)]);
     step(bufc, fr[SL], sks);
   };
-  // unrolled by 4 (2 K' buffers, 4 fragment slots): every index static
-  for (int s = 0; s < nsb; s += 4) {
-    iter(s, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
-    if (s + 2 < nsb) iter(s + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 2>{});
-    if (s + 3 < nsb) iter(s + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 3>{});
+  // unrolled by UR = lcm(2, PF + 1) (2 K' buffers, PF + 1 fragment slots): every index static
+  constexpr int UR = (PF + 1) % 2 == 0 ? PF + 1 : 2 * (PF + 1);
+  for (int s = 0; s < nsb; s += UR) {
+    static_for<UR>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      if (s + u < nsb) iter(s + u, std::integral_constant<int, u % 2>{}, std::integral_constant<int, u % (PF + 1)>{});
+    });
   }
 
   // dQ through LDS (a quarter of the K' buffers per wave, free once every wave is done)
