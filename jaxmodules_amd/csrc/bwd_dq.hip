@@ -211,7 +211,7 @@ void bwd_dq_mfma(KArgs a) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (!mask_bit(w32, r)) st[r] = 0.f;
+          st[r] = mask_zero(st[r], mask_ones(w32, r));
       }
       u32x4 pk[2];
 #pragma unroll

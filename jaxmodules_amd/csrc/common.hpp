@@ -344,6 +344,22 @@ __device__ __forceinline__ void tr_write(uint16_t* T, const u32x4* x, int r0, in
 __device__ __forceinline__ bool mask_bit(uint32_t w32, int r) {
   return (w32 >> (8 * (r >> 2) + (r & 3))) & 1u;
 }
+// the same bit as all ones (set) or zero (clear): one v_bfe_i32, after which
+// masking an element is one v_and_b32 (to 0) or v_bfi_b32 (to -inf) instead
+// of a compare and a select
+__device__ __forceinline__ uint32_t mask_ones(uint32_t w32, int r) {
+  uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)w32, 8 * (r >> 2) + (r & 3), 1);
+  // opaque to the compiler, which would otherwise turn the AND back into a
+  // compare and a select (and an s_nop for the VCC hazard between them)
+  asm("" : "+v"(m));
+  return m;
+}
+__device__ __forceinline__ float mask_zero(float x, uint32_t m) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & m);
+}
+__device__ __forceinline__ float mask_neg_inf(float x, uint32_t m) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x) & m) | (~m & 0xff800000u));
+}
 
 // max / sum of x over lanes l and l ^ 32 (v_permlane32_swap: no LDS access, so
 // no wait on outstanding global->LDS loads)

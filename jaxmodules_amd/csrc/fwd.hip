@@ -239,7 +239,7 @@ void fwd_mfma(KArgs a) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (!mask_bit(w32, r)) st[t][r] = NEG_INF;
+          st[t][r] = mask_neg_inf(st[t][r], mask_ones(w32, r));
       }
     }
     float mx = NEG_INF;
