@@ -72,9 +72,21 @@ void bwd_pre(KArgs a) {
   constexpr int PER = D / 4;
   constexpr int CS = O_F32 ? 4 : 8;  // values per 16-byte input chunk
   __shared__ f32x2 red[8];
-  const int tile = blockIdx.x;  // (b * Hq + h) * nqt + qt
-  const int qt = tile % a.nqt, bh = tile / a.nqt;
-  const int h = bh % a.Hq, b = bh / a.Hq;
+  // Launch position -> (b, h, qt).  When a row of O holds all heads ([B, L, H,
+  // D]), the head runs fastest, so that the workgroups running together read
+  // whole rows of O and dO between them; otherwise the query tile does.
+  int b, h, qt;
+  if (a.os[2] < a.os[1]) {
+    h = blockIdx.x % a.Hq;
+    qt = (blockIdx.x / a.Hq) % a.nqt;
+    b = blockIdx.x / (a.Hq * a.nqt);
+  } else {
+    qt = blockIdx.x % a.nqt;
+    h = (blockIdx.x / a.nqt) % a.Hq;
+    b = blockIdx.x / (a.nqt * a.Hq);
+  }
+  const int bh = b * a.Hq + h;
+  const int tile = bh * a.nqt + qt;  // (b * Hq + h) * nqt + qt
   const int tid = threadIdx.x, part = tid & 3;
   const int q = qt * TILE + (tid >> 2);
   const bool live = q < a.Lq;

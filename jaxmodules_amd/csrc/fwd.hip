@@ -37,8 +37,20 @@ template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void cvt_v(KArgs a) {
   __shared__ f32x2 red[8];
-  const int kt = blockIdx.x % a.nkt, bh = blockIdx.x / a.nkt;
-  const int hk = bh % a.Hkv, b = bh / a.Hkv;
+  // launch position -> (b, kv head, key tile), the head fastest when a row of V
+  // holds all kv heads, so that the workgroups running together read whole rows
+  int b, hk, kt;
+  if (a.vs[2] < a.vs[1]) {
+    hk = blockIdx.x % a.Hkv;
+    kt = (blockIdx.x / a.Hkv) % a.nkt;
+    b = blockIdx.x / (a.Hkv * a.nkt);
+  } else {
+    kt = blockIdx.x % a.nkt;
+    hk = (blockIdx.x / a.nkt) % a.Hkv;
+    b = blockIdx.x / (a.nkt * a.Hkv);
+  }
+  const int bh = b * a.Hkv + hk;
+  const int tile = bh * a.nkt + kt;
   const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
   TileRows<D> t;
   tile_load<D>(t, (const uint16_t*)a.v + (int64_t)b * a.vs[0] + (int64_t)(kt * TILE) * a.vs[1] +
@@ -50,8 +62,8 @@ void cvt_v(KArgs a) {
   for (int j = 0; j < TileRows<D>::CPL; ++j)
     *(u32x4*)(dst + 8 * TileRows<D>::chunk(part, j)) = chunk_f16<Tag>(t.x[j], s);
   if (threadIdx.x == 0) {
-    a.vsc[blockIdx.x] = s;
-    a.vmax[blockIdx.x] = m[0];
+    a.vsc[tile] = s;
+    a.vmax[tile] = m[0];
   }
 }
 
