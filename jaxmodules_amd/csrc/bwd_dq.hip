@@ -432,10 +432,13 @@ void bwd_dq_ds(KArgs a) {
   };
 
   // Sub-block s: its K' rows were loaded (into buffer s % 2) one iteration
-  // ahead, its fragments PF iterations ahead into ring slot s % (PF + 1).  The
-  // wait before the barrier covers this wave's K' loads of s; the fragment
-  // loads issued after them (those of s + 1 .. s + PF - 1 that exist: 4 loads
-  // each) may stay outstanding, since vector memory loads return in order.
+  // ahead, its fragments PF iterations ahead into ring slot s % (PF + 1).
+  // Vector memory loads retire in issue order (the K' DMA included), so the
+  // wait before the barrier may leave outstanding only what was issued after
+  // the later of this wave's K' loads of s and fragment loads of s.  Issue
+  // order: K'(0), F(0) .. F(PF - 1), then per iteration s: K'(s + 1), F(s + PF).
+  // At s = 0 that is F(1) .. F(PF - 1) (those that exist); at s >= 1, K'(s)
+  // (iteration s - 1) comes after F(s), and only F(s + PF - 1) follows it.
   u32x4 fr[PF + 1][4];
   int nkt_ = 0;
   float nks = 1.f;  // key tile and K' scale of the prepared sub-block
@@ -453,9 +456,9 @@ void bwd_dq_ds(KArgs a) {
     const float sks = nks;
     int kt1 = 0;
     if (s + 1 < nsb) entry(s + 1, kt1, nks);
-    // this wave's K' loads of s landed; the fragment loads of the n = min(PF -
-    // 1, nsb - 1 - s) later sub-blocks, issued after them, may stay in flight
-    const int n = min(PF - 1, nsb - 1 - s);
+    // this wave's K' and fragment loads of s landed; the n sub-blocks of
+    // fragment loads issued after them (4 loads each) may stay in flight
+    const int n = s == 0 ? min(PF, nsb) - 1 : (s + PF - 1 < nsb ? 1 : 0);
     static_for<PF>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       if (n == j) __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * j));
