@@ -368,11 +368,16 @@ void bwd_dq_ds(KArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) lds_load16(kp + kld[i], (BUF ? K1 : K0) + wofs + i * BLK);
   };
-  // fragments of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2)
+  // fragments of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2);
+  // past the row's last sub-block the same four loads read one 16-byte line
+  // at the start of the dS area for every lane (a cache hit, results unused),
+  // so that the number of loads issued per iteration does not depend on s
   auto fetch = [&](int s, u32x4 (&f)[4]) {
-    const uint16_t* p = frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512;
+    const bool real = s < nsb;
+    const uint16_t* p = real ? frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512 : a.ds;
+    const int step = real ? 512 : 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) f[k] = __builtin_nontemporal_load((const u32x4*)(p + k * 512));
+    for (int k = 0; k < 4; ++k) f[k] = __builtin_nontemporal_load((const u32x4*)(p + k * step));
   };
 
   f32x16 acc[NMD];
@@ -437,8 +442,11 @@ void bwd_dq_ds(KArgs a) {
   // wait before the barrier may leave outstanding only what was issued after
   // the later of this wave's K' loads of s and fragment loads of s.  Issue
   // order: K'(0), F(0) .. F(PF - 1), then per iteration s: K'(s + 1), F(s + PF).
-  // At s = 0 that is F(1) .. F(PF - 1) (those that exist); at s >= 1, K'(s)
-  // (iteration s - 1) comes after F(s), and only F(s + PF - 1) follows it.
+  // At s >= 1, K'(s) (iteration s - 1) comes after F(s), and only F(s + PF -
+  // 1) follows it: 4 loads, issued (from a dummy address) also where that
+  // sub-block does not exist, so the wait is the same vmcnt(4) on every path
+  // into the loop's barrier (tests/lds_waits.py checks it on the compiled
+  // code).  At s = 0 it also waits for F(1) .. F(PF - 2), one sub-block early.
   u32x4 fr[PF + 1][4];
   int nkt_ = 0;
   float nks = 1.f;  // key tile and K' scale of the prepared sub-block
@@ -448,7 +456,7 @@ void bwd_dq_ds(KArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     static_for<PF>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
-      if (p < nsb) fetch(p, fr[p]);
+      fetch(p, fr[p]);
     });
   }
   auto iter = [&](int s, auto bufc, auto slc) {
@@ -456,20 +464,16 @@ void bwd_dq_ds(KArgs a) {
     const float sks = nks;
     int kt1 = 0;
     if (s + 1 < nsb) entry(s + 1, kt1, nks);
-    // this wave's K' and fragment loads of s landed; the n sub-blocks of
-    // fragment loads issued after them (4 loads each) may stay in flight
-    const int n = s == 0 ? min(PF, nsb) - 1 : (s + PF - 1 < nsb ? 1 : 0);
-    static_for<PF>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      if (n == j) __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * j));
-    });
+    // this wave's K' and fragment loads of s landed; the fragment loads of
+    // s + PF - 1 (4 loads), issued after them, may stay in flight
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
     // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
     // wave's operand reads ended with lgkmcnt(0)).  No __syncthreads: its
     // fence would also wait for the fragment loads in flight.
     barrier_lds();
     if (s + 1 < nsb) launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
     __builtin_amdgcn_sched_barrier(0);  // the fragment loads stay behind the K' loads
-    if (s + PF < nsb) fetch(s + PF, fr[(SL + PF) % (PF + 1)]);
+    fetch(s + PF, fr[(SL + PF) % (PF + 1)]);
     step(bufc, fr[SL], sks);
   };
   // unrolled by UR = lcm(2, PF + 1) (2 K' buffers, PF + 1 fragment slots): every index static

@@ -16,6 +16,15 @@ own reads pending at a back edge are then not tracked into the loop, which
 hides no newer read (older operations retire first).
 An ``lgkmcnt(N > 0)`` wait while a scalar-memory load is outstanding (those
 complete out of order) is reported as well.
+
+``check_dma`` checks the other counter: every global->LDS load (the ``lds``
+forms of ``global_load`` / ``buffer_load``) must have retired at the next
+``s_barrier``, which is where the double-buffered kernels hand a filled LDS
+buffer to the other waves.  Vector memory operations (loads and, on gfx9,
+stores) retire in issue order, so ``vmcnt(N)`` retires all but the N most
+recent.  Loads legitimately stay in flight across a loop's back edge (the
+prefetch of the next iteration), so there the walk is repeated with the back
+edges' states added at the loop header until no new state reaches it.
 """
 from __future__ import annotations
 
@@ -127,3 +136,78 @@ def check(lines: list) -> tuple:
     for label in fwd:
         problems.append(f"branch to {label}, which is not in the walked code")
     return reads, sorted(set(problems), key=problems.index)
+
+
+_VMEM = ("global_load", "global_store", "global_atomic", "buffer_load", "buffer_store", "buffer_atomic",
+         "flat_", "scratch_")
+
+
+def _dma_walk(lines: list, loop_in: dict) -> tuple:
+    """One layout-order walk for check_dma: (problems, back-edge states by label)."""
+    problems = []
+    states = [()]
+    fwd, seen, back = {}, set(), {}
+    reachable = True
+    for n, raw in enumerate(lines):
+        t = raw.split(";")[0].strip()
+        if not t:
+            continue
+        if t.endswith(":"):
+            label = t[:-1]
+            incoming = fwd.pop(label, []) + list(loop_in.get(label, ()))
+            if reachable:
+                incoming += states
+            states = list(dict.fromkeys(incoming)) or [()]
+            seen.add(label)
+            reachable = True
+            continue
+        if t.startswith("."):
+            continue
+        op = t.split()[0]
+        if op.startswith(("s_branch", "s_cbranch")):
+            target = t[len(op):].strip().split()[0] if t[len(op):].strip() else ""
+            if target in seen:
+                back.setdefault(target, set()).update(states)
+            else:
+                fwd.setdefault(target, []).extend(states)
+            if op.startswith("s_branch"):
+                reachable = False
+            continue
+        if op in ("s_endpgm", "s_setpc_b64"):
+            reachable = False
+            continue
+        if op == "s_waitcnt":
+            m = re.search(r"vmcnt\((\d+)\)", t)
+            if m or re.fullmatch(r"s_waitcnt\s+0", t):
+                lim = int(m.group(1)) if m else 0
+                states = [st[max(0, len(st) - lim):] if lim else () for st in states]
+            continue
+        if op == "s_barrier":
+            for st in states:
+                for kind, ln in st:
+                    if kind == "dma":
+                        problems.append(f"line {n}: s_barrier with the global->LDS load of line {ln} outstanding")
+            continue
+        if op.startswith(_VMEM):
+            kind = "dma" if re.search(r"\blds\b", t[len(op):]) or op.endswith("_lds_dwordx4") else "vmem"
+            states = [st + ((kind, n),) for st in states]
+    for label in fwd:
+        problems.append(f"branch to {label}, which is not in the walked code")
+    return problems, back
+
+
+def check_dma(lines: list, max_rounds: int = 20) -> tuple:
+    """(number of global->LDS loads seen, list of problem descriptions)."""
+    dma = sum(1 for l in lines if re.search(r"^\s*(global_load_lds_\w+|buffer_load_\w+.*\blds\b)", l.split(";")[0]))
+    loop_in: dict = {}
+    for _ in range(max_rounds):
+        problems, back = _dma_walk(lines, loop_in)
+        grown = False
+        for label, sts in back.items():
+            cur = loop_in.setdefault(label, set())
+            if not sts <= cur:
+                cur |= sts
+                grown = True
+        if not grown:
+            return dma, sorted(set(problems), key=problems.index)
+    return dma, ["the loop states did not settle"]

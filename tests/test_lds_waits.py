@@ -1,5 +1,7 @@
-"""The hand-counted LDS waits of the forward, dK/dV and dQ kernels, checked on
-their compiled gfx950 assembly (no GPU needed: hipcc cross-compiles here)."""
+"""The hand-counted LDS waits of the forward, dK/dV and dQ kernels, and the
+vmcnt waits that must retire their global->LDS loads before each barrier,
+checked on their compiled gfx950 assembly (no GPU needed: hipcc
+cross-compiles here)."""
 import os
 import re
 import shutil
@@ -90,3 +92,56 @@ def test_checker_follows_forward_branches():
     assert any("touches the registers" in p for p in problems)
     fixed = _BRANCHY.replace(".LBB0_2:\n", ".LBB0_2:\n\ts_waitcnt lgkmcnt(0)\n")
     assert lds_waits.check(fixed.split("\n"))[1] == []
+
+
+@pytest.mark.parametrize("which", ["dkdv", "dq", "dq_ds", "fwd"])
+def test_every_instantiation_retires_its_lds_dma_before_each_barrier(which, dkdv_asm, dq_asm, fwd_asm):
+    asm, stem, count = {
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 8),
+        "dq": (dq_asm, "11bwd_dq_mfma", 4),
+        "dq_ds": (dq_asm, "9bwd_dq_ds", 4),
+        "fwd": (fwd_asm, "8fwd_mfma", 8),
+    }[which]
+    names = _kernels(asm, stem)
+    assert len(names) == count, names
+    for name in names:
+        dma, problems = lds_waits.check_dma(lds_waits.kernel_body(asm, name))
+        assert dma >= 10, (name, dma)
+        assert not problems, (name, problems[:5])
+
+
+def test_dma_checker_flags_the_dq_ds_wait_that_skipped_the_k_tile(dq_asm):
+    """vmcnt(8) ahead of dQ's barrier (two sub-blocks of fragment loads left in
+    flight, as an earlier count had it) leaves the K' DMA of the sub-block
+    outstanding: reported."""
+    name = _kernels(dq_asm, "9bwd_dq_ds")[0]
+    body = lds_waits.kernel_body(dq_asm, name)
+    waits = [i for i, l in enumerate(body) if l.strip() == "s_waitcnt vmcnt(4)"]
+    assert waits
+    planted = [("\ts_waitcnt vmcnt(8)" if i in waits else l) for i, l in enumerate(body)]
+    _, problems = lds_waits.check_dma(planted)
+    assert any("global->LDS load" in p for p in problems)
+
+
+_LOOP = """\
+\tglobal_load_lds_dwordx4 v1, s[0:1]
+\tglobal_load_dwordx4 v[4:7], v[2:3], off
+\tglobal_load_dwordx4 v[8:11], v[2:3], off
+.LBB0_1:
+\ts_waitcnt vmcnt(2)
+\ts_barrier
+\tglobal_load_lds_dwordx4 v1, s[0:1]
+\tglobal_load_dwordx4 v[4:7], v[2:3], off
+\ts_cbranch_scc1 .LBB0_1
+\ts_waitcnt vmcnt(0)
+\ts_endpgm
+"""
+
+
+def test_dma_checker_carries_loads_across_the_back_edge():
+    """On entry two loads follow the DMA, so vmcnt(2) retires it; around the
+    loop only one does, and the same wait leaves the loop's DMA outstanding."""
+    _, problems = lds_waits.check_dma(_LOOP.split("\n"))
+    assert problems and all("load of line 6 outstanding" in p for p in problems), problems
+    fixed = _LOOP.replace("vmcnt(2)", "vmcnt(1)", 1)
+    assert lds_waits.check_dma(fixed.split("\n"))[1] == []
