@@ -185,6 +185,9 @@ void bwd_dq_mfma(KArgs a) {
     // its two dQ k-steps before the next half starts (halves the live state).
     static_for<2>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
+      // a half whose block (the wave's 32 queries x 32 keys) is entirely
+      // masked adds nothing to dQ (dS = 0): skipped
+      if (masked && !__any((uint32_t)(mw >> (32 * t)) != 0u)) return;
       f32x16 st = f32x16{}, dp = cvec;
       u32x4 ka[PS + 1], va[PS + 1];
       auto rd = [&](auto kc) {

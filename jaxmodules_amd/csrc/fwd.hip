@@ -246,6 +246,12 @@ void fwd_mfma(KArgs a) {
     }
     if (masked) {
       const uint64_t mw = (BUF ? M1 : M0)[qloc];
+      // a wave whose 32 rows allow no key of the sub-block (all mask words
+      // zero) stops here: masked (-inf) elements would leave its softmax
+      // state as it is (a pending V' rescale, a power of two, then lands at
+      // the next sub-block it computes).  Its S chain ran, as it carries the
+      // wave's share of the next sub-block's loads.
+      if (!__any(mw != 0)) return;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
