@@ -149,6 +149,78 @@ _CACHE: "OrderedDict[tuple, bmap.TileMap]" = OrderedDict()
 _CACHE_SIZE = 32
 
 
+class _Unfrozen(Exception):
+    pass
+
+
+def _freeze(v, depth=0):
+    """A hashable value standing for what ``v`` contributes to a mask function's
+    result: plain values as they are, containers and numpy arrays (and small
+    host tensors) by content, modules by name, functions by their own key;
+    anything else raises _Unfrozen."""
+    import types
+
+    if depth > 8:
+        raise _Unfrozen
+    if v is None or isinstance(v, (bool, int, float, complex, str, bytes)):
+        return (type(v).__name__, v)
+    if isinstance(v, np.generic):
+        return ("np", v.dtype.str, v.item())
+    if isinstance(v, np.ndarray):
+        import hashlib
+        return ("nd", v.dtype.str, v.shape, hashlib.sha1(np.ascontiguousarray(v).tobytes()).hexdigest())
+    if isinstance(v, torch.Tensor):
+        if v.is_cuda or v.numel() > (1 << 24):
+            raise _Unfrozen
+        return _freeze(v.detach().numpy(), depth + 1)
+    if isinstance(v, (tuple, list, frozenset, set)):
+        items = sorted(v, key=repr) if isinstance(v, (set, frozenset)) else v
+        return (type(v).__name__, tuple(_freeze(x, depth + 1) for x in items))
+    if isinstance(v, dict):
+        return ("dict", tuple(sorted(((repr(k), _freeze(x, depth + 1)) for k, x in v.items()))))
+    if isinstance(v, types.ModuleType):
+        return ("module", v.__name__)
+    if isinstance(v, types.FunctionType):
+        return ("fn", _fn_content(v, depth + 1))
+    if isinstance(v, (types.BuiltinFunctionType, np.ufunc)):
+        return ("builtin", getattr(v, "__module__", None), v.__name__)
+    raise _Unfrozen
+
+
+def _fn_content(fn, depth=0):
+    """What a plain Python function computes, as a hashable value: its code,
+    defaults, closure contents and the values of the globals its code names
+    (read now, so a changed value gives another key)."""
+    code = fn.__code__
+    names, stack = set(), [code]
+    while stack:  # the names of nested code objects (inner lambdas) too
+        c = stack.pop()
+        names.update(c.co_names)
+        stack.extend(x for x in c.co_consts if hasattr(x, "co_names"))
+    g = fn.__globals__
+    try:
+        cells = tuple(_freeze(c.cell_contents, depth + 1) for c in (fn.__closure__ or ()))
+    except ValueError:  # an empty closure cell
+        raise _Unfrozen
+    return (code, _freeze(fn.__defaults__, depth + 1), _freeze(fn.__kwdefaults__, depth + 1), cells,
+            tuple((n, _freeze(g[n], depth + 1)) for n in sorted(names) if n in g))
+
+
+def _mask_key(mask_fn):
+    """Cache key of a mask function: by content when every value it reads is
+    one _freeze can describe -- so a new but identical lambda per call (the
+    usual way to pass a mask) finds the map already traced -- and the function
+    object itself otherwise."""
+    import types
+
+    if isinstance(mask_fn, types.FunctionType):
+        try:
+            return ("content", _fn_content(mask_fn))
+        except (_Unfrozen, TypeError, RecursionError):
+            pass
+    return mask_fn
+
+
 def clear_cache():
     _CACHE.clear()
     _BM_CACHE.clear()
@@ -165,7 +237,7 @@ def trace_call(q_shape, k_shape, v_shape, *, is_causal=False, mask_fn=None, bloc
     Both give the same map."""
     plan = bmap.make_plan(q_shape, k_shape, v_shape, is_causal=is_causal, mask_fn=mask_fn,
                           block_size=block_size, window_size=window_size)
-    key = (bool(is_causal), mask_fn, block_size,
+    key = (bool(is_causal), _mask_key(mask_fn), block_size,
            None if window_size is None else tuple(window_size),
            plan.B, plan.N, plan.L, plan.Hq, plan.Hkv)
     tm = _CACHE.get(key)

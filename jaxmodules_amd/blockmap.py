@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from dataclasses import dataclass, field
 from typing import Callable, Optional, Tuple
 
@@ -285,43 +286,65 @@ def trace(plan: Plan) -> TileMap:
                         plan.Hkv, plan.N, plan.L, map_b, map_h)
 
 
+def _classify_strip(strip, qt, map_b, map_h, nkt):
+    """One query strip's present tiles: (pairs, map row / batch / head indices,
+    key tiles, full flags, packed row and column bits of the partial tiles)."""
+    m = strip(qt * TILE)
+    assert m.shape == (map_b, map_h, TILE, nkt * TILE), m.shape
+    pairs = int(np.count_nonzero(m))
+    t = m.reshape(map_b, map_h, TILE, nkt, TILE)
+    anyb = t.any(axis=(2, 4))
+    allb = t.all(axis=(2, 4))
+    mb, mh, kt = np.nonzero(anyb)
+    full = allb[mb, mh, kt]
+    part = np.nonzero(~full)[0]
+    rb = cb = None
+    if len(part):
+        tiles = t[mb[part], mh[part], :, kt[part], :]          # [P, 128 q, 128 k]
+        rb = np.ascontiguousarray(np.packbits(tiles, axis=2, bitorder="little")).view(np.uint64)
+        cb = np.ascontiguousarray(np.packbits(tiles.transpose(0, 2, 1), axis=2,
+                                              bitorder="little")).view(np.uint64)
+        # [P, 128 rows, 2 words] -> [P, 2 words, 128 rows]: a wave's 32 rows of one
+        # 64-wide half are then one contiguous 256-byte block
+        rb = np.ascontiguousarray(rb.transpose(0, 2, 1))
+        cb = np.ascontiguousarray(cb.transpose(0, 2, 1))
+    return pairs, mb, mh, kt, full, part, rb, cb
+
+
+# host threads for trace_strips (numpy releases the GIL in the array work)
+TRACE_THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
 def trace_strips(strip, B, Hq, Hkv, N, L, map_b, map_h) -> TileMap:
     """TileMap of the mask whose query rows [q0, q0+128) ``strip(q0)`` returns as
     bool [map_b, map_h, 128, nkt*128] (False beyond N and L); map_b / map_h are
-    1 where the mask is the same for every batch / head."""
+    1 where the mask is the same for every batch / head.  The strips are
+    classified on TRACE_THREADS threads and merged in strip order, so the map
+    (mask numbering included) does not depend on the thread count."""
     import time
+    from concurrent.futures import ThreadPoolExecutor
 
     t0 = time.perf_counter()
     nqt, nkt = -(-N // TILE), -(-L // TILE)
-    nmap = map_b * map_h
 
     masks: dict = {}
     row_bits, col_bits = [], []
     ent_row, ent_kt, ent_mid = [], [], []   # map row index, key tile, mask id
     pairs_map = 0
     n_full = n_partial = 0
-    for qt in range(nqt):
-        m = strip(qt * TILE)
-        assert m.shape == (map_b, map_h, TILE, nkt * TILE), m.shape
-        pairs_map += int(np.count_nonzero(m))
-        t = m.reshape(map_b, map_h, TILE, nkt, TILE)
-        anyb = t.any(axis=(2, 4))
-        allb = t.all(axis=(2, 4))
-        mb, mh, kt = np.nonzero(anyb)
-        if len(kt) == 0:
-            continue
-        full = allb[mb, mh, kt]
-        mids = np.full(len(kt), -1, np.int64)
-        part = np.nonzero(~full)[0]
-        if len(part):
-            tiles = t[mb[part], mh[part], :, kt[part], :]          # [P, 128 q, 128 k]
-            rb = np.ascontiguousarray(np.packbits(tiles, axis=2, bitorder="little")).view(np.uint64)
-            cb = np.ascontiguousarray(np.packbits(tiles.transpose(0, 2, 1), axis=2,
-                                                  bitorder="little")).view(np.uint64)
-            # [P, 128 rows, 2 words] -> [P, 2 words, 128 rows]: a wave's 32 rows of one
-            # 64-wide half are then one contiguous 256-byte block
-            rb = np.ascontiguousarray(rb.transpose(0, 2, 1))
-            cb = np.ascontiguousarray(cb.transpose(0, 2, 1))
+    work = lambda qt: _classify_strip(strip, qt, map_b, map_h, nkt)
+    threads = min(TRACE_THREADS, nqt)
+    if threads > 1:
+        ex = ThreadPoolExecutor(threads)
+        results = ex.map(work, range(nqt))
+    else:
+        ex, results = None, map(work, range(nqt))
+    try:
+        for qt, (pairs, mb, mh, kt, full, part, rb, cb) in enumerate(results):
+            pairs_map += pairs
+            if len(kt) == 0:
+                continue
+            mids = np.full(len(kt), -1, np.int64)
             for i, p in enumerate(part):
                 key = rb[i].tobytes()
                 mid = masks.get(key)
@@ -331,11 +354,14 @@ def trace_strips(strip, B, Hq, Hkv, N, L, map_b, map_h) -> TileMap:
                     row_bits.append(rb[i])
                     col_bits.append(cb[i])
                 mids[p] = mid
-        n_full += int(full.sum())
-        n_partial += int((~full).sum())
-        ent_row.append((mb * map_h + mh) * nqt + qt)
-        ent_kt.append(kt)
-        ent_mid.append(mids)
+            n_full += int(full.sum())
+            n_partial += int((~full).sum())
+            ent_row.append((mb * map_h + mh) * nqt + qt)
+            ent_kt.append(kt)
+            ent_mid.append(mids)
+    finally:
+        if ex is not None:
+            ex.shutdown()
 
     if ent_row:
         r = np.concatenate(ent_row)
