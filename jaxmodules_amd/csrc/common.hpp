@@ -15,8 +15,9 @@
 // 16*j + {0..3, 8..11} (hi = 0) or 16*j + {4..7, 12..15} (hi = 1): exactly
 // the 8 values a B (or A) operand of the next product needs for a 16-deep
 // k-step, provided the matching operand is read with the same row
-// permutation.  Transposed LDS buffers store rows in that permuted order
-// (tslot) so that each lane's 8 operand values are one 16-byte read.
+// permutation: the transposed operand reads (two ds_read_b64_tr_b16 of 4
+// rows each, tr_src) fetch rows {4 hi .. 4 hi + 3} and {8 + 4 hi .. 8 + 4 hi
+// + 3} of the k-step.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -294,59 +295,11 @@ __device__ __forceinline__ int tr_src(int lane, int mt, int sec) {
   return r * D + ((c ^ swz<D>(r)) << 3) + 4 * (i & 1);
 }
 
-// Permuted position of row r (0..63) of a sub-block inside a transposed row:
-// within every group of 16, rows {0-3, 8-11, 4-7, 12-15} are stored in that
-// order (bits 2 and 3 swapped), so the 8 rows one lane's C registers hold for
-// a 16-deep k-step are contiguous.
-__device__ __forceinline__ int tslot(int r) {
-  const int w = r & 15;
-  return (r & ~15) | (w & 3) | ((w & 4) << 1) | ((w & 8) >> 1);
-}
-
-// Transposed tile [D][64]: row d (128 bytes = 32 banks) holds 64 sequence
-// positions in tslot order, its 16-byte chunks XOR-swizzled with (d >> 1) & 7
-// so that 16 lanes reading rows d..d+15 at one chunk hit 16 distinct bank
-// groups (the row parity picks the bank half).
-__device__ __forceinline__ int tpos(int d, int s) {
-  return d * 64 + (((s >> 3) ^ ((d >> 1) & 7)) << 3) + (s & 7);
-}
-
-// Offset of the 16-byte operand chunk for k-step ks (16 rows) and lane half hi.
-__device__ __forceinline__ int tchunk(int d, int ks, int hi) {
-  return d * 64 + (((2 * ks + hi) ^ ((d >> 1) & 7)) << 3);
-}
-
-// Transposed write of G consecutive sequence rows r0..r0+G-1 (r0 % G == 0) of
-// head dims [8c, 8c+8), held as G 16-byte chunks.  Iteration j writes dim
-// 8c + (j ^ (c & 1)): the loaders give consecutive 16-lane groups consecutive
-// c, so the two halves of a 32-lane write cycle land on opposite row parities.
-template <int G>
-__device__ __forceinline__ void tr_write(uint16_t* T, const u32x4* x, int r0, int c) {
-  const int p = c & 1;
-  const int s0 = tslot(r0);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int jj = j ^ p;
-    const int sh = (jj & 1) * 16;
-    const int d = 8 * c + jj;
-    if constexpr (G == 4) {
-      const u32x2 w = {((x[0][j >> 1] >> sh) & 0xffffu) | ((x[1][j >> 1] >> sh) << 16),
-                       ((x[2][j >> 1] >> sh) & 0xffffu) | ((x[3][j >> 1] >> sh) << 16)};
-      *(u32x2*)&T[tpos(d, s0)] = w;
-    } else {
-      *(uint32_t*)&T[tpos(d, s0)] = ((x[0][j >> 1] >> sh) & 0xffffu) | ((x[1][j >> 1] >> sh) << 16);
-    }
-  }
-}
-
 // Bit of a 64-bit tile-mask word for C-register r of MFMA row tile t (rows
-// 32t + 8(r/4) + 4hi + r%4): w32 is the word's half for t, pre-shifted by 4hi.
-__device__ __forceinline__ bool mask_bit(uint32_t w32, int r) {
-  return (w32 >> (8 * (r >> 2) + (r & 3))) & 1u;
-}
-// the same bit as all ones (set) or zero (clear): one v_bfe_i32, after which
-// masking an element is one v_and_b32 (to 0) or v_bfi_b32 (to -inf) instead
-// of a compare and a select
+// 32t + 8(r/4) + 4hi + r%4), w32 being the word's half for t pre-shifted by
+// 4hi, as all ones (set) or zero (clear): one v_bfe_i32, after which masking
+// an element is one v_and_b32 (to 0) or bit-select (to -inf) instead of a
+// compare and a select
 __device__ __forceinline__ uint32_t mask_ones(uint32_t w32, int r) {
   uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)w32, 8 * (r >> 2) + (r & 3), 1);
   // opaque to the compiler, which would otherwise turn the AND back into a
