@@ -221,14 +221,6 @@ __device__ __forceinline__ int sw_off(int r, int c) {  // element offset of chun
   return r * D + ((c ^ swz<D>(r)) << 3);
 }
 
-// Row-major tile [rows][D] with rows padded to D + 8 elements, written from
-// VGPRs by a coalesced loader: 16 lanes reading 16 consecutive rows at one
-// chunk hit 16 distinct bank groups.
-template <int D>
-__device__ __forceinline__ int rm_off(int r, int c) {
-  return r * (D + 8) + (c << 3);
-}
-
 // Direct global->LDS tile loader: one global_load_lds_dwordx4 moves 1 KiB
 // (64 lanes x 16 bytes, lane L to LDS byte 16 L of the instruction's block).
 // Lane L of instruction block n covers row n * RPI + L / CPR of the tile and
@@ -271,18 +263,12 @@ __device__ __forceinline__ void lds_load16_buf(__amdgpu_buffer_rsrc_t r, uint32_
                                           (int)soff, 0, 0);
 }
 
-// Transposed operand read (ds_read_b64_tr_b16): inside each 16-lane group, if
-// lane j addresses X[r + j/4][c + 4 (j % 4)], lane i receives
-// X[r + k][c + i] for k = 0..3.
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(p));
-  return __builtin_bit_cast(u32x2, v);
-}
-
+// Transposed operand read (ds_read_b64_tr_b16, ds_read_tr8 below): inside
+// each 16-lane group, if lane j addresses X[r + j/4][c + 4 (j % 4)], lane i
+// receives X[r + k][c + i] for k = 0..3.
+//
 // Element offset, within a swizzled [rows][D] tile, of the address lane
-// `lane` supplies to lds_read_tr so that it receives the A operand
+// `lane` supplies to that read so that it receives the A operand
 // A[i = 32 mt + lane % 32][k = rows 16 ks + 4 hi + 8 sec + 0..3] of a
 // 32x32x16 MFMA k-step (sec = 0: operand slots 0-3, sec = 1: slots 4-7),
 // i.e. X[16 ks + 8 sec + 4 hi + k][32 mt + lane % 32].  Returned for ks = 0;
@@ -459,15 +445,11 @@ __device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return v;
 }
-// 16-byte LDS write issued where it stands, like ds_write64 below.
+// 16-byte LDS write issued where it stands (asm, like ds_read128: the
+// compiler neither reorders it against the asm reads nor makes it wait for
+// LDS-DMA loads it cannot tell apart from it).
 __device__ __forceinline__ void ds_write128(uint32_t addr, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
-}
-// 8-byte LDS write issued where it stands (asm, like ds_read128: the compiler
-// neither reorders it against the asm reads nor makes it wait for LDS-DMA loads
-// it cannot tell apart from it).
-__device__ __forceinline__ void ds_write64(uint32_t addr, u32x2 v) {
-  asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
 // s_waitcnt lgkmcnt(N) in the asm order; values read by ds_read128 /
 // ds_read_tr8 before it are passed through hold() after it, so that nothing
