@@ -437,7 +437,7 @@ __device__ __forceinline__ u32x4 ds_read128(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return v;
 }
-// Transposed 8-byte LDS read (ds_read_b64_tr_b16, lane mapping as lds_read_tr)
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16, lane mapping as at tr_src)
 // issued where it stands, like ds_read128.
 template <int OFF>
 __device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
