@@ -236,9 +236,10 @@ class Runner:
         self.res = torch.empty(nres + 256, dtype=torch.uint8, device=dev)
         self.rptr = (self.res.data_ptr() + 255) & ~255
         self.stream = torch.cuda.current_stream(dev).cuda_stream
+        from jaxmodules_amd import blockmap as bmap
+
         self.pairs = tm.pairs
-        self.fwd_flop = 4 * d * tm.pairs
-        self.bwd_flop = 10 * d * tm.pairs
+        self.fwd_flop, self.bwd_flop = bmap.flops(tm, d)  # 4 d and 10 d per unmasked pair
 
     def fwd(self):
         self._lib.check(self.lib.mattn_fwd(ctypes.byref(self.p), ctypes.byref(self.bm),
