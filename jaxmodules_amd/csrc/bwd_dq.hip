@@ -280,7 +280,7 @@ void bwd_dq_mfma(KArgs a) {
 // The dK/dV kernel left dS~ = f s dS of every present tile as its waves held
 // it (lane = key; DS_TILE layout in common.hpp), so per 64-key sub-block each
 // wave only streams its four 1 KiB blocks (one nontemporal 16-byte load per
-// lane each, PF sub-blocks ahead of use), turns them into B operands (lane =
+// lane each, one sub-block ahead of use), turns them into B operands (lane =
 // query) through 4 KiB of LDS of its own -- written as loaded, read back with
 // ds_read_b64_tr_b16, which the blocks' chunk order makes conflict-free -- and
 // runs
@@ -300,7 +300,6 @@ void bwd_dq_ds(KArgs a) {
   constexpr int NMD = D / 32;
   constexpr int NI = D / 32;       // load instructions per wave per 64-row sub-block
   constexpr int BLK = 512;         // elements one load instruction fills
-  constexpr int PF = 3;            // sub-blocks of fragments in flight ahead of use
 
   __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
   __shared__ __attribute__((aligned(16))) uint16_t FX[4 * 2048];  // per wave: one sub-block's blocks
@@ -374,7 +373,7 @@ void bwd_dq_ds(KArgs a) {
   // fragments of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2);
   // past the row's last sub-block the same four loads read one 16-byte line
   // at the start of the dS area for every lane (a cache hit, results unused),
-  // so that the number of loads issued per iteration does not depend on s
+  // which keeps the loop body free of a branch
   auto fetch = [&](int s, u32x4 (&f)[4]) {
     const bool real = s < nsb;
     const uint16_t* p = real ? frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512 : a.ds;
@@ -439,53 +438,41 @@ void bwd_dq_ds(KArgs a) {
     });
   };
 
-  // Sub-block s: its K' rows were loaded (into buffer s % 2) one iteration
-  // ahead, its fragments PF iterations ahead into ring slot s % (PF + 1).
-  // Vector memory loads retire in issue order (the K' DMA included), so the
-  // wait before the barrier may leave outstanding only what was issued after
-  // the later of this wave's K' loads of s and fragment loads of s.  Issue
-  // order: K'(0), F(0) .. F(PF - 1), then per iteration s: K'(s + 1), F(s + PF).
-  // At s >= 1, K'(s) (iteration s - 1) comes after F(s), and only F(s + PF -
-  // 1) follows it: 4 loads, issued (from a dummy address) also where that
-  // sub-block does not exist, so the wait is the same vmcnt(4) on every path
-  // into the loop's barrier (tests/lds_waits.py checks it on the compiled
-  // code).  At s = 0 it also waits for F(1) .. F(PF - 2), one sub-block early.
-  u32x4 fr[PF + 1][4];
+  // Sub-block s: its K' rows (into buffer s % 2) and its fragments (into slot
+  // s % 2) were loaded one iteration ahead.  Per iteration the wave waits for
+  // all its loads, issues the fragment loads of s + 1, passes the barrier and
+  // only then the K' loads of s + 1, into the buffer sub-block s - 1 used.
+  // Fragments two or three sub-blocks ahead, with the wait leaving the newer
+  // ones in flight, measured slower (0.470 and 0.485 against 0.452 ms on
+  // the 8192-query causal problem at 32 heads).
+  u32x4 fr[2][4];
   int nkt_ = 0;
   float nks = 1.f;  // key tile and K' scale of the prepared sub-block
   if (nsb > 0) {
     entry(0, nkt_, nks);
     launch(0, nkt_, std::integral_constant<int, 0>{});
-    __builtin_amdgcn_sched_barrier(0);
-    static_for<PF>([&](auto pc) {
-      constexpr int p = decltype(pc)::value;
-      fetch(p, fr[p]);
-    });
+    fetch(0, fr[0]);
   }
-  auto iter = [&](int s, auto bufc, auto slc) {
-    constexpr int BUF = decltype(bufc)::value, SL = decltype(slc)::value;
+  auto iter = [&](int s, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
     const float sks = nks;
     int kt1 = 0;
     if (s + 1 < nsb) entry(s + 1, kt1, nks);
-    // this wave's K' and fragment loads of s landed; the fragment loads of
-    // s + PF - 1 (4 loads), issued after them, may stay in flight
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's K' and fragment loads of s landed
+    fetch(s + 1, fr[1 - BUF]);                   // slot of s - 1, whose step is done
+    __builtin_amdgcn_sched_barrier(0);
     // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
     // wave's operand reads ended with lgkmcnt(0)).  No __syncthreads: its
-    // fence would also wait for the fragment loads in flight.
+    // fence would also wait for the fragment loads just issued.
     barrier_lds();
     if (s + 1 < nsb) launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
-    __builtin_amdgcn_sched_barrier(0);  // the fragment loads stay behind the K' loads
-    fetch(s + PF, fr[(SL + PF) % (PF + 1)]);
-    step(bufc, fr[SL], sks);
+    __builtin_amdgcn_sched_barrier(0);
+    step(bufc, fr[BUF], sks);
   };
-  // unrolled by UR = lcm(2, PF + 1) (2 K' buffers, PF + 1 fragment slots): every index static
-  constexpr int UR = (PF + 1) % 2 == 0 ? PF + 1 : 2 * (PF + 1);
-  for (int s = 0; s < nsb; s += UR) {
-    static_for<UR>([&](auto uc) {
-      constexpr int u = decltype(uc)::value;
-      if (s + u < nsb) iter(s + u, std::integral_constant<int, u % 2>{}, std::integral_constant<int, u % (PF + 1)>{});
-    });
+  // unrolled by two (two K' buffers, two fragment slots): every index static
+  for (int s = 0; s < nsb; s += 2) {
+    iter(s, std::integral_constant<int, 0>{});
+    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
   }
 
   // dQ through LDS (a quarter of the K' buffers per wave, free once every wave is done)

@@ -51,7 +51,7 @@ def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm, fwd_asm):
         # D = 64 / 128 x bfloat16 / float16 x storing dS or not
         "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 100, 8),
         "dq": (dq_asm, "11bwd_dq_mfma", 60, 4),
-        "dq_ds": (dq_asm, "9bwd_dq_ds", 60, 4),
+        "dq_ds": (dq_asm, "9bwd_dq_ds", 40, 4),
         "fwd": (fwd_asm, "8fwd_mfma", 50, 8),            # ... x float32 / 16-bit output
     }[which]
     names = _kernels(asm, stem)
@@ -96,29 +96,29 @@ def test_checker_follows_forward_branches():
 
 @pytest.mark.parametrize("which", ["dkdv", "dq", "dq_ds", "fwd"])
 def test_every_instantiation_retires_its_lds_dma_before_each_barrier(which, dkdv_asm, dq_asm, fwd_asm):
-    asm, stem, count = {
-        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 8),
-        "dq": (dq_asm, "11bwd_dq_mfma", 4),
-        "dq_ds": (dq_asm, "9bwd_dq_ds", 4),
-        "fwd": (fwd_asm, "8fwd_mfma", 8),
+    asm, stem, least, count = {
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 10, 8),
+        "dq": (dq_asm, "11bwd_dq_mfma", 10, 4),
+        "dq_ds": (dq_asm, "9bwd_dq_ds", 6, 4),      # D = 64: 2 K' loads x (prologue + 2 unrolled steps)
+        "fwd": (fwd_asm, "8fwd_mfma", 10, 8),
     }[which]
     names = _kernels(asm, stem)
     assert len(names) == count, names
     for name in names:
         dma, problems = lds_waits.check_dma(lds_waits.kernel_body(asm, name))
-        assert dma >= 10, (name, dma)
+        assert dma >= least, (name, dma)
         assert not problems, (name, problems[:5])
 
 
 def test_dma_checker_flags_the_dq_ds_wait_that_skipped_the_k_tile(dq_asm):
-    """vmcnt(8) ahead of dQ's barrier (two sub-blocks of fragment loads left in
-    flight, as an earlier count had it) leaves the K' DMA of the sub-block
-    outstanding: reported."""
+    """The K' DMA of a sub-block is the last thing a dQ wave issues before the
+    next iteration's wait; vmcnt(4) there (one sub-block of loads left in
+    flight) leaves it outstanding at the barrier: reported."""
     name = _kernels(dq_asm, "9bwd_dq_ds")[0]
     body = lds_waits.kernel_body(dq_asm, name)
-    waits = [i for i, l in enumerate(body) if l.strip() == "s_waitcnt vmcnt(4)"]
+    waits = [i for i, l in enumerate(body) if l.strip() == "s_waitcnt vmcnt(0)"]
     assert waits
-    planted = [("\ts_waitcnt vmcnt(8)" if i in waits else l) for i, l in enumerate(body)]
+    planted = [("\ts_waitcnt vmcnt(4)" if i in waits else l) for i, l in enumerate(body)]
     _, problems = lds_waits.check_dma(planted)
     assert any("global->LDS load" in p for p in problems)
 
