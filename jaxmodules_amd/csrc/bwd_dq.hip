@@ -279,11 +279,11 @@ void bwd_dq_mfma(KArgs a) {
 // ---------------------------------------------------------------------------
 // The dK/dV kernel left dS~ = f s dS of every present tile as its waves held
 // it (lane = key; DS_TILE layout in common.hpp), so per 64-key sub-block each
-// wave only streams its four 1 KiB blocks (one nontemporal 16-byte load per
-// lane each, one sub-block ahead of use), turns them into B operands (lane =
-// query) through 4 KiB of LDS of its own -- written as loaded, read back with
-// ds_read_b64_tr_b16, which the blocks' chunk order makes conflict-free -- and
-// runs
+// wave only streams its four 1 KiB blocks (nontemporal direct global->LDS
+// loads, 16 bytes per lane each, one sub-block ahead of use, into 4 KiB of LDS
+// of its own per buffer) and turns them into B operands (lane = query) with
+// ds_read_b64_tr_b16, which the blocks' chunk order makes conflict-free; it
+// then runs
 //   dQ^T += K'^T dS~^T    (A: K'^T by transposed reads of the K' tile in LDS)
 // 2 D flop per pair instead of recomputing S and dP (another 4 D); the
 // kernel streams 2 bytes per allowed pair from HBM.  Masked elements of a
@@ -302,7 +302,8 @@ void bwd_dq_ds(KArgs a) {
   constexpr int BLK = 512;         // elements one load instruction fills
 
   __shared__ __attribute__((aligned(16))) uint16_t K0[BN * D], K1[BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t FX[4 * 2048];  // per wave: one sub-block's blocks
+  // per buffer and wave: one sub-block's four dS~ blocks (buffer b at byte 16384 b)
+  __shared__ __attribute__((aligned(16))) uint16_t FX[2 * 4 * 2048];
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
@@ -370,16 +371,18 @@ void bwd_dq_ds(KArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) lds_load16(kp + kld[i], (BUF ? K1 : K0) + wofs + i * BLK);
   };
-  // fragments of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2);
-  // past the row's last sub-block the same four loads read one 16-byte line
-  // at the start of the dS area for every lane (a cache hit, results unused),
-  // which keeps the loop body free of a branch
-  auto fetch = [&](int s, u32x4 (&f)[4]) {
-    const bool real = s < nsb;
-    const uint16_t* p = real ? frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512 : a.ds;
-    const int step = real ? 512 : 0;
+  // the four blocks of sub-block s (k-steps 4 (s % 2) .. + 3 of tile e0 + s / 2)
+  // by direct global->LDS loads into buffer BUF: lane l's 16 bytes land at
+  // chunk l of each block, where the reads below expect them.  Nontemporal
+  // (cache policy 2): every byte is read once; temporal loads measured 4% slower.
+  auto fetch = [&](int s, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* p = frag + (int64_t)(e0 + (s >> 1)) * DS_TILE + (s & 1) * 4 * 512;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) f[k] = __builtin_nontemporal_load((const u32x4*)(p + k * step));
+    for (int k = 0; k < 4; ++k)
+      __builtin_amdgcn_global_load_lds(p + k * 512,
+                                       (__attribute__((address_space(3))) void*)(FX + BUF * 8192 + wave * 2048 + k * 512),
+                                       16, 0, 2);
   };
 
   f32x16 acc[NMD];
@@ -387,7 +390,7 @@ void bwd_dq_ds(KArgs a) {
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
   float kcur = 1.f;  // K' tile scale the accumulator is in
 
-  auto step = [&](auto bufc, const u32x4 (&f)[4], float sks) {
+  auto step = [&](auto bufc, float sks) {
     constexpr int BUF = decltype(bufc)::value;
     if (sks != kcur) {  // a tile with another K' scale (uniform; powers of two: exact)
       const float r = sks / kcur;
@@ -399,15 +402,10 @@ void bwd_dq_ds(KArgs a) {
     const uint32_t kb0 = lds_addr(BUF ? K1 : K0);
     const int tzo = opaque(tz);
     const uint32_t a0 = kb0 + 2 * (uint32_t)opaque(tb0), a1 = kb0 + 2 * (uint32_t)opaque(tb1);
-    // the sub-block's dS~ blocks into the wave's LDS and back transposed; the
-    // previous sub-block's reads of FX returned before its last MFMA (LDS
-    // serves a wave in order), so these writes cannot overtake them
-    const uint32_t fxo = opaque(fxw) + 16 * lane;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ds_write128(fxo + 1024 * k, f[k]);
+    // the sub-block's dS~ blocks read back transposed (B operands)
     u32x2 bq[4][2];
     static_for<4>([&](auto kc) {
-      constexpr int kk = decltype(kc)::value, off = 2048 * (kk / 2) + 256 * (kk % 2);
+      constexpr int kk = decltype(kc)::value, off = 16384 * BUF + 2048 * (kk / 2) + 256 * (kk % 2);
       bq[kk][0] = ds_read_tr8<off>(fb0);
       bq[kk][1] = ds_read_tr8<off>(fb1);
     });
@@ -423,7 +421,7 @@ void bwd_dq_ds(KArgs a) {
       constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PQ + 1);
       if constexpr (i + PQ < NSTEP) rq(std::integral_constant<int, i + PQ>{});
       lgkm_wait<2 * (i + PQ < NSTEP ? PQ : NSTEP - 1 - i)>();
-      if constexpr (i == 0) {  // this wait also covered the earlier FX writes and reads
+      if constexpr (i == 0) {  // this wait also covered the B operand reads
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           hold(bq[kk][0]);
@@ -438,38 +436,38 @@ void bwd_dq_ds(KArgs a) {
     });
   };
 
-  // Sub-block s: its K' rows (into buffer s % 2) and its fragments (into slot
-  // s % 2) were loaded one iteration ahead.  Per iteration the wave waits for
-  // all its loads, issues the fragment loads of s + 1, passes the barrier and
-  // only then the K' loads of s + 1, into the buffer sub-block s - 1 used.
-  // Fragments two or three sub-blocks ahead, with the wait leaving the newer
-  // ones in flight, measured slower (0.470 and 0.485 against 0.452 ms on
-  // the 8192-query causal problem at 32 heads).
-  u32x4 fr[2][4];
+  // Sub-block s: its K' rows and its dS~ blocks were loaded (into buffers
+  // s % 2) one iteration ahead.  Per iteration the wave waits for all its
+  // loads, passes the barrier and issues the loads of s + 1 into the buffers
+  // that sub-block s - 1 used.  On the 8192-query causal problem at 32 heads
+  // (0.449 ms) this measured as fast as loading the blocks one sub-block
+  // ahead into registers and writing them to LDS (161 against 127 registers),
+  // and faster than two or three sub-blocks ahead through registers (0.485
+  // and 0.470 ms).
   int nkt_ = 0;
   float nks = 1.f;  // key tile and K' scale of the prepared sub-block
   if (nsb > 0) {
     entry(0, nkt_, nks);
     launch(0, nkt_, std::integral_constant<int, 0>{});
-    fetch(0, fr[0]);
+    fetch(0, std::integral_constant<int, 0>{});
   }
   auto iter = [&](int s, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     const float sks = nks;
     int kt1 = 0;
     if (s + 1 < nsb) entry(s + 1, kt1, nks);
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's K' and fragment loads of s landed
-    fetch(s + 1, fr[1 - BUF]);                   // slot of s - 1, whose step is done
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's loads of s landed
     // every wave's K' loads of s landed; sub-block s - 1 fully consumed (each
-    // wave's operand reads ended with lgkmcnt(0)).  No __syncthreads: its
-    // fence would also wait for the fragment loads just issued.
+    // wave's operand reads ended with lgkmcnt(0))
     barrier_lds();
-    if (s + 1 < nsb) launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
+    if (s + 1 < nsb) {
+      launch(s + 1, kt1, std::integral_constant<int, 1 - BUF>{});
+      fetch(s + 1, std::integral_constant<int, 1 - BUF>{});
+    }
     __builtin_amdgcn_sched_barrier(0);
-    step(bufc, fr[BUF], sks);
+    step(bufc, sks);
   };
-  // unrolled by two (two K' buffers, two fragment slots): every index static
+  // unrolled by two (two buffers of each): every index static
   for (int s = 0; s < nsb; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});

@@ -445,12 +445,6 @@ __device__ __forceinline__ u32x2 ds_read_tr8(uint32_t addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
   return v;
 }
-// 16-byte LDS write issued where it stands (asm, like ds_read128: the
-// compiler neither reorders it against the asm reads nor makes it wait for
-// LDS-DMA loads it cannot tell apart from it).
-__device__ __forceinline__ void ds_write128(uint32_t addr, u32x4 v) {
-  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
-}
 // s_waitcnt lgkmcnt(N) in the asm order; values read by ds_read128 /
 // ds_read_tr8 before it are passed through hold() after it, so that nothing
 // using them is scheduled ahead of the wait.  hold() also pins an MFMA result

@@ -110,10 +110,10 @@ def test_every_instantiation_retires_its_lds_dma_before_each_barrier(which, dkdv
         assert not problems, (name, problems[:5])
 
 
-def test_dma_checker_flags_the_dq_ds_wait_that_skipped_the_k_tile(dq_asm):
-    """The K' DMA of a sub-block is the last thing a dQ wave issues before the
-    next iteration's wait; vmcnt(4) there (one sub-block of loads left in
-    flight) leaves it outstanding at the barrier: reported."""
+def test_dma_checker_flags_a_dq_ds_wait_that_leaves_a_dma_in_flight(dq_asm):
+    """A dQ wave's last loads before the next iteration's wait are the DMA of
+    the next sub-block's K' rows and dS~ blocks; vmcnt(4) there leaves the
+    newest of them outstanding at the barrier: reported."""
     name = _kernels(dq_asm, "9bwd_dq_ds")[0]
     body = lds_waits.kernel_body(dq_asm, name)
     waits = [i for i, l in enumerate(body) if l.strip() == "s_waitcnt vmcnt(0)"]
