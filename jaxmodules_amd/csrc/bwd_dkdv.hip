@@ -421,7 +421,7 @@ void bwd_dkdv_mfma(KArgs a) {
       const int c = TileRows<D>::chunk(part, j);
       const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl);
       *(u32x4*)&Ks[sw_off<D>(r, c)] = yk;
-      *(u32x4*)(kd + 8 * c) = yk;
+      __builtin_nontemporal_store(yk, (u32x4*)(kd + 8 * c));
     }
     if (tid == 0) a.ksc[col] = kscl;
     ksc = kscl;
@@ -504,8 +504,8 @@ void bwd_dkdv_mfma(KArgs a) {
     const u32x4 xk = *(const u32x4*)((const uint16_t*)sk + off);
     const u32x4 xv = *(const u32x4*)((const uint16_t*)sv + off);
     if (key_n < a.Lk) {
-      *(u32x4*)((char*)a.dk + 2 * ((int64_t)b * a.dks[0] + (int64_t)key_n * a.dks[1] + (int64_t)hk * a.dks[2] + 8 * c)) = xk;
-      *(u32x4*)((char*)a.dv + 2 * ((int64_t)b * a.dvs[0] + (int64_t)key_n * a.dvs[1] + (int64_t)hk * a.dvs[2] + 8 * c)) = xv;
+      __builtin_nontemporal_store(xk, (u32x4*)((char*)a.dk + 2 * ((int64_t)b * a.dks[0] + (int64_t)key_n * a.dks[1] + (int64_t)hk * a.dks[2] + 8 * c)));
+      __builtin_nontemporal_store(xv, (u32x4*)((char*)a.dv + 2 * ((int64_t)b * a.dvs[0] + (int64_t)key_n * a.dvs[1] + (int64_t)hk * a.dvs[2] + 8 * c)));
     }
   }
 }

@@ -269,7 +269,7 @@ void bwd_dq_mfma(KArgs a) {
   uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * 32 * D;
   static_assert(2 * 32 * D <= 2 * BN * D, "output staging");
   const int r0 = qt * TILE + 32 * wave;
-  store_rows<D, 2>(acc, a.scale * pow2_rcp(tds * ds_s * kcur), stage, a.dq,
+  store_rows<D, 2, true>(acc, a.scale * pow2_rcp(tds * ds_s * kcur), stage, a.dq,
                    (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2], a.dqs[1],
                    min(32, a.Lq - r0), lane, E::pack2);
 }
@@ -478,7 +478,7 @@ void bwd_dq_ds(KArgs a) {
   __syncthreads();
   uint16_t* stage = (wave < 2 ? K0 : K1) + (wave & 1) * 32 * D;
   static_assert(2 * 32 * D <= BN * D, "output staging");
-  store_rows<D, 2>(acc, osc * pow2_rcp(kcur), stage, odq, orow, ostr, nrows, lane, E::pack2);
+  store_rows<D, 2, true>(acc, osc * pow2_rcp(kcur), stage, odq, orow, ostr, nrows, lane, E::pack2);
 }
 
 // ---------------------------------------------------------------------------

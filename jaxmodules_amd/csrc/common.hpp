@@ -380,8 +380,9 @@ struct EntryCache {
 // chunks, chunk c of row r at c ^ (r % chunks-per-row), then read back so that
 // each global store instruction writes whole rows, 16 bytes per lane.  Row r
 // goes to out + ES * (row0 + r * rstride) when r < nrows.  ES = 4 stores
-// float32, ES = 2 the 16-bit values pack2 makes.
-template <int D, int ES, class Pack>
+// float32, ES = 2 the 16-bit values pack2 makes.  NT: nontemporal stores
+// (rows that no kernel of the step reads back soon).
+template <int D, int ES, bool NT, class Pack>
 __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc, void* lds, void* out,
                                            int64_t row0, int64_t rstride, int nrows, int lane, Pack pack2) {
   constexpr int RB = D * ES;     // bytes per row
@@ -407,7 +408,11 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc
     const int n = 64 * i + lane;
     const int row = n / CPR, c = n % CPR;
     const u32x4 v = *(const u32x4*)(L + row * RB + ((c ^ (row & (CPR - 1))) << 4));
-    if (row < nrows) *(u32x4*)((char*)out + (int64_t)ES * (row0 + (int64_t)row * rstride) + 16 * c) = v;
+    u32x4* dst = (u32x4*)((char*)out + (int64_t)ES * (row0 + (int64_t)row * rstride) + 16 * c);
+    if (row < nrows) {
+      if constexpr (NT) __builtin_nontemporal_store(v, dst);
+      else *dst = v;
+    }
   }
 }
 

@@ -348,7 +348,7 @@ void fwd_mfma(KArgs a) {
   uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * BN * D;
   static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
   const int r0 = qt * TILE + 32 * wave;
-  store_rows<D, OUT_F32 ? 4 : 2>(acc, inv, stage, a.out,
+  store_rows<D, OUT_F32 ? 4 : 2, true>(acc, inv, stage, a.out,
                                  (int64_t)b * a.os[0] + (int64_t)r0 * a.os[1] + (int64_t)h * a.os[2], a.os[1],
                                  min(32, a.Lq - r0), lane, E::pack2);
 }
