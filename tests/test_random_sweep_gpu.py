@@ -5,9 +5,10 @@ size, query/key lengths (1..400, often ragged), GQA layout, head dim
 output dtype and one mask family: causal, none, an element window with the
 reference's block window, packed documents, a per-head tile table, a
 head-specific lambda, or cross lengths.  The draw is fixed by the seed, so
-every run checks the same problems: seeds 0-23, and the draws of a one-off
+every run checks the same problems: seeds 0-23, the draws of a one-off
 600-problem run (seeds 24-623) that failed the gate with the kernels' earlier
-bfloat16 dS / dO operands (KNOWN_DRAWS).
+bfloat16 dS / dO operands (KNOWN_DRAWS), and the three draws of a second
+one-off run (seeds 624-1023, the current kernels) that miss it (LATER_FLOOR).
 
 threshold_kernel is a softmax with scale 1 instead of 1/sqrt(d), so its
 draws see logits of unit variance (Q, K ~ N(0,1) d^-0.25), seven times
@@ -119,6 +120,23 @@ FLOOR = {
 @pytest.mark.parametrize("seed", [pytest.param(s, marks=pytest.mark.xfail(strict=True, reason=FLOOR[s]))
                                   if s in FLOOR else s for s in KNOWN_DRAWS])
 def test_known_draw(seed):
+    run_draw(seed)
+
+
+# The misses of the 400 draws of seeds 624-1023: one bfloat16 output element
+# each, rounded one ulp off because the float32 sum of float16-rounded products
+# lands past the rounding midpoint.  tests/test_rounding_model.py reproduces
+# each ratio with the model of the kernels' roundings.
+LATER_FLOOR = {
+    647: "1 dQ element of 199680 at 1.015x the bound (threshold_kernel; float16 operand floor)",
+    696: "1 dV element of 188928 at 1.051x the bound (float16 operand floor)",
+    976: "1 dV element of 247040 at 1.024x the bound (float16 operand floor)",
+}
+
+
+@pytest.mark.parametrize("seed", [pytest.param(s, marks=pytest.mark.xfail(strict=True, reason=r))
+                                  for s, r in sorted(LATER_FLOOR.items())])
+def test_later_floor_draw(seed):
     run_draw(seed)
 
 
