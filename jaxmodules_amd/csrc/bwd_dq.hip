@@ -340,8 +340,9 @@ void bwd_dq_ds(KArgs a) {
   const int tb1 = tr_src<D>(lane, 0, 1) - tz;
   const int wofs = __builtin_amdgcn_readfirstlane(NI * wave * BLK);
   EntryCache ec;
-  // The wave's LDS blocks: block b = 2 (kk / 2) + t (32-key group kk / 2 of the
-  // sub-block, 16-query half t) at 1 KiB b, chunk of lane l at 16 l.  B operand
+  // The wave's LDS blocks in each buffer (buffer u at byte 16384 u of FX):
+  // block b = 2 (kk / 2) + t (32-key group kk / 2 of the sub-block, 16-query
+  // half t) at 1 KiB b, chunk of lane l at 16 l.  B operand
   // of k-step kk (keys 16 kk + 4 hi + 8 j + i, i = 0..3, in slots 4 j + i) of
   // lane (query 16 t + i16, half hi): read j supplies, for lane i16 of its
   // 16-lane group, the 8 bytes of key 16 (kk % 2) + 4 hi + 8 j + i16 / 4 (of
