@@ -26,7 +26,6 @@ reference's ``create_block_mask``.
 from __future__ import annotations
 
 import ctypes
-import math
 import os
 from dataclasses import dataclass, field
 from typing import Callable, Optional, Tuple
