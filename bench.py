@@ -251,7 +251,7 @@ class Runner:
         self._lib.check(self.lib.mattn_bwd_stage(
             ctypes.byref(self.p), ctypes.byref(self.bm), stage, self.q.data_ptr(), self.k.data_ptr(),
             self.v.data_ptr(), self.o.data_ptr(), self.do.data_ptr(), self.lse.data_ptr(), self.rptr,
-            self.wptr, self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.stream),
+            self.wptr, self.ws_bytes, self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.stream),
             f"bwd stage {stage}")
 
     def measure(self, steps, warmup):

@@ -26,9 +26,8 @@
  *     gradients (attention.py:91-100).
  *   - All buffers are caller-owned device memory.  The library never
  *     allocates, frees or synchronises on the call path; every launch is
- *     enqueued on the caller's stream.  The only atomics are maxima of
- *     non-negative floats in the backward preprocess, whose result does not
- *     depend on their order, so results are bitwise reproducible.
+ *     enqueued on the caller's stream.  No kernel uses atomics, so results
+ *     are bitwise reproducible.
  *   - Return value 0 is success, a negative value is an error code whose text
  *     is given by mattn_strerror().
  */
@@ -57,7 +56,11 @@ enum mattn_status {
   MATTN_ERR_LAUNCH = -7,        /* the HIP runtime rejected a launch           */
   MATTN_ERR_TOO_LARGE = -8,     /* a size exceeds 32-bit index ranges          */
   MATTN_ERR_SCRATCH = -9,       /* mattn_bwd_noalloc: workspace > scratch      */
-  MATTN_ERR_DEVICE = -10        /* mattn_bwd_noalloc: no current device/scratch */
+  MATTN_ERR_DEVICE = -10,       /* mattn_bwd_noalloc: no current device/scratch,
+                                   or the stream belongs to another device     */
+  MATTN_ERR_WORKSPACE = -11,    /* workspace_bytes < mattn_bwd_workspace_bytes */
+  MATTN_ERR_RESIDUAL = -12      /* MFMA backward without MATTN_FWD_FOR_BWD: the
+                                   residual holds no float16 copy of Q         */
 };
 
 /* mattn_problem.flags: the forward also leaves in its residual the float16
@@ -70,6 +73,19 @@ enum mattn_status {
  * 16-bit inputs at D <= 128 (ignored on the SIMT path).  Faster at D = 128,
  * where recomputing costs more than streaming 2 bytes per allowed pair. */
 #define MATTN_BWD_DS 2
+/* mattn_problem.flags: float32 arithmetic for 16-bit inputs.  The problem runs
+ * on the SIMT kernels (every product and sum in float32, the inputs read
+ * exactly), as float32 inputs do, instead of the MFMA kernels, whose
+ * operands P, dS and dO are rounded to float16 (11 significant bits).  Set it
+ * for a forward and for its backward alike; the forward then has no residual.
+ * For kernels sharper than the default scale 1/sqrt(d) (the reference's
+ * threshold_kernel has scale 1, attention.py:18-36), where rows concentrate
+ * on single keys and dS = P (dP - delta) cancels below the float16 operand
+ * rounding.  The scores are then compensated dot products (about twice
+ * float32's precision) for every dtype, and the forward's residual
+ * (mattn_fwd_workspace_bytes) holds each row's lse rounding error, which the
+ * backward reads. */
+#define MATTN_PRECISE 4
 
 /* Tile size of the block map, in queries x keys. */
 #define MATTN_TILE_Q 128
@@ -81,7 +97,7 @@ typedef struct mattn_problem {
   int32_t o_dtype;   /* enum mattn_dtype of O and dO: dtype, or MATTN_F32  */
   float scale;       /* softmax scale; the reference's default_kernel uses
                         1/sqrt(D) (attention.py:39-50)                     */
-  int32_t flags;     /* MATTN_FWD_FOR_BWD or 0                             */
+  int32_t flags;     /* MATTN_FWD_FOR_BWD | MATTN_BWD_DS | MATTN_PRECISE   */
   /* element strides {batch, sequence, head}; D is contiguous */
   int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3];
   int64_t do_stride[3], dq_stride[3], dk_stride[3], dv_stride[3];
@@ -147,8 +163,9 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
  * aligned pointer); with it, mattn_bwd_workspace_bytes(p, bm).  0 for an
  * invalid problem.
  * Head dimensions 64 and 128 with 16-bit inputs run on the MFMA kernels;
- * float32 inputs, and D = 256 for every dtype (the host pads d in (128, 256]
- * with zeros), run on float32 SIMT kernels, whose workspace is delta alone. */
+ * float32 inputs, D = 256 for every dtype (the host pads d in (128, 256]
+ * with zeros) and MATTN_PRECISE problems run on float32 SIMT kernels, whose
+ * workspace is one float32 per query row. */
 size_t mattn_workspace_bytes(const mattn_problem* p);
 
 /* Bytes of device workspace mattn_bwd needs for this map, MATTN_BWD_DS
@@ -157,11 +174,11 @@ size_t mattn_workspace_bytes(const mattn_problem* p);
  * (Hq / map_h) tiles.  Host only; 0 for an invalid problem or map. */
 size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* bm);
 
-/* Bytes of the forward's residual buffer (256-byte aligned pointer; 0 for
- * float32 inputs and for D = 256): float16 copies of V and (with
- * MATTN_FWD_FOR_BWD) Q, each
- * times a power of two per 128-row tile, which the forward's P V product and
- * the backward read. */
+/* Bytes of the forward's residual buffer (256-byte aligned pointer): float16
+ * copies of V and (with MATTN_FWD_FOR_BWD) Q, each times a power of two per
+ * 128-row tile, which the forward's P V product and the backward read (16-bit
+ * inputs at D <= 128); one float32 per query row under MATTN_PRECISE; 0
+ * otherwise (float32 inputs, D = 256). */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
 
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).
@@ -178,27 +195,31 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm,
  *   do_       : upstream gradient, [B, Lq, Hq, D] of o_dtype
  *   o, lse    : the forward's outputs
  *   residual  : the forward's residual buffer (16-bit inputs at D <= 128;
- *               that forward ran with MATTN_FWD_FOR_BWD), read only; may be
- *               NULL when mattn_fwd_workspace_bytes(p) == 0
- *   workspace : mattn_bwd_workspace_bytes(p, bm) bytes (scratch)
+ *               that forward ran with MATTN_FWD_FOR_BWD, which p->flags must
+ *               carry, else MATTN_ERR_RESIDUAL), read only; may be NULL when
+ *               mattn_fwd_workspace_bytes(p) == 0
+ *   workspace : workspace_bytes bytes of scratch, at least
+ *               mattn_bwd_workspace_bytes(p, bm) (else MATTN_ERR_WORKSPACE)
  *   dq, dk, dv: gradients of dtype, every element written (no pre-zeroing). */
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm,
               const void* q, const void* k, const void* v,
               const void* o, const void* do_, const float* lse, const void* residual,
-              void* workspace, void* dq, void* dk, void* dv, void* stream);
+              void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv, void* stream);
 
 /* The three stages of mattn_bwd, in the order they must run on one stream:
  * MATTN_BWD_PRE (delta = rowsum(dO * O) and the float16 copy of dO, into the
  * workspace), MATTN_BWD_DKDV (also writes the float16 copy of K, and with
  * MATTN_BWD_DS every tile's dS, into the workspace), then MATTN_BWD_DQ (reads
- * them).  mattn_bwd == the three stages
+ * them).  On the SIMT path MATTN_BWD_PRE does nothing: those kernels take
+ * dP - delta as dO . (V - O) per pair.  mattn_bwd == the three stages
  * in order.  Same arguments as mattn_bwd; exposed so a caller can time the
  * stages. */
 enum mattn_bwd_stage { MATTN_BWD_PRE = 0, MATTN_BWD_DKDV = 1, MATTN_BWD_DQ = 2 };
 int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     const void* q, const void* k, const void* v,
                     const void* o, const void* do_, const float* lse, const void* residual,
-                    void* workspace, void* dq, void* dk, void* dv, void* stream);
+                    void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv,
+                    void* stream);
 
 /* Size of the library's static device scratch used by mattn_bwd_noalloc. */
 #define MATTN_SCRATCH_BYTES (256u << 20)
@@ -211,7 +232,9 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
  * is for callers that cannot allocate: code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Problems whose
  * mattn_bwd_workspace_bytes(p, bm) exceeds MATTN_SCRATCH_BYTES return
- * MATTN_ERR_SCRATCH (clear MATTN_BWD_DS to run a larger one here).  Every call on one device shares that device's scratch:
+ * MATTN_ERR_SCRATCH (clear MATTN_BWD_DS to run a larger one here).  The
+ * stream must belong to the current device (MATTN_ERR_DEVICE otherwise: the
+ * scratch used is that device's).  Every call on one device shares that device's scratch:
  * calls that overlap on one device (other streams, other threads) race.  No
  * scratch content carries over between calls (each call writes all it reads). */
 int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm,

@@ -18,8 +18,9 @@ LIB_PATH = os.environ.get("MATTN_LIBRARY") or os.path.join(
 MATTN_BF16, MATTN_F16, MATTN_F32 = 0, 1, 2
 MATTN_FWD_FOR_BWD = 1
 MATTN_BWD_DS = 2
+MATTN_PRECISE = 4
 TILE_Q = TILE_K = 128
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 STATUS = {
     0: "MATTN_OK",
@@ -33,6 +34,8 @@ STATUS = {
     -8: "MATTN_ERR_TOO_LARGE",
     -9: "MATTN_ERR_SCRATCH",
     -10: "MATTN_ERR_DEVICE",
+    -11: "MATTN_ERR_WORKSPACE",
+    -12: "MATTN_ERR_RESIDUAL",
 }
 
 # every symbol include/mattn.h declares
@@ -118,9 +121,10 @@ def load():
         lib.mattn_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mattn_fwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_fwd.restype = ctypes.c_int
-        lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        sz = ctypes.c_size_t
+        lib.mattn_bwd.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp, vp, vp, vp]
         lib.mattn_bwd.restype = ctypes.c_int
-        lib.mattn_bwd_stage.argtypes = [P, M, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.mattn_bwd_stage.argtypes = [P, M, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp, vp, vp, vp]
         lib.mattn_bwd_noalloc.argtypes = [P, M, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.mattn_bwd_noalloc.restype = ctypes.c_int
         lib.mattn_bwd_stage.restype = ctypes.c_int

@@ -83,7 +83,7 @@ def threshold_kernel(threshold: Optional[float] = None):
     return kernel_fn
 
 
-_PROBED: dict = {}
+_PROBED: "OrderedDict[tuple, float]" = OrderedDict()  # bounded like the tile-map cache
 
 
 def _call_kernel(kernel_fn, q, k) -> float:
@@ -111,8 +111,9 @@ def kernel_scale(kernel_fn, d: int) -> float:
     s = getattr(kernel_fn, "_mattn_scale", "missing")
     if s != "missing":
         return 1.0 / math.sqrt(d) if s is None else float(s)
-    key = (kernel_fn, d)
+    key = (_mask_key(kernel_fn), d)  # by content, like mask functions (identity as fallback)
     if key in _PROBED:
+        _PROBED.move_to_end(key)
         return _PROBED[key]
     rng = np.random.default_rng(1234)
     xs, ys = [], []
@@ -138,6 +139,8 @@ def kernel_scale(kernel_fn, d: int) -> float:
     # jnp-based kernels, while the scale itself is a float32 kernel argument
     sc = float(np.float32(sc))
     _PROBED[key] = sc
+    if len(_PROBED) > _CACHE_SIZE:
+        _PROBED.popitem(last=False)
     return sc
 
 
@@ -153,11 +156,24 @@ class _Unfrozen(Exception):
     pass
 
 
-def _freeze(v, depth=0):
+# modules whose functions and classes are keyed by name: their behaviour is
+# fixed by the installed library, not by values a caller can change
+_LIB_MODULES = ("numpy", "torch", "math", "builtins", "operator")
+
+
+def _lib_object(v) -> bool:
+    mod = getattr(v, "__module__", None) or type(v).__module__ or ""
+    return mod.split(".")[0] in _LIB_MODULES
+
+
+def _freeze(v, depth=0, names=()):
     """A hashable value standing for what ``v`` contributes to a mask function's
     result: plain values as they are, containers and numpy arrays (and small
-    host tensors) by content, modules by name, functions by their own key;
-    anything else raises _Unfrozen."""
+    host tensors) by content, functions by their own key, library functions and
+    classes by name, and a module by the values of those of its attributes that
+    the mask's code names (``names``: its co_names, which hold every global
+    and attribute it reads), so that a changed module attribute gives another
+    key; anything else raises _Unfrozen."""
     import types
 
     if depth > 8:
@@ -175,15 +191,18 @@ def _freeze(v, depth=0):
         return _freeze(v.detach().numpy(), depth + 1)
     if isinstance(v, (tuple, list, frozenset, set)):
         items = sorted(v, key=repr) if isinstance(v, (set, frozenset)) else v
-        return (type(v).__name__, tuple(_freeze(x, depth + 1) for x in items))
+        return (type(v).__name__, tuple(_freeze(x, depth + 1, names) for x in items))
     if isinstance(v, dict):
-        return ("dict", tuple(sorted(((repr(k), _freeze(x, depth + 1)) for k, x in v.items()))))
+        return ("dict", tuple(sorted(((repr(k), _freeze(x, depth + 1, names)) for k, x in v.items()))))
     if isinstance(v, types.ModuleType):
-        return ("module", v.__name__)
+        d = vars(v)
+        return ("module", v.__name__, tuple((n, _freeze(d[n], depth + 1, names)) for n in sorted(names) if n in d))
     if isinstance(v, types.FunctionType):
         return ("fn", _fn_content(v, depth + 1))
-    if isinstance(v, (types.BuiltinFunctionType, np.ufunc)):
-        return ("builtin", getattr(v, "__module__", None), v.__name__)
+    if isinstance(v, (types.BuiltinFunctionType, np.ufunc)) or (
+            (isinstance(v, type) or type(v).__name__ == "_ArrayFunctionDispatcher") and _lib_object(v)):
+        return ("builtin", getattr(v, "__module__", None), getattr(v, "__qualname__", None),
+                getattr(v, "__name__", None))
     raise _Unfrozen
 
 
@@ -199,11 +218,11 @@ def _fn_content(fn, depth=0):
         stack.extend(x for x in c.co_consts if hasattr(x, "co_names"))
     g = fn.__globals__
     try:
-        cells = tuple(_freeze(c.cell_contents, depth + 1) for c in (fn.__closure__ or ()))
+        cells = tuple(_freeze(c.cell_contents, depth + 1, names) for c in (fn.__closure__ or ()))
     except ValueError:  # an empty closure cell
         raise _Unfrozen
-    return (code, _freeze(fn.__defaults__, depth + 1), _freeze(fn.__kwdefaults__, depth + 1), cells,
-            tuple((n, _freeze(g[n], depth + 1)) for n in sorted(names) if n in g))
+    return (code, _freeze(fn.__defaults__, depth + 1, names), _freeze(fn.__kwdefaults__, depth + 1, names), cells,
+            tuple((n, _freeze(g[n], depth + 1, names)) for n in sorted(names) if n in g))
 
 
 def _mask_key(mask_fn):
@@ -332,13 +351,14 @@ def _stream(device) -> int:
 
 
 def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float32,
-                  heads_major: bool = False, for_backward: bool = False):
+                  heads_major: bool = False, for_backward: bool = False, precise: bool = False):
     """(O [B, N, Hq, d] in out_dtype, base-2 LSE [B, Hq, N], residual) via
     mattn_fwd.  ``heads_major`` lays O out in memory as [B, Hq, N, d] (the
     returned tensor is the [B, N, Hq, d] view of it).  The residual (a uint8
-    tensor; None for float32 inputs and at d = 256, which the SIMT kernels
-    serve) holds the float16 V copy and, with ``for_backward``, the float16 Q
-    copy that mattn_backward reads."""
+    tensor; None for float32 inputs, at d = 256 and with ``precise``, which
+    the SIMT kernels serve) holds the float16 V copy and, with
+    ``for_backward``, the float16 Q copy that mattn_backward reads.
+    ``precise``: float32 arithmetic for 16-bit inputs (MATTN_PRECISE)."""
     lib = _lib.load()
     B, N, Hq, d = q.shape
     if heads_major:
@@ -348,7 +368,7 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
     lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
     _check_map(tm, q, k)
     p = _problem(q, k, v, o, scale)
-    p.flags = _lib.MATTN_FWD_FOR_BWD if for_backward else 0
+    p.flags = (_lib.MATTN_FWD_FOR_BWD if for_backward else 0) | (_lib.MATTN_PRECISE if precise else 0)
     bm = device_blockmap(tm, q.device)
     nws = int(lib.mattn_fwd_workspace_bytes(ctypes.byref(p)))
     res, rptr = _workspace(nws, q.device)
@@ -383,7 +403,7 @@ def bwd_flags(p, bm) -> int:
     forward's flags plus MATTN_BWD_DS where STORE_DS selects it."""
     lib = _lib.load()
     flags = p.flags & ~_lib.MATTN_BWD_DS
-    if STORE_DS is False or p.dtype == _lib.MATTN_F32 or p.D > 128:
+    if STORE_DS is False or p.dtype == _lib.MATTN_F32 or p.D > 128 or (p.flags & _lib.MATTN_PRECISE):
         return flags
     if STORE_DS is None:
         if p.D != 128:
@@ -397,15 +417,16 @@ def bwd_flags(p, bm) -> int:
     return flags | _lib.MATTN_BWD_DS
 
 
-def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None):
+def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None, precise: bool = False):
     """(dQ, dK, dV) via mattn_bwd; ``res`` is mattn_forward's residual (run
-    with for_backward=True)."""
+    with for_backward=True and the same ``precise``)."""
     lib = _lib.load()
     _check_map(tm, q, k)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     p = _problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
+    p.flags = _lib.MATTN_FWD_FOR_BWD | (_lib.MATTN_PRECISE if precise else 0)
     bm = device_blockmap(tm, q.device)
     p.flags = bwd_flags(p, bm)
     nws = int(lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)))
@@ -414,7 +435,8 @@ def mattn_backward(q, k, v, o, lse, do, tm: bmap.TileMap, scale: float, res=None
     ws, wptr = _workspace(max(nws, 256), q.device)
     _lib.check(lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(),
                              v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(), _aligned(res),
-                             wptr, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)),
+                             wptr, max(nws, 256), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                             _stream(q.device)),
                "mattn_bwd")
     return dq, dk, dv
 
@@ -431,19 +453,20 @@ class _MaskedAttention(torch.autograd.Function):
     rounding (2^-9 of |V|) in dQ and dK."""
 
     @staticmethod
-    def forward(ctx, q, k, v, tm, scale, out_dtype, heads_major=False):
+    def forward(ctx, q, k, v, tm, scale, out_dtype, heads_major=False, precise=False):
         grads = any(ctx.needs_input_grad[:3])
-        o, lse, res = mattn_forward(q, k, v, tm, scale, torch.float32, heads_major, for_backward=grads)
+        o, lse, res = mattn_forward(q, k, v, tm, scale, torch.float32, heads_major, for_backward=grads,
+                                    precise=precise)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.tm, ctx.scale, ctx.res = tm, scale, res
+        ctx.tm, ctx.scale, ctx.res, ctx.precise = tm, scale, res, precise
         return o if out_dtype == torch.float32 else o.to(out_dtype)
 
     @staticmethod
     def backward(ctx, do):
         q, k, v, o, lse = ctx.saved_tensors
         do = _ready(do.to(o.dtype))
-        dq, dk, dv = mattn_backward(q, k, v, o, lse, do, ctx.tm, ctx.scale, ctx.res)
-        return dq, dk, dv, None, None, None, None
+        dq, dk, dv = mattn_backward(q, k, v, o, lse, do, ctx.tm, ctx.scale, ctx.res, ctx.precise)
+        return dq, dk, dv, None, None, None, None, None
 
 
 def _kernel_dim(d: int) -> int:
@@ -458,6 +481,28 @@ def _pad_dim(x: torch.Tensor, D: int) -> torch.Tensor:
     return x if x.shape[-1] == D else torch.nn.functional.pad(x, (0, D - x.shape[-1]))
 
 
+PRECISIONS = (None, "default", "highest")
+
+
+def use_precise(precision: Optional[str], scale: float, d: int) -> bool:
+    """Whether a problem runs with MATTN_PRECISE.
+
+    "default": 16-bit inputs run on the MFMA kernels, whose computed operands
+    (P, dS, dO) are rounded to float16, 11 significant bits; float32 inputs on
+    the float32 SIMT kernels.  "highest": the float32 SIMT kernels for every
+    dtype, with the scores formed as compensated dot products (about twice
+    float32's precision).  None picks "highest" for kernels sharper than the
+    default scale 1/sqrt(d) (threshold_kernel's is 1, attention.py:18-36):
+    their logits spread sqrt(d) times wider, rows concentrate on single keys,
+    dS = P (dP - delta) cancels below what 11-bit operands resolve, and scores
+    of tens of units carry float32's own rounding into the weights."""
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+    if precision is None:
+        return abs(scale) > (1.0 + 1e-6) / math.sqrt(d)
+    return precision == "highest"
+
+
 def masked_attention_via_map(
     Q: torch.Tensor,
     K: torch.Tensor,
@@ -469,6 +514,7 @@ def masked_attention_via_map(
     block_size: Optional[int] = None,
     window_size: Optional[Tuple[int, int]] = None,
     out_dtype: Optional[torch.dtype] = None,
+    precision: Optional[str] = None,
 ) -> torch.Tensor:
     """Memory-efficient masked attention (attention.py:347-455).
 
@@ -485,6 +531,11 @@ def masked_attention_via_map(
     out_dtype: dtype of the output.  Default float32, which is what the
         reference returns (its running accumulators are float32,
         attention.py:173); pass Q.dtype for a 16-bit output.
+    precision: None, "default" or "highest" (use_precise): 16-bit inputs run
+        on float16-operand MFMA kernels by default and in float32 arithmetic
+        (compensated scores) with "highest", which None selects for kernels
+        sharper than default_kernel (threshold_kernel).  Not a reference
+        argument.
 
     Returns [B, N, Hq, d] (or [N, Hq, d]); differentiable w.r.t. Q, K, V.
     Rows with no allowed key are zero (attention.py:91-100).
@@ -507,9 +558,10 @@ def masked_attention_via_map(
         Q, scale = -Q, -scale
     elif scale == 0:
         Q, scale = Q * 0, 1.0
+    precise = use_precise(precision, scale, plan.d)
     q, k, v = (_ready(_pad_dim(x.to(dt), D)) for x in (Q, K, V))
     od = _out_dtype(dt, out_dtype)
-    out = _MaskedAttention.apply(q, k, v, tm, scale, od)
+    out = _MaskedAttention.apply(q, k, v, tm, scale, od, False, precise)
     if D != plan.d:
         out = out[..., :plan.d]
     return out[0] if plan.squeeze_batch else out
@@ -555,7 +607,7 @@ def _block_mask_tiles(block_mask, B, Hq, Hkv, L, S, element_head="kv") -> bmap.T
 def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    score_mod: Optional[Callable] = None, block_mask=None, scale=None,
                    enable_gqa: bool = False, return_lse: bool = False,
-                   out_dtype: Optional[torch.dtype] = None, *,
+                   out_dtype: Optional[torch.dtype] = None, *, precision: Optional[str] = None,
                    _element_head: str = "kv") -> torch.Tensor:
     """Block-sparse softmax attention over a ``BlockMask`` (attention.py:456-692).
 
@@ -571,7 +623,8 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     Same checks and exception types as the reference (AssertionError for shape
     mismatches, NotImplementedError for ``return_lse``).  ``score_mod`` has no
     kernel here and raises NotImplementedError, as does a value head dimension
-    different from the query's.
+    different from the query's.  ``precision`` as for masked_attention_via_map
+    (None selects float32 arithmetic for a ``scale`` above 1/sqrt(E)).
     """
     if return_lse:
         raise NotImplementedError("return_lse is not supported yet")
@@ -604,6 +657,7 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     s = 1.0 / math.sqrt(E) if scale is None else float(scale)
     if not math.isfinite(s):
         raise ValueError(f"scale must be finite, got {s}")
+    precise = use_precise(precision, s, E)
     tm = _block_mask_tiles(block_mask, B, Hq, Hkv, L, S, _element_head)
     D = _kernel_dim(E)
     q = query.to(dt)
@@ -614,18 +668,18 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         q, s = q * 0, 1.0
     # [B, H, L, E] tensors are strided [B, L, H, E] views for the kernels
     q, k, v = (_ready(_pad_dim(x, D).transpose(1, 2)) for x in (q, key.to(dt), value.to(dt)))
-    out = _MaskedAttention.apply(q, k, v, tm, s, _out_dtype(dt, out_dtype), True)
+    out = _MaskedAttention.apply(q, k, v, tm, s, _out_dtype(dt, out_dtype), True, precise)
     out = out.transpose(1, 2)
     return out[..., :E] if D != E else out
 
 
 def flex_attention_slow(query, key, value, score_mod=None, block_mask=None, scale=None,
-                        enable_gqa=False, return_lse=False, out_dtype=None):
+                        enable_gqa=False, return_lse=False, out_dtype=None, precision=None):
     """The reference's materialised-mask variant (attention.py:695-820) on the
     same kernels.  As there: Hq != Hkv is accepted without ``enable_gqa``,
     ``return_lse`` is ignored, and partial-tile elements are evaluated with the
     query head (``materialize_mask``).  A row with no allowed key is zero here;
     the reference's softmax over an all -inf row gives NaN."""
     return flex_attention(query, key, value, score_mod=score_mod, block_mask=block_mask,
-                          scale=scale, enable_gqa=True, out_dtype=out_dtype,
+                          scale=scale, enable_gqa=True, out_dtype=out_dtype, precision=precision,
                           _element_head="query")

@@ -177,10 +177,10 @@ static void launch_pre_16(const KArgs& a, hipStream_t st) {
 hipError_t launch_bwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid, int kv_grid,
                            hipStream_t st);
 
-hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,
+hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, bool simt, int stage, int q_grid,
                             int kv_grid, hipStream_t st) {
   const bool of32 = (o_dtype == MATTN_F32);
-  if (dtype == MATTN_F32 || D > 128) return launch_bwd_simt(a, D, dtype, o_dtype, stage, q_grid, kv_grid, st);
+  if (simt) return launch_bwd_simt(a, D, dtype, o_dtype, stage, q_grid, kv_grid, st);
   if (stage == MATTN_BWD_DKDV) return launch_dkdv(a, D, dtype, kv_grid, st);
   if (stage == MATTN_BWD_DQ) return launch_dq(a, D, dtype, q_grid, st);
   if (dtype == MATTN_BF16) {

@@ -10,8 +10,8 @@
 #include "common.hpp"
 
 namespace mattn {
-hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st);
-hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, int stage, int q_grid,
+hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, bool simt, int grid, hipStream_t st);
+hipError_t launch_bwd_stage(const KArgs& a, int D, int dtype, int o_dtype, bool simt, int stage, int q_grid,
                             int kv_grid, hipStream_t st);
 }  // namespace mattn
 
@@ -19,7 +19,7 @@ using namespace mattn;
 
 namespace {
 
-constexpr int kAbiVersion = 7;
+constexpr int kAbiVersion = 8;
 
 int elem_size(int dt) { return dt == MATTN_F32 ? 4 : 2; }
 
@@ -35,9 +35,11 @@ bool strides_ok(const int64_t s[3], int esz) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// problems served by the SIMT kernels, which need no residual and no
-// backward workspace beyond delta
-bool simt_path(const mattn_problem* p) { return p->dtype == MATTN_F32 || p->D > 128; }
+// problems served by the SIMT kernels (float32 arithmetic), which need no
+// residual and no backward workspace beyond one float per query row
+bool simt_path(const mattn_problem* p) {
+  return p->dtype == MATTN_F32 || p->D > 128 || (p->flags & MATTN_PRECISE);
+}
 
 // the backward keeps dS (MATTN_BWD_DS on the MFMA path)
 bool ds_path(const mattn_problem* p) { return (p->flags & MATTN_BWD_DS) && !simt_path(p); }
@@ -51,13 +53,18 @@ size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
 // [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
 // scale, and each V tile's max |V|.
+// MATTN_PRECISE on the SIMT kernels: the rounding error of each row's lse
+// (float32, [B, Hq, Lq]), which the backward adds back.
 struct FwdWs {
-  size_t vh, qh, vsc, vmax, qsc, total;
+  size_t vh, qh, vsc, vmax, qsc, lse_lo, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
   FwdWs w{};
-  if (simt_path(p)) return w;
+  if (simt_path(p)) {
+    if (p->flags & MATTN_PRECISE) w.total = align256((size_t)p->B * p->Hq * p->Lq * sizeof(float));
+    return w;
+  }
   const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
   const size_t qtiles = (size_t)p->B * p->Hq * cdiv(p->Lq, MATTN_TILE_Q);
   w.vh = 0;
@@ -130,6 +137,7 @@ KArgs make_args(const mattn_problem* p, const mattn_blockmap* bm) {
   a.q_order = bm->q_order;
   a.kv_order = bm->kv_order;
   a.kv_desc = bm->kv_desc;
+  a.precise = (p->flags & MATTN_PRECISE) ? 1 : 0;
   return a;
 }
 
@@ -151,7 +159,9 @@ const char* mattn_strerror(int status) {
     case MATTN_ERR_LAUNCH: return "kernel launch failed";
     case MATTN_ERR_TOO_LARGE: return "problem exceeds 32-bit index ranges";
     case MATTN_ERR_SCRATCH: return "backward workspace exceeds the library's static scratch (MATTN_SCRATCH_BYTES; clear MATTN_BWD_DS)";
-    case MATTN_ERR_DEVICE: return "the HIP runtime could not resolve the device or its scratch";
+    case MATTN_ERR_DEVICE: return "the HIP runtime could not resolve the device or its scratch, or the stream belongs to another device";
+    case MATTN_ERR_WORKSPACE: return "workspace smaller than mattn_bwd_workspace_bytes(p, bm)";
+    case MATTN_ERR_RESIDUAL: return "the backward needs the float16 Q copy: run the forward with MATTN_FWD_FOR_BWD and pass that flag to the backward";
     default: return "unknown status";
   }
 }
@@ -165,7 +175,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite
-  if (p->flags & ~(MATTN_FWD_FOR_BWD | MATTN_BWD_DS)) return MATTN_ERR_SHAPE;
+  if (p->flags & ~(MATTN_FWD_FOR_BWD | MATTN_BWD_DS | MATTN_PRECISE)) return MATTN_ERR_SHAPE;
   const int es = elem_size(p->dtype), eo = elem_size(p->o_dtype);
   if (!strides_ok(p->q_stride, es) || !strides_ok(p->k_stride, es) || !strides_ok(p->v_stride, es) ||
       !strides_ok(p->dq_stride, es) || !strides_ok(p->dk_stride, es) ||
@@ -231,26 +241,31 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
   a.out = o;
   a.lse = lse;
   char* ws = (char*)workspace;
-  if (w.total > 0) {
+  if (w.total > 0 && simt_path(p)) {
+    a.lse_lo = (float*)(ws + w.lse_lo);
+  } else if (w.total > 0) {
     a.vh = (uint16_t*)(ws + w.vh);
     a.vsc = (float*)(ws + w.vsc);
     a.vmax = (float*)(ws + w.vmax);
     a.qsc = (float*)(ws + w.qsc);
     a.qh = (p->flags & MATTN_FWD_FOR_BWD) ? (uint16_t*)(ws + w.qh) : nullptr;
   }
-  hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, bm->n_q_order, (hipStream_t)stream);
+  hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, simt_path(p), bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
 }
 
 int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage, const void* q,
                     const void* k, const void* v, const void* o, const void* do_, const float* lse,
-                    const void* residual, void* workspace, void* dq, void* dk, void* dv, void* stream) {
+                    const void* residual, void* workspace, size_t workspace_bytes, void* dq, void* dk,
+                    void* dv, void* stream) {
   int rc = mattn_validate(p, bm);
   if (rc != MATTN_OK) return rc;
   if (!bm) return MATTN_ERR_NULL;
   if (stage != MATTN_BWD_PRE && stage != MATTN_BWD_DKDV && stage != MATTN_BWD_DQ) return MATTN_ERR_SHAPE;
   if (!q || !k || !v || !o || !do_ || !lse || !workspace || !dq || !dk || !dv) return MATTN_ERR_NULL;
-  if (!simt_path(p) && !residual) return MATTN_ERR_NULL;
+  if (workspace_bytes < mattn_bwd_workspace_bytes(p, bm)) return MATTN_ERR_WORKSPACE;
+  if (!simt_path(p) && !(p->flags & MATTN_FWD_FOR_BWD)) return MATTN_ERR_RESIDUAL;
+  if (mattn_fwd_workspace_bytes(p) > 0 && !residual) return MATTN_ERR_NULL;
   if (ds_path(p) && bm->nnz > 0 && !bm->col_row) return MATTN_ERR_NULL;
   if (!simt_path(p) && stage == MATTN_BWD_DKDV && !bm->kv_desc) return MATTN_ERR_NULL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(do_) ||
@@ -270,7 +285,9 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
-  if (!simt_path(p)) {
+  if (simt_path(p) && (p->flags & MATTN_PRECISE)) {
+    a.lse_lo = (float*)((const char*)residual + fwd_ws_layout(p).lse_lo);
+  } else if (!simt_path(p)) {
     a.lsf = (float*)(ws + w.lsf);
     a.doh = (uint16_t*)(ws + w.doh);
     a.kh = (uint16_t*)(ws + w.kh);
@@ -291,17 +308,17 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
       a.ds_nnz = bm->nnz;
     }
   }
-  hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, stage, bm->n_q_order,
+  hipError_t e = launch_bwd_stage(a, p->D, p->dtype, p->o_dtype, simt_path(p), stage, bm->n_q_order,
                                   bm->n_kv_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
 }
 
 int mattn_bwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, const void* k,
               const void* v, const void* o, const void* do_, const float* lse, const void* residual,
-              void* workspace, void* dq, void* dk, void* dv, void* stream) {
+              void* workspace, size_t workspace_bytes, void* dq, void* dk, void* dv, void* stream) {
   for (int stage = MATTN_BWD_PRE; stage <= MATTN_BWD_DQ; ++stage) {
-    const int rc = mattn_bwd_stage(p, bm, stage, q, k, v, o, do_, lse, residual, workspace, dq, dk, dv,
-                                   stream);
+    const int rc = mattn_bwd_stage(p, bm, stage, q, k, v, o, do_, lse, residual, workspace, workspace_bytes,
+                                   dq, dk, dv, stream);
     if (rc != MATTN_OK) return rc;
   }
   return MATTN_OK;
@@ -343,9 +360,13 @@ int mattn_bwd_noalloc(const mattn_problem* p, const mattn_blockmap* bm, const vo
   if (need > (size_t)MATTN_SCRATCH_BYTES) return MATTN_ERR_SCRATCH;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MATTN_ERR_DEVICE;
+  if (stream) {  // the scratch is the current device's: the stream must run there
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev) return MATTN_ERR_DEVICE;
+  }
   void* ws = device_scratch(dev);
   if (!ws) return MATTN_ERR_DEVICE;
-  return mattn_bwd(p, bm, q, k, v, o, do_, lse, residual, ws, dq, dk, dv, stream);
+  return mattn_bwd(p, bm, q, k, v, o, do_, lse, residual, ws, (size_t)MATTN_SCRATCH_BYTES, dq, dk, dv, stream);
 }
 
 }  // extern "C"

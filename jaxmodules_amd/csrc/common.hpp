@@ -95,6 +95,8 @@ struct KArgs {
   const int* col_row;
   int ds_nnz;
   const int* kv_desc;  // per dK/dV launch slot: { item, g, e, e_end, n_sub, qt, mask, row }
+  int precise;         // MATTN_PRECISE: the SIMT kernels form the scores as compensated dot products
+  float* lse_lo;       // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq], (m + log2 l) - lse
 };
 
 // dS storage slot base of (b, h): the map's entries are shared by the (b, h)

@@ -369,9 +369,9 @@ static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStr
 
 hipError_t launch_fwd_simt(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st);
 
-hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, int grid, hipStream_t st) {
+hipError_t launch_fwd(const KArgs& a, int D, int dtype, int o_dtype, bool simt, int grid, hipStream_t st) {
   const bool of32 = (o_dtype == MATTN_F32);
-  if (dtype == MATTN_F32 || D > 128) return launch_fwd_simt(a, D, dtype, o_dtype, grid, st);
+  if (simt) return launch_fwd_simt(a, D, dtype, o_dtype, grid, st);
   if (dtype == MATTN_BF16)
     return D == 64 ? launch_fwd_mfma<64, bf16_tag>(a, grid, of32, st)
                    : launch_fwd_mfma<128, bf16_tag>(a, grid, of32, st);

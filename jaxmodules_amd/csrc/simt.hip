@@ -4,10 +4,16 @@
 //     dimensions 64, 128 and 256;
 //   * 16-bit inputs at head dimension 256 (any d in (128, 256], zero-padded by
 //     the host), which the MFMA kernels' register and LDS tiling does not hold.
+//   * 16-bit inputs at D = 64 and 128 under MATTN_PRECISE (callers whose
+//     kernels are too sharp for float16 operands).
 // Same maths and tile walk as the MFMA path (/root/reference/jaxmodules/
 // attention.py:52-105 forward, :266-342 backward): per 32-key (or 32-query)
 // sub-block an online softmax, P = exp2(scale_log2 S - lse) in the backward,
 // dS = P (dP - delta), dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO.
+// dP - delta is formed as dO . (V_k - O) (delta = dO . O): where one key
+// dominates a row, V_k - O is small and exact to float32 rounding, while
+// dO . V_k and dO . O are two large dot products whose roundings (2^-24 of
+// |dO| |V|) would be all that is left of their difference.
 // TPR threads share a row (query or key), each holding D / TPR head dims; a
 // workgroup of 512 threads owns 512 / TPR rows of a 128-row map tile, so a
 // tile takes 128 TPR / 512 workgroups (one for TPR = 4, two for TPR = 8).
@@ -58,6 +64,51 @@ __device__ __forceinline__ float row_sum(float x) {
 #pragma unroll
   for (int o = 1; o < TPR; o <<= 1) x += __shfl_xor(x, o);
   return x;
+}
+
+// a + b = s + e exactly (Knuth's TwoSum)
+__device__ __forceinline__ void two_sum(float a, float b, float& s, float& e) {
+  s = a + b;
+  const float z = s - a;
+  e = (a - (s - z)) + (b - z);
+}
+
+// Score of a row pair, q . y over the TPR lanes of the row (DP elements each),
+// as hi + lo.  With `comp` (MATTN_PRECISE) it is the compensated dot product
+// Dot2 of Ogita, Rump and Oishi (SIAM J. Sci. Comput. 26(6), 2005): every
+// product's rounding error (an FMA gives it exactly) and every addition's
+// (TwoSum) are summed apart, so hi + lo carries the dot product to about twice
+// float32's precision.  The scores of a kernel sharper than 1/sqrt(d) reach
+// tens of units (base 2 after scaling), where float32's 2^-24 relative
+// rounding alone moves the weights exp2(S - lse) by 1e-5; otherwise lo = 0.
+template <int DP, int TPR>
+__device__ __forceinline__ void score(const float* qv, const float* y, bool comp, float& hi, float& lo) {
+  if (!comp) {
+    float p = 0.f;
+#pragma unroll
+    for (int i = 0; i < DP; ++i) p = fmaf(qv[i], y[i], p);
+    hi = row_sum<TPR>(p);
+    lo = 0.f;
+    return;
+  }
+  float s = 0.f, c = 0.f;
+#pragma unroll
+  for (int i = 0; i < DP; ++i) {
+    const float pr = qv[i] * y[i];
+    const float ep = fmaf(qv[i], y[i], -pr);
+    float e;
+    two_sum(s, pr, s, e);
+    c += ep + e;
+  }
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) {
+    const float so = __shfl_xor(s, o), co = __shfl_xor(c, o);
+    float e;
+    two_sum(s, so, s, e);
+    c += co + e;
+  }
+  hi = s;
+  lo = c;
 }
 
 // rows [r0, r0 + SB) of a [rows, D] tensor slice (row stride rs) as floats in
@@ -113,14 +164,14 @@ void fwd_simt(KArgs a) {
       uint32_t bits = 0xffffffffu;
       if (mask >= 0)
         bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
-      float sc[SB];
+      float sc[SB], sl[SB];  // scores s (scaled: s * scale_log2 = sc + sl)
       float mx = NEG_INF;
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        float p = 0.f;
-#pragma unroll
-        for (int i = 0; i < DP; ++i) p = fmaf(qv[i], Ks[j * D + part * DP + i], p);
-        float x = row_sum<TPR>(p) * a.scale_log2;
+        float hi, lo;
+        score<DP, TPR>(qv, Ks + j * D + part * DP, a.precise, hi, lo);
+        float x = hi * a.scale_log2;
+        sl[j] = fmaf(hi, a.scale_log2, -x) + lo * a.scale_log2;  // rounding of x, and the low part
         if (!((bits >> j) & 1u)) x = NEG_INF;
         sc[j] = x;
         mx = fmaxf(mx, x);
@@ -134,7 +185,7 @@ void fwd_simt(KArgs a) {
       for (int i = 0; i < DP; ++i) ov[i] *= alpha;
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        const float p = exp2f(sc[j] - mu);
+        const float p = exp2f((sc[j] - mu) + sl[j]);  // -inf + finite: 0 for masked keys
         l += p;
 #pragma unroll
         for (int i = 0; i < DP; ++i) ov[i] = fmaf(p, Vs[j * D + part * DP + i], ov[i]);
@@ -143,39 +194,15 @@ void fwd_simt(KArgs a) {
   }
   if (q >= a.Lq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (part == 0) a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m + log2f(l) : NEG_INF;
+  if (part == 0) {
+    float lse = NEG_INF, lo = 0.f;
+    if (l > 0.f) two_sum(m, log2f(l), lse, lo);  // lse + lo = m + log2 l exactly
+    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = lse;
+    if (a.precise) a.lse_lo[((int64_t)b * a.Hq + h) * a.Lq + q] = lo;
+  }
   const int64_t oo = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * DP;
 #pragma unroll
   for (int i = 0; i < DP; ++i) Mem<OT>::put(a.out, oo + i, ov[i] * inv);
-}
-
-// delta = rowsum(dO * O), O and dO in OT: 16 lanes per (b, q, h) row, 16 rows
-// per workgroup of 256 threads
-template <int D, class OT>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
-void bwd_delta_simt(KArgs a) {
-  constexpr int PER = D / 16;
-  const uint32_t nrows = (uint32_t)a.B * a.Lq * a.Hq;  // < 2^31 (checked by the C ABI)
-  const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  if (row >= nrows) return;  // uniform per 16-lane group; no barrier below
-  const int h = (int)(row % (uint32_t)a.Hq);
-  const uint32_t bq = row / (uint32_t)a.Hq;
-  const int q = (int)(bq % (uint32_t)a.Lq), b = (int)(bq / (uint32_t)a.Lq);
-  const int64_t oo = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + sub * PER;
-  const int64_t go = (int64_t)b * a.dos[0] + (int64_t)q * a.dos[1] + (int64_t)h * a.dos[2] + sub * PER;
-  float acc = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; i += 4) {
-    float x[4], g[4];
-    Mem<OT>::get4(a.o, oo + i, x);
-    Mem<OT>::get4(a.dO, go + i, g);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc = fmaf(x[j], g[j], acc);
-  }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, 16);
-  if (sub == 0) a.delta[((int64_t)b * a.Hq + h) * a.Lq + q] = acc;
 }
 
 template <int D, int TPR, class IT, class OT>
@@ -198,17 +225,19 @@ void bwd_dq_simt(KArgs a) {
   const int q = qt * TILE + row;
   const int qc = min(q, a.Lq - 1);
 
-  float qv[DP], gv[DP], dq[DP];
+  float qv[DP], gv[DP], ov[DP], dq[DP];
   const int64_t qo = (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] + (int64_t)h * a.qs[2] + part * DP;
   const int64_t go = (int64_t)b * a.dos[0] + (int64_t)qc * a.dos[1] + (int64_t)h * a.dos[2] + part * DP;
+  const int64_t oo = (int64_t)b * a.os[0] + (int64_t)qc * a.os[1] + (int64_t)h * a.os[2] + part * DP;
 #pragma unroll
   for (int i = 0; i < DP; i += 4) {
     Mem<IT>::get4(a.q, qo + i, qv + i);
     Mem<OT>::get4(a.dO, go + i, gv + i);
+    Mem<OT>::get4(a.o, oo + i, ov + i);
     dq[i] = dq[i + 1] = dq[i + 2] = dq[i + 3] = 0.f;
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
-  const float lse = a.lse[rs], dl = a.delta[rs];
+  const float lse = a.lse[rs], lse_lo = a.precise ? a.lse_lo[rs] : 0.f;
   const char* kb = (const char*)a.k + ES * ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2]);
   const char* vb = (const char*)a.v + ES * ((int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2]);
 
@@ -225,26 +254,24 @@ void bwd_dq_simt(KArgs a) {
       if (mask >= 0)
         bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
       for (int j = 0; j < SB; ++j) {
-        float s = 0.f, g = 0.f;
+        float g = 0.f;
 #pragma unroll
-        for (int i = 0; i < DP; ++i) {
-          s = fmaf(qv[i], Ks[j * D + part * DP + i], s);
-          g = fmaf(gv[i], Vs[j * D + part * DP + i], g);
-        }
-        s = row_sum<TPR>(s);
+        for (int i = 0; i < DP; ++i) g = fmaf(gv[i], Vs[j * D + part * DP + i] - ov[i], g);  // dP - delta
         g = row_sum<TPR>(g);
-        float p = exp2f(s * a.scale_log2 - lse);
+        float hi, lo;
+        score<DP, TPR>(qv, Ks + j * D + part * DP, a.precise, hi, lo);
+        float p = exp2f(fmaf(hi, a.scale_log2, -lse) + fmaf(lo, a.scale_log2, -lse_lo));
         if (!((bits >> j) & 1u)) p = 0.f;
-        const float ds = p * (g - dl);
+        const float ds = p * g;
 #pragma unroll
         for (int i = 0; i < DP; ++i) dq[i] = fmaf(ds, Ks[j * D + part * DP + i], dq[i]);
       }
     }
   }
   if (q >= a.Lq) return;
-  const int64_t oo = (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2] + part * DP;
+  const int64_t qo2 = (int64_t)b * a.dqs[0] + (int64_t)q * a.dqs[1] + (int64_t)h * a.dqs[2] + part * DP;
 #pragma unroll
-  for (int i = 0; i < DP; ++i) Mem<IT>::put(a.dq, oo + i, dq[i] * a.scale);
+  for (int i = 0; i < DP; ++i) Mem<IT>::put(a.dq, qo2 + i, dq[i] * a.scale);
 }
 
 template <int D, int TPR, class IT, class OT>
@@ -255,7 +282,8 @@ void bwd_dkdv_simt(KArgs a) {
   constexpr int EO = std::is_same<OT, float>::value ? 4 : 2;
   __shared__ __attribute__((aligned(16))) float Qs[SB * D];
   __shared__ __attribute__((aligned(16))) float Gs[SB * D];
-  __shared__ float Ls[SB], Dl[SB];
+  __shared__ __attribute__((aligned(16))) float Os[SB * D];
+  __shared__ float Ls[SB], Llo[SB];
 
   const int item = a.kv_order[blockIdx.x / SPLIT];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
@@ -283,6 +311,7 @@ void bwd_dkdv_simt(KArgs a) {
     const int e0 = a.col_ptr[mc], e1 = a.col_ptr[mc + 1];
     const char* qb = (const char*)a.q + ES * ((int64_t)b * a.qs[0] + (int64_t)h * a.qs[2]);
     const char* gb = (const char*)a.dO + EO * ((int64_t)b * a.dos[0] + (int64_t)h * a.dos[2]);
+    const char* ob = (const char*)a.o + EO * ((int64_t)b * a.os[0] + (int64_t)h * a.os[2]);
     for (int e = e0; e < e1; ++e) {
       const int qt = a.col_ent[2 * e], mask = a.col_ent[2 * e + 1];
       for (int sb = 0; sb < TILE / SB; ++sb) {
@@ -291,28 +320,27 @@ void bwd_dkdv_simt(KArgs a) {
         __syncthreads();
         stage_rows<D, IT>(Qs, qb, a.qs[1], q0, a.Lq);
         stage_rows<D, OT>(Gs, gb, a.dos[1], q0, a.Lq);
-        if (tid < 2 * SB) {
-          const int qq = min(q0 + (tid & (SB - 1)), a.Lq - 1);
-          const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qq;
-          if (tid < SB) Ls[tid] = a.lse[rs];
-          else Dl[tid - SB] = a.delta[rs];
+        stage_rows<D, OT>(Os, ob, a.os[1], q0, a.Lq);
+        if (tid < SB) {
+          const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + min(q0 + tid, a.Lq - 1);
+          Ls[tid] = a.lse[rs];
+          Llo[tid] = a.precise ? a.lse_lo[rs] : 0.f;
         }
         __syncthreads();
         uint32_t bits = 0xffffffffu;
         if (mask >= 0)
           bits = (uint32_t)(a.col_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
         for (int j = 0; j < SB; ++j) {
-          float s = 0.f, gd = 0.f;
+          float gd = 0.f;
 #pragma unroll
-          for (int i = 0; i < DP; ++i) {
-            s = fmaf(kv[i], Qs[j * D + part * DP + i], s);
-            gd = fmaf(vv[i], Gs[j * D + part * DP + i], gd);
-          }
-          s = row_sum<TPR>(s);
+          for (int i = 0; i < DP; ++i)
+            gd = fmaf(vv[i] - Os[j * D + part * DP + i], Gs[j * D + part * DP + i], gd);  // dP - delta
           gd = row_sum<TPR>(gd);
-          float p = exp2f(s * a.scale_log2 - Ls[j]);
+          float hi, lo;
+          score<DP, TPR>(kv, Qs + j * D + part * DP, a.precise, hi, lo);
+          float p = exp2f(fmaf(hi, a.scale_log2, -Ls[j]) + fmaf(lo, a.scale_log2, -Llo[j]));
           if (!((bits >> j) & 1u)) p = 0.f;
-          const float ds = p * (gd - Dl[j]);
+          const float ds = p * gd;
 #pragma unroll
           for (int i = 0; i < DP; ++i) {
             dv[i] = fmaf(p, Gs[j * D + part * DP + i], dv[i]);
@@ -341,8 +369,7 @@ struct Simt {
   }
   static void bwd(const KArgs& a, int stage, int q_grid, int kv_grid, hipStream_t st) {
     if (stage == MATTN_BWD_PRE) {
-      const int64_t rows = (int64_t)a.B * a.Lq * a.Hq;
-      hipLaunchKernelGGL((bwd_delta_simt<D, OT>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, a);
+      // nothing: the SIMT kernels form dP - delta per pair from O
     } else if (stage == MATTN_BWD_DKDV) {
       hipLaunchKernelGGL((bwd_dkdv_simt<D, TPR, IT, OT>), dim3(kv_grid * SPLIT), dim3(512), 0, st, a);
     } else {
@@ -351,9 +378,15 @@ struct Simt {
   }
 };
 
-// f(Simt<...>{}) for the problem's combination: float32 at D = 64, 128 (4
-// threads per row) or 256 (8); 16-bit inputs at D = 256 with a float32 or
+// f(Simt<...>{}) for the problem's combination: D = 64, 128 (4 threads per
+// row) or 256 (8); float32 inputs, or 16-bit inputs with a float32 or
 // same-dtype output
+template <class Tag, class F>
+void dispatch16(int D, bool of32, F&& f) {
+  if (D == 64) { if (of32) f(Simt<64, 4, Tag, float>{}); else f(Simt<64, 4, Tag, Tag>{}); }
+  else if (D == 128) { if (of32) f(Simt<128, 4, Tag, float>{}); else f(Simt<128, 4, Tag, Tag>{}); }
+  else { if (of32) f(Simt<256, 8, Tag, float>{}); else f(Simt<256, 8, Tag, Tag>{}); }
+}
 template <class F>
 hipError_t dispatch(int D, int dtype, int o_dtype, F&& f) {
   const bool of32 = o_dtype == MATTN_F32;
@@ -362,11 +395,9 @@ hipError_t dispatch(int D, int dtype, int o_dtype, F&& f) {
     else if (D == 128) f(Simt<128, 4, float, float>{});
     else f(Simt<256, 8, float, float>{});
   } else if (dtype == MATTN_BF16) {
-    if (of32) f(Simt<256, 8, bf16_tag, float>{});
-    else f(Simt<256, 8, bf16_tag, bf16_tag>{});
+    dispatch16<bf16_tag>(D, of32, f);
   } else {
-    if (of32) f(Simt<256, 8, f16_tag, float>{});
-    else f(Simt<256, 8, f16_tag, f16_tag>{});
+    dispatch16<f16_tag>(D, of32, f);
   }
   return hipGetLastError();
 }

@@ -160,7 +160,8 @@ def test_flags_validated(lib):
     assert _validate(lib, _problem(flags=_lib.MATTN_FWD_FOR_BWD)) == 0
     assert _validate(lib, _problem(flags=_lib.MATTN_BWD_DS)) == 0
     assert _validate(lib, _problem(flags=_lib.MATTN_FWD_FOR_BWD | _lib.MATTN_BWD_DS)) == 0
-    assert _validate(lib, _problem(flags=4)) == -2
+    assert _validate(lib, _problem(flags=_lib.MATTN_PRECISE)) == 0
+    assert _validate(lib, _problem(flags=8)) == -2
 
 
 def test_bwd_workspace_bytes_with_stored_ds(lib):
@@ -190,9 +191,10 @@ def test_bwd_workspace_bytes_with_stored_ds(lib):
     # the stored dS needs the column entries' row indices
     bm.nqt = 3
     bm.col_row = None
-    args = [8] * 13
-    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), 1, *args[:3], 8, 8, 8, 256, 256, 8, 8, 8,
-                               None) == -1
+    p.flags |= _lib.MATTN_FWD_FOR_BWD
+    need = lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm))
+    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), 1, 8, 8, 8, 8, 8, 8, 256, 256, need,
+                               8, 8, 8, None) == -1
 
 
 def test_dkdv_stage_needs_the_launch_descriptors(lib):
@@ -202,7 +204,8 @@ def test_dkdv_stage_needs_the_launch_descriptors(lib):
     p = _problem()
     bm = _lib.MattnBlockmap(map_b=1, map_h=1, nqt=3, nkt=3, n_masks=0, nnz=0, row_ptr=8, col_ptr=8,
                             q_order=8, kv_order=8, n_q_order=2 * 8 * 3, n_kv_order=2 * 2 * 3, kv_desc=None)
-    ptrs = [8, 8, 8, 8, 8, 8, 256, 256, 8, 8, 8]
+    p.flags = _lib.MATTN_FWD_FOR_BWD
+    ptrs = [8, 8, 8, 8, 8, 8, 256, 256, 1 << 30, 8, 8, 8]
     assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), _lib.BWD_DKDV, *ptrs, None) == -1
 
 
@@ -235,8 +238,37 @@ def test_entry_points_reject_before_launch(lib):
     p = _problem()
     rc = lib.mattn_fwd(ctypes.byref(p), None, None, None, None, None, None, None, None)
     assert rc == -1
-    rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 12))
+    rc = lib.mattn_bwd_stage(ctypes.byref(p), None, 5, *([None] * 8), 0, *([None] * 4))
     assert rc == -1
+
+
+def test_backward_checks_workspace_size_and_residual_flag(lib):
+    """ABI 8: the backward rejects a workspace smaller than
+    mattn_bwd_workspace_bytes (MATTN_ERR_WORKSPACE) and, on the MFMA path, a
+    problem without MATTN_FWD_FOR_BWD, whose residual holds no float16 Q copy
+    (MATTN_ERR_RESIDUAL), both before any launch.  MATTN_PRECISE problems run
+    on the SIMT kernels: no residual, a one-float-per-row workspace."""
+    p = _problem(flags=_lib.MATTN_FWD_FOR_BWD | _lib.MATTN_BWD_DS)
+    bm = _lib.MattnBlockmap(map_b=1, map_h=1, nqt=3, nkt=3, n_masks=0, nnz=4, row_ptr=8, col_ptr=8,
+                            row_ent=8, col_ent=8, q_order=8, kv_order=8, n_q_order=2 * 8 * 3,
+                            n_kv_order=2 * 2 * 3, col_row=8, kv_desc=8)
+    need = lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm))
+    ptrs = [8, 8, 8, 8, 8, 8, 256, 256]
+    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), 0, *ptrs, need - 1, 8, 8, 8, None) == -11
+    assert lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), *ptrs, need - 1, 8, 8, 8, None) == -11
+    p.flags = _lib.MATTN_BWD_DS
+    need = lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm))
+    assert lib.mattn_bwd_stage(ctypes.byref(p), ctypes.byref(bm), 0, *ptrs, need, 8, 8, 8, None) == -12
+    # float32 arithmetic for 16-bit inputs: SIMT path, no residual, no stored dS
+    p.flags = _lib.MATTN_PRECISE | _lib.MATTN_BWD_DS
+    assert lib.mattn_validate(ctypes.byref(p), ctypes.byref(bm)) == 0
+    rows = p.B * p.Hq * p.Lq           # the residual: each row's lse rounding error
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == (rows * 4 + 255) // 256 * 256
+    p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
+    assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == \
+        lib.mattn_workspace_bytes(ctypes.byref(p32))
+    p.flags = 8  # an undefined flag bit
+    assert lib.mattn_validate(ctypes.byref(p), None) == -2
 
 
 def test_library_missing_raises(monkeypatch, tmp_path):

@@ -15,7 +15,7 @@ import pytest
 
 from jaxmodules_amd.block_mask import BlockMask, create_block_mask
 from oracle import attention_oracle as ao
-from tests.helpers import assert_close
+from tests.helpers import Floor, Ref, assert_close, magnitudes
 
 torch = pytest.importorskip("torch")
 
@@ -99,11 +99,12 @@ def _oracle(q, k, v, allowed, scale, do=None):
     B, L, Hq, _ = Q.shape
     al = np.broadcast_to(allowed, (B, Hq, L, K.shape[1]))
     O, _ = ao.dense_forward(Q, K, V, al, scale=scale)
+    mags = magnitudes(Q, K, V, al, None if do is None else np.swapaxes(do, 1, 2), scale)
     g = None
     if do is not None:
-        g = tuple(np.swapaxes(x, 1, 2) for x in ao.dense_backward(Q, K, V, al, np.swapaxes(do, 1, 2),
-                                                                  scale=scale))
-    return np.swapaxes(O, 1, 2), g
+        g = tuple(Ref(np.swapaxes(x, 1, 2), np.swapaxes(m, 1, 2))
+                  for x, m in zip(ao.dense_backward(Q, K, V, al, np.swapaxes(do, 1, 2), scale=scale), mags[1:]))
+    return Ref(np.swapaxes(O, 1, 2), np.swapaxes(mags[0], 1, 2)), g
 
 
 def _inputs(shape_q, shape_kv, seed, dtype, scaled=True):
@@ -117,21 +118,31 @@ def _inputs(shape_q, shape_kv, seed, dtype, scaled=True):
 
 
 def _check(q, k, v, do, allowed, scale, dtype_name, grads=True, **kw):
+    """flex (or ``fn``) against the oracle; a default-path miss within the
+    float16 operands' bound (tests/helpers.py Floor) reruns the case at
+    precision "highest", which must meet the gate, and then xfails."""
     import jaxmodules_amd as jm
+    from jaxmodules_amd import attention as A
 
     fn = kw.pop("fn", jm.flex_attention)
+    precision = kw.pop("precision", None)
     qg, kg, vg = (x.clone().requires_grad_(grads) for x in (q, k, v))
-    o = fn(qg, kg, vg, scale=scale, **kw)
+    o = fn(qg, kg, vg, scale=scale, precision=precision, **kw)
     assert o.shape == q.shape and o.dtype == torch.float32
     qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
-    O, g = _oracle(qn, kn, vn, allowed, 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale,
-                   do.cpu().numpy() if grads else None)
-    assert_close(o.detach().cpu().numpy(), O, dtype_name, "O", "float32")
+    s = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    O, g = _oracle(qn, kn, vn, allowed, s, do.cpu().numpy() if grads else None)
+    fast = dtype_name != "float32" and not A.use_precise(precision, s, q.shape[-1])
+    floor = Floor() if fast else None
+    assert_close(o.detach().cpu().numpy(), O, dtype_name, "O", "float32", floor=floor)
     if grads:
         o.backward(do)
         for name, t, r in (("dQ", qg, g[0]), ("dK", kg, g[1]), ("dV", vg, g[2])):
             assert t.grad.shape == t.shape and t.grad.dtype == t.dtype
-            assert_close(t.grad.float().cpu().numpy(), r, dtype_name, name)
+            assert_close(t.grad.float().cpu().numpy(), r, dtype_name, name, floor=floor)
+    if floor is not None and floor.misses:
+        _check(q, k, v, do, allowed, scale, dtype_name, grads, fn=fn, precision="highest", **kw)
+        floor.finish()
     return o
 
 
@@ -245,13 +256,16 @@ def test_masked_attention_padded_head_dim(d):
 
     kw = dict(mask_fn=lambda h, q, k: (q - k) % 4 != 1, block_size=32)
     Q, K, V, dO = seeded_inputs(1, 96, 96, 4, 2, d, 9)
+    floor = Floor()
     for dt, name in ((torch.float32, "float32"), (torch.bfloat16, "bfloat16")):
         q, k, v = (torch.from_numpy(x).to("cuda", dt).requires_grad_() for x in (Q, K, V))
         o = jm.masked_attention_via_map(q, k, v, **kw)
         assert o.shape == (1, 96, 4, d)
         Qr, Kr, Vr = (x.detach().float().cpu().numpy() for x in (q, k, v))
         O, _, g, _ = oracle(Qr, Kr, Vr, dO, kw)
-        assert_close(o.detach().cpu().numpy(), O, name, f"d={d} {name} O", "float32")
+        fl = floor if name != "float32" and d <= 128 else None   # d > 128: float32 SIMT kernels
+        assert_close(o.detach().cpu().numpy(), O, name, f"d={d} {name} O", "float32", floor=fl)
         o.backward(torch.from_numpy(dO).cuda())
         for nm, t, r in (("dQ", q, g[0]), ("dK", k, g[1]), ("dV", v, g[2])):
-            assert_close(t.grad.float().cpu().numpy(), r, name, f"d={d} {name} {nm}")
+            assert_close(t.grad.float().cpu().numpy(), r, name, f"d={d} {name} {nm}", floor=fl)
+    floor.finish()

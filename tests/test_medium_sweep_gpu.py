@@ -9,7 +9,7 @@ the kernels' earlier operands.  Same gate as the small sweep (tests/helpers.py).
 import numpy as np
 import pytest
 
-from tests.helpers import assert_close, oracle, seeded_inputs
+from tests.helpers import Floor, assert_close, oracle, seeded_inputs
 
 torch = pytest.importorskip("torch")
 
@@ -48,26 +48,38 @@ def draw(seed):
     return dict(shape=(B, N, N, Hq, Hkv, d), kw=kw, dtype=dtype, fam=fam)
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 12])
-def test_medium_problem(seed):
+def run_medium(seed, precision=None):
+    """One draw against the oracle; a default-path miss within the float16
+    operands' bound (tests/helpers.py Floor) reruns it at precision
+    "highest", which must meet the gate, and then xfails."""
     import jaxmodules_amd as jm
 
     c = draw(seed)
     B, N, L, Hq, Hkv, d = c["shape"]
     print(f"[medium] seed={seed} {c['fam']} shape={c['shape']} dtype={c['dtype']} "
-          f"block={c['kw']['block_size']}", flush=True)
+          f"block={c['kw']['block_size']} precision={precision}", flush=True)
     Q, K, V, dO = seeded_inputs(B, N, L, Hq, Hkv, d, 9000 + seed)
     td = getattr(torch, c["dtype"])
     q, k, v = (torch.from_numpy(x).to("cuda", td).requires_grad_() for x in (Q, K, V))
-    o = jm.masked_attention_via_map(q, k, v, **c["kw"])
+    o = jm.masked_attention_via_map(q, k, v, precision=precision, **c["kw"])
     Qr, Kr, Vr = (x.detach().float().cpu().numpy() for x in (q, k, v))
     do_t = torch.from_numpy(dO).to("cuda", o.dtype)
     O_ref, _, g_ref, _ = oracle(Qr, Kr, Vr, do_t.float().cpu().numpy(), c["kw"])
-    assert_close(o.detach().float().cpu().numpy(), O_ref, c["dtype"], "O", str(o.dtype).replace("torch.", ""))
+    floor = Floor() if precision is None else None
+    assert_close(o.detach().float().cpu().numpy(), O_ref, c["dtype"], "O", str(o.dtype).replace("torch.", ""),
+                 floor=floor)
     o.backward(do_t)
     for name, t, r in (("dQ", q, g_ref[0]), ("dK", k, g_ref[1]), ("dV", v, g_ref[2])):
-        assert_close(t.grad.float().cpu().numpy(), r, c["dtype"], name)
+        assert_close(t.grad.float().cpu().numpy(), r, c["dtype"], name, floor=floor)
     torch.cuda.synchronize()
+    if floor is not None and floor.misses:
+        run_medium(seed, precision="highest")
+        floor.finish()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 12])
+def test_medium_problem(seed):
+    run_medium(seed)
 
 
 def test_draws_cover_every_family():

