@@ -391,11 +391,17 @@ def _aligned(t):
     return None if t is None else (t.data_ptr() + 255) & ~255
 
 
-# Whether the backward keeps dS (MATTN_BWD_DS): None = where it pays (16-bit
-# inputs at kernel head dim 128, dS within DS_MAX_BYTES), True = wherever the
-# kernels support it (16-bit inputs, head dim <= 128), False = never.
+# Whether the backward keeps dS (MATTN_BWD_DS): None = where it pays and fits
+# (16-bit inputs at kernel head dim 128, the dS workspace at most DS_MAX_BYTES),
+# True = wherever the kernels support it (16-bit inputs, head dim <= 128),
+# False = never.  The stored dS takes 2 bytes per pair of every present tile,
+# O(L^2 density) -- 2.2 GB at B=1 L=8192 H=32 causal, 8.7 GB at L=16384 --
+# where the recomputing backward needs O(L) workspace like the reference
+# (attention.py:233-237 keeps memory at O(block_size L)).  By default its extra
+# workspace is therefore bounded by DS_MAX_BYTES, 4 GiB (1.5% of an MI355X's
+# 288 GB); larger problems recompute dS in the dQ pass (4 D flop per pair).
 STORE_DS: Optional[bool] = None
-DS_MAX_BYTES = 16 << 30
+DS_MAX_BYTES = 4 << 30
 
 
 def bwd_flags(p, bm) -> int:

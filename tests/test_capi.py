@@ -291,3 +291,39 @@ def test_noalloc_rejects_before_any_device_call(lib):
     assert lib.mattn_bwd_noalloc(ctypes.byref(_problem(D=96)), None, *args) == -3
     small = _problem()
     assert lib.mattn_workspace_bytes(ctypes.byref(small)) <= _lib.SCRATCH_BYTES
+
+
+def _causal_map(B, L, H):
+    """A mattn_blockmap of a causal map broadcast over batch and heads (host
+    sizes only; the pointers are never dereferenced)."""
+    nt = -(-L // 128)
+    return _lib.MattnBlockmap(map_b=1, map_h=1, nqt=nt, nkt=nt, n_masks=1, nnz=nt * (nt + 1) // 2,
+                              row_ptr=8, col_ptr=8, row_ent=8, col_ent=8, row_bits=8, col_bits=8,
+                              q_order=8, kv_order=8, n_q_order=B * H * nt, n_kv_order=B * H * nt,
+                              col_row=8, kv_desc=8)
+
+
+def test_stored_ds_default_stays_within_its_cap(lib):
+    """The default backward keeps dS only while its extra workspace is at most
+    attention.DS_MAX_BYTES (4 GiB): B=1 L=8192 H=32 causal (2.2 GB) keeps it,
+    L=16384 (8.7 GB, O(L^2)) recomputes dS instead, with the O(L) workspace."""
+    from jaxmodules_amd import attention as A
+
+    assert A.STORE_DS is None and A.DS_MAX_BYTES == 4 << 30
+    for L, keeps in ((8192, True), (16384, False)):
+        p = _problem(B=1, Lq=L, Lk=L, Hq=32, Hkv=32, flags=_lib.MATTN_FWD_FOR_BWD)
+        for name in ("q", "k", "v", "dq", "dk", "dv"):
+            setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(L * 32 * 128, 32 * 128, 128))
+        for name in ("o", "do"):
+            setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(L * 32 * 128, 32 * 128, 128))
+        bm = _causal_map(1, L, 32)
+        flags = A.bwd_flags(p, bm)
+        assert bool(flags & _lib.MATTN_BWD_DS) == keeps, L
+        p.flags = flags
+        extra = lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) - \
+            lib.mattn_workspace_bytes(ctypes.byref(p))
+        assert extra <= A.DS_MAX_BYTES
+        if not keeps:
+            # the recomputing backward's workspace: O(L) per head (delta, shifted lse,
+            # the float16 dO and K copies, per-tile scales)
+            assert lib.mattn_workspace_bytes(ctypes.byref(p)) < 2 * L * 32 * 128 * 2 + (8 << 20)
