@@ -364,7 +364,9 @@ def mattn_forward(q, k, v, tm: bmap.TileMap, scale: float, out_dtype=torch.float
     if heads_major:
         o = torch.empty((B, Hq, N, d), dtype=out_dtype, device=q.device).transpose(1, 2)
     else:
-        o = torch.empty((B, N, Hq, d), dtype=out_dtype, device=q.device)
+        # q's memory order when q is a dense view (the residue rewrite's strided
+        # [P, L / P, H, d] view), so that O lands in the caller's order
+        o = torch.empty_like(q, dtype=out_dtype)
     lse = torch.empty((B, Hq, N), dtype=torch.float32, device=q.device)
     _check_map(tm, q, k)
     p = _problem(q, k, v, o, scale)
@@ -509,6 +511,54 @@ def use_precise(precision: Optional[str], scale: float, d: int) -> bool:
     return precision == "highest"
 
 
+def _residue_rewrite(Q, K, V, is_causal, kernel_fn, mask_fn, block_size, window_size, out_dtype,
+                     precision):
+    """The strided mask of the reference's benchmark, k % P == q % P (and
+    k <= q: check_attn.py:9-32), as P independent problems of length L / P.
+
+    Position q = s P + r is step s of residue class r, and a query attends only
+    keys of its own class, so the [1, L, H, d] tensors viewed as [P, L / P, H, d]
+    (batch = class, stride H d; sequence = step, stride P H d: views, no copy)
+    carry the same attention under a causal mask (or none).  The tiles of the
+    original problem each hold one allowed key per row in 128 (every present
+    tile partial); the rewritten problem's are dense causal.  Applies to a
+    closed-form mask (jaxmodules_amd.masks) that is a residue class, with or
+    without causal, and nothing else, no window_size, B = 1 (or 3-D inputs),
+    equal query and key lengths divisible by P; None otherwise."""
+    from . import masks
+
+    spec = masks.spec_of(mask_fn) if mask_fn is not None else None
+    if (spec is None or is_causal or window_size is not None or spec.period is None or spec.period <= 1
+            or spec.win_left is not None or spec.win_right is not None or spec.doc_q is not None
+            or spec.table is not None):
+        return None
+    three = Q.dim() == 3
+    q4, k4, v4 = (x[None] if three else x for x in (Q, K, V))
+    if q4.dim() != 4 or k4.dim() != 4 or v4.dim() != 4:
+        return None
+    B, N, Hq, d = q4.shape
+    L, P = k4.shape[1], spec.period
+    if B != 1 or N != L or L % P or v4.shape[1] != L:
+        return None
+    # the reference's checks (and exception types) on the original call
+    bmap.make_plan(tuple(Q.shape), tuple(K.shape), tuple(V.shape), mask_fn=mask_fn,
+                   block_size=block_size, window_size=window_size)
+    out = masked_attention_via_map(*(residue_view(x, P) for x in (q4, k4, v4)), is_causal=spec.causal,
+                                   kernel_fn=kernel_fn, out_dtype=out_dtype, precision=precision)
+    out = residue_unview(out)
+    return out[0] if three else out
+
+
+def residue_view(x: torch.Tensor, P: int) -> torch.Tensor:
+    """[1, L, H, d] -> the [P, L / P, H, d] view whose [r, s] is position s P + r."""
+    return x[0].reshape(x.shape[1] // P, P, x.shape[2], x.shape[3]).transpose(0, 1)
+
+
+def residue_unview(y: torch.Tensor) -> torch.Tensor:
+    """The inverse of residue_view: [P, n, H, d] -> [1, n P, H, d]."""
+    return y.transpose(0, 1).reshape(1, y.shape[0] * y.shape[1], y.shape[2], y.shape[3])
+
+
 def masked_attention_via_map(
     Q: torch.Tensor,
     K: torch.Tensor,
@@ -545,7 +595,14 @@ def masked_attention_via_map(
 
     Returns [B, N, Hq, d] (or [N, Hq, d]); differentiable w.r.t. Q, K, V.
     Rows with no allowed key are zero (attention.py:91-100).
+
+    A residue-class mask (masks.same_residue, with or without masks.causal:
+    the reference benchmark's, check_attn.py:9-32) runs as L / P-long problems
+    over strided views (_residue_rewrite).
     """
+    rw = _residue_rewrite(Q, K, V, is_causal, kernel_fn, mask_fn, block_size, window_size, out_dtype, precision)
+    if rw is not None:
+        return rw
     plan, tm = trace_call(tuple(Q.shape), tuple(K.shape), tuple(V.shape), is_causal=is_causal,
                           mask_fn=mask_fn, block_size=block_size, window_size=window_size,
                           device=Q.device if Q.is_cuda else None)

@@ -209,3 +209,47 @@ def test_tilemap_entry_points_reject_before_launch(lib):
                                   None) == -2
     assert lib.mattn_tilemap_bits(ctypes.byref(s), 100, 100, 1, 1, None, 0, 0, 1, None, None, None,
                                   None) == 0                          # nothing to do
+
+
+def test_residue_view_is_the_class_major_permutation():
+    """check_attn's mask k % P == q % P as P problems of length L / P:
+    residue_view puts position s P + r at [r, s] without a copy, and
+    residue_unview undoes it."""
+    import torch
+
+    from jaxmodules_amd import attention as A
+
+    L, P, H, d = 48, 8, 3, 16
+    x = torch.arange(L * H * d, dtype=torch.float32).reshape(1, L, H, d)
+    v = A.residue_view(x, P)
+    assert v.shape == (P, L // P, H, d) and v.data_ptr() == x.data_ptr()
+    for r in range(P):
+        for s in range(L // P):
+            assert torch.equal(v[r, s], x[0, s * P + r])
+    assert torch.equal(A.residue_unview(v), x)
+    # within class r the mask (q - k) % P == 0 & k <= q is causal in the step index
+    q, k = np.arange(L)[:, None], np.arange(L)[None, :]
+    m = ((q - k) % P == 0) & (k <= q)
+    for r in range(P):
+        idx = np.arange(r, L, P)
+        assert np.array_equal(m[np.ix_(idx, idx)], np.tril(np.ones((L // P, L // P), bool)))
+        assert m[idx].sum() == m[np.ix_(idx, idx)].sum()      # no allowed key outside the class
+
+
+def test_residue_rewrite_applies_only_to_plain_residue_masks():
+    import torch
+
+    from jaxmodules_amd import attention as A
+
+    q = torch.zeros(1, 64, 2, 16)
+    args = dict(kernel_fn=A.default_kernel, block_size=None, window_size=None, out_dtype=None, precision=None)
+    for mf in (masks.intersect(masks.same_residue(8), masks.window(10, 0)), masks.causal(),
+               masks.intersect(masks.same_residue(8), masks.documents(np.zeros(64, int)))):
+        assert A._residue_rewrite(q, q, q, False, mask_fn=mf, **args) is None
+    mf = masks.same_residue(7)                       # L % P != 0
+    assert A._residue_rewrite(q, q, q, False, mask_fn=mf, **args) is None
+    mf = masks.same_residue(8)
+    assert A._residue_rewrite(torch.zeros(2, 64, 2, 16), torch.zeros(2, 64, 2, 16), torch.zeros(2, 64, 2, 16),
+                              False, mask_fn=mf, **args) is None    # B > 1
+    assert A._residue_rewrite(q, q, q, False, mask_fn=mf, kernel_fn=A.default_kernel, block_size=None,
+                              window_size=(8, 0), out_dtype=None, precision=None) is None
