@@ -82,9 +82,10 @@ enum mattn_status {
  * threshold_kernel has scale 1, attention.py:18-36), where rows concentrate
  * on single keys and dS = P (dP - delta) cancels below the float16 operand
  * rounding.  The scores are then compensated dot products (about twice
- * float32's precision) for every dtype, and the forward's residual
- * (mattn_fwd_workspace_bytes) holds each row's lse rounding error, which the
- * backward reads. */
+ * float32's precision) for every dtype, O and the row sums accumulate in
+ * float64, and the forward's residual (mattn_fwd_workspace_bytes) holds what
+ * the stored lse and O round off (one float per query row and per element of
+ * O), which the backward reads. */
 #define MATTN_PRECISE 4
 
 /* Tile size of the block map, in queries x keys. */
@@ -177,8 +178,8 @@ size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* b
 /* Bytes of the forward's residual buffer (256-byte aligned pointer): float16
  * copies of V and (with MATTN_FWD_FOR_BWD) Q, each times a power of two per
  * 128-row tile, which the forward's P V product and the backward read (16-bit
- * inputs at D <= 128); one float32 per query row under MATTN_PRECISE; 0
- * otherwise (float32 inputs, D = 256). */
+ * inputs at D <= 128); (1 + D) float32 per query row under MATTN_PRECISE;
+ * 0 otherwise (float32 inputs, D = 256). */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
 
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).

@@ -53,16 +53,20 @@ size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
 // [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
 // scale, and each V tile's max |V|.
-// MATTN_PRECISE on the SIMT kernels: the rounding error of each row's lse
-// (float32, [B, Hq, Lq]), which the backward adds back.
+// MATTN_PRECISE on the SIMT kernels: what the stored lse and O round off
+// (float32, [B, Hq, Lq] and [B, Hq, Lq, D]), which the backward adds back.
 struct FwdWs {
-  size_t vh, qh, vsc, vmax, qsc, lse_lo, total;
+  size_t vh, qh, vsc, vmax, qsc, lse_lo, o_lo, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
   FwdWs w{};
   if (simt_path(p)) {
-    if (p->flags & MATTN_PRECISE) w.total = align256((size_t)p->B * p->Hq * p->Lq * sizeof(float));
+    if (p->flags & MATTN_PRECISE) {
+      const size_t rows = (size_t)p->B * p->Hq * p->Lq;
+      w.o_lo = align256(rows * sizeof(float));
+      w.total = w.o_lo + align256(rows * p->D * sizeof(float));
+    }
     return w;
   }
   const size_t ktiles = (size_t)p->B * p->Hkv * cdiv(p->Lk, MATTN_TILE_K);
@@ -243,6 +247,7 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
   char* ws = (char*)workspace;
   if (w.total > 0 && simt_path(p)) {
     a.lse_lo = (float*)(ws + w.lse_lo);
+    a.o_lo = (float*)(ws + w.o_lo);
   } else if (w.total > 0) {
     a.vh = (uint16_t*)(ws + w.vh);
     a.vsc = (float*)(ws + w.vsc);
@@ -286,7 +291,9 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
   char* ws = (char*)workspace;
   a.delta = (float*)(ws + w.delta);
   if (simt_path(p) && (p->flags & MATTN_PRECISE)) {
-    a.lse_lo = (float*)((const char*)residual + fwd_ws_layout(p).lse_lo);
+    const FwdWs r = fwd_ws_layout(p);
+    a.lse_lo = (float*)((const char*)residual + r.lse_lo);
+    a.o_lo = (float*)((const char*)residual + r.o_lo);
   } else if (!simt_path(p)) {
     a.lsf = (float*)(ws + w.lsf);
     a.doh = (uint16_t*)(ws + w.doh);

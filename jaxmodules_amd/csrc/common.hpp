@@ -97,6 +97,7 @@ struct KArgs {
   const int* kv_desc;  // per dK/dV launch slot: { item, g, e, e_end, n_sub, qt, mask, row }
   int precise;         // MATTN_PRECISE: the SIMT kernels form the scores as compensated dot products
   float* lse_lo;       // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq], (m + log2 l) - lse
+  float* o_lo;         // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq, D], exact O - stored O
 };
 
 // dS storage slot base of (b, h): the map's entries are shared by the (b, h)

@@ -121,9 +121,16 @@ __device__ __forceinline__ void stage_rows(float* dst, const void* base, int64_t
   }
 }
 
-template <int D, int TPR, class IT, class OT>
+// PREC (MATTN_PRECISE): compensated scores, O and the row sum accumulated in
+// float64 (v_fma_f64 issues at the rate of the scalar float32 FMA on these
+// CUs), and the residual keeps what the stored lse and O round off: the
+// backward's dP - delta = dO . (V_k - O) then sees O to float64 accuracy,
+// which a row dominated by one key needs (V_k - O is then a small fraction of
+// |V|, and O's own float32 rounding a large part of it).
+template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void fwd_simt(KArgs a) {
+  using acc_t = typename std::conditional<PREC, double, float>::type;
   constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
   constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
   __shared__ __attribute__((aligned(16))) float Ks[SB * D];
@@ -141,16 +148,18 @@ void fwd_simt(KArgs a) {
   const int q = qt * TILE + row;
   const int qc = min(q, a.Lq - 1);
 
-  float qv[DP], ov[DP];
+  float qv[DP];
+  acc_t ov[DP];
   const int64_t qo = (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] + (int64_t)h * a.qs[2] + part * DP;
 #pragma unroll
   for (int i = 0; i < DP; i += 4) {
     Mem<IT>::get4(a.q, qo + i, qv + i);
-    ov[i] = ov[i + 1] = ov[i + 2] = ov[i + 3] = 0.f;
+    ov[i] = ov[i + 1] = ov[i + 2] = ov[i + 3] = 0;
   }
   const char* kb = (const char*)a.k + ES * ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2]);
   const char* vb = (const char*)a.v + ES * ((int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2]);
-  float m = NEG_INF, l = 0.f;
+  float m = NEG_INF;
+  acc_t l = 0;
 
   for (int e = e0; e < e1; ++e) {
     const int kt = a.row_ent[2 * e], mask = a.row_ent[2 * e + 1];
@@ -169,7 +178,7 @@ void fwd_simt(KArgs a) {
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
         float hi, lo;
-        score<DP, TPR>(qv, Ks + j * D + part * DP, a.precise, hi, lo);
+        score<DP, TPR>(qv, Ks + j * D + part * DP, PREC, hi, lo);
         float x = hi * a.scale_log2;
         sl[j] = fmaf(hi, a.scale_log2, -x) + lo * a.scale_log2;  // rounding of x, and the low part
         if (!((bits >> j) & 1u)) x = NEG_INF;
@@ -178,34 +187,48 @@ void fwd_simt(KArgs a) {
       }
       const float mn = fmaxf(m, mx);
       const float mu = (mn == NEG_INF) ? 0.f : mn;
-      const float alpha = exp2f(m - mu);
+      const acc_t alpha = exp2f(m - mu);   // a power of two's neighbourhood: exact enough in float
       m = mn;
       l *= alpha;
 #pragma unroll
       for (int i = 0; i < DP; ++i) ov[i] *= alpha;
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        const float p = exp2f((sc[j] - mu) + sl[j]);  // -inf + finite: 0 for masked keys
+        const acc_t p = exp2f((sc[j] - mu) + sl[j]);  // -inf + finite: 0 for masked keys
         l += p;
 #pragma unroll
-        for (int i = 0; i < DP; ++i) ov[i] = fmaf(p, Vs[j * D + part * DP + i], ov[i]);
+        for (int i = 0; i < DP; ++i) ov[i] = p * (acc_t)Vs[j * D + part * DP + i] + ov[i];
       }
     }
   }
   if (q >= a.Lq) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const acc_t inv = l > 0 ? 1 / l : 0;
+  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + q;
   if (part == 0) {
     float lse = NEG_INF, lo = 0.f;
-    if (l > 0.f) two_sum(m, log2f(l), lse, lo);  // lse + lo = m + log2 l exactly
-    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = lse;
-    if (a.precise) a.lse_lo[((int64_t)b * a.Hq + h) * a.Lq + q] = lo;
+    if (l > 0) {
+      if constexpr (PREC) {
+        const double full = (double)m + log2((double)l);
+        lse = (float)full;
+        lo = (float)(full - (double)lse);
+      } else {
+        two_sum(m, log2f(l), lse, lo);
+      }
+    }
+    a.lse[rs] = lse;
+    if constexpr (PREC) a.lse_lo[rs] = lo;  // lse + lse_lo = m + log2 l (to ~2^-48)
   }
   const int64_t oo = (int64_t)b * a.os[0] + (int64_t)q * a.os[1] + (int64_t)h * a.os[2] + part * DP;
 #pragma unroll
-  for (int i = 0; i < DP; ++i) Mem<OT>::put(a.out, oo + i, ov[i] * inv);
+  for (int i = 0; i < DP; ++i) {
+    const acc_t o = ov[i] * inv;
+    Mem<OT>::put(a.out, oo + i, (float)o);
+    if constexpr (PREC)  // what the stored O (in OT) leaves off
+      a.o_lo[rs * D + part * DP + i] = (float)(o - (acc_t)Mem<OT>::get(a.out, oo + i));
+  }
 }
 
-template <int D, int TPR, class IT, class OT>
+template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_dq_simt(KArgs a) {
   constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
@@ -225,19 +248,21 @@ void bwd_dq_simt(KArgs a) {
   const int q = qt * TILE + row;
   const int qc = min(q, a.Lq - 1);
 
-  float qv[DP], gv[DP], ov[DP], dq[DP];
+  float qv[DP], gv[DP], ov[DP], ol[DP], dq[DP];
   const int64_t qo = (int64_t)b * a.qs[0] + (int64_t)qc * a.qs[1] + (int64_t)h * a.qs[2] + part * DP;
   const int64_t go = (int64_t)b * a.dos[0] + (int64_t)qc * a.dos[1] + (int64_t)h * a.dos[2] + part * DP;
   const int64_t oo = (int64_t)b * a.os[0] + (int64_t)qc * a.os[1] + (int64_t)h * a.os[2] + part * DP;
+  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
 #pragma unroll
   for (int i = 0; i < DP; i += 4) {
     Mem<IT>::get4(a.q, qo + i, qv + i);
     Mem<OT>::get4(a.dO, go + i, gv + i);
     Mem<OT>::get4(a.o, oo + i, ov + i);
+    if constexpr (PREC) Mem<float>::get4(a.o_lo, rs * D + part * DP + i, ol + i);
+    else ol[i] = ol[i + 1] = ol[i + 2] = ol[i + 3] = 0.f;
     dq[i] = dq[i + 1] = dq[i + 2] = dq[i + 3] = 0.f;
   }
-  const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
-  const float lse = a.lse[rs], lse_lo = a.precise ? a.lse_lo[rs] : 0.f;
+  const float lse = a.lse[rs], lse_lo = PREC ? a.lse_lo[rs] : 0.f;
   const char* kb = (const char*)a.k + ES * ((int64_t)b * a.ks[0] + (int64_t)hk * a.ks[2]);
   const char* vb = (const char*)a.v + ES * ((int64_t)b * a.vs[0] + (int64_t)hk * a.vs[2]);
 
@@ -256,10 +281,10 @@ void bwd_dq_simt(KArgs a) {
       for (int j = 0; j < SB; ++j) {
         float g = 0.f;
 #pragma unroll
-        for (int i = 0; i < DP; ++i) g = fmaf(gv[i], Vs[j * D + part * DP + i] - ov[i], g);  // dP - delta
+        for (int i = 0; i < DP; ++i) g = fmaf(gv[i], (Vs[j * D + part * DP + i] - ov[i]) - ol[i], g);  // dP - delta
         g = row_sum<TPR>(g);
         float hi, lo;
-        score<DP, TPR>(qv, Ks + j * D + part * DP, a.precise, hi, lo);
+        score<DP, TPR>(qv, Ks + j * D + part * DP, PREC, hi, lo);
         float p = exp2f(fmaf(hi, a.scale_log2, -lse) + fmaf(lo, a.scale_log2, -lse_lo));
         if (!((bits >> j) & 1u)) p = 0.f;
         const float ds = p * g;
@@ -274,7 +299,7 @@ void bwd_dq_simt(KArgs a) {
   for (int i = 0; i < DP; ++i) Mem<IT>::put(a.dq, qo2 + i, dq[i] * a.scale);
 }
 
-template <int D, int TPR, class IT, class OT>
+template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_dkdv_simt(KArgs a) {
   constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
@@ -283,6 +308,7 @@ void bwd_dkdv_simt(KArgs a) {
   __shared__ __attribute__((aligned(16))) float Qs[SB * D];
   __shared__ __attribute__((aligned(16))) float Gs[SB * D];
   __shared__ __attribute__((aligned(16))) float Os[SB * D];
+  __shared__ __attribute__((aligned(16))) float Ol[PREC ? SB * D : 4];   // O's low parts (PREC)
   __shared__ float Ls[SB], Llo[SB];
 
   const int item = a.kv_order[blockIdx.x / SPLIT];
@@ -321,10 +347,11 @@ void bwd_dkdv_simt(KArgs a) {
         stage_rows<D, IT>(Qs, qb, a.qs[1], q0, a.Lq);
         stage_rows<D, OT>(Gs, gb, a.dos[1], q0, a.Lq);
         stage_rows<D, OT>(Os, ob, a.os[1], q0, a.Lq);
+        if constexpr (PREC) stage_rows<D, float>(Ol, a.o_lo + ((int64_t)b * a.Hq + h) * a.Lq * D, D, q0, a.Lq);
         if (tid < SB) {
           const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + min(q0 + tid, a.Lq - 1);
           Ls[tid] = a.lse[rs];
-          Llo[tid] = a.precise ? a.lse_lo[rs] : 0.f;
+          Llo[tid] = PREC ? a.lse_lo[rs] : 0.f;
         }
         __syncthreads();
         uint32_t bits = 0xffffffffu;
@@ -333,11 +360,14 @@ void bwd_dkdv_simt(KArgs a) {
         for (int j = 0; j < SB; ++j) {
           float gd = 0.f;
 #pragma unroll
-          for (int i = 0; i < DP; ++i)
-            gd = fmaf(vv[i] - Os[j * D + part * DP + i], Gs[j * D + part * DP + i], gd);  // dP - delta
+          for (int i = 0; i < DP; ++i) {
+            float dvo = vv[i] - Os[j * D + part * DP + i];  // V_k - O, then O's low part
+            if constexpr (PREC) dvo -= Ol[j * D + part * DP + i];
+            gd = fmaf(dvo, Gs[j * D + part * DP + i], gd);  // dP - delta
+          }
           gd = row_sum<TPR>(gd);
           float hi, lo;
-          score<DP, TPR>(kv, Qs + j * D + part * DP, a.precise, hi, lo);
+          score<DP, TPR>(kv, Qs + j * D + part * DP, PREC, hi, lo);
           float p = exp2f(fmaf(hi, a.scale_log2, -Ls[j]) + fmaf(lo, a.scale_log2, -Llo[j]));
           if (!((bits >> j) & 1u)) p = 0.f;
           const float ds = p * gd;
@@ -365,15 +395,22 @@ template <int D, int TPR, class IT, class OT>
 struct Simt {
   static constexpr int SPLIT = TILE * TPR / 512;
   static void fwd(const KArgs& a, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((fwd_simt<D, TPR, IT, OT>), dim3(grid * SPLIT), dim3(512), 0, st, a);
+    if (a.precise) hipLaunchKernelGGL((fwd_simt<D, TPR, IT, OT, true>), dim3(grid * SPLIT), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((fwd_simt<D, TPR, IT, OT, false>), dim3(grid * SPLIT), dim3(512), 0, st, a);
   }
   static void bwd(const KArgs& a, int stage, int q_grid, int kv_grid, hipStream_t st) {
     if (stage == MATTN_BWD_PRE) {
       // nothing: the SIMT kernels form dP - delta per pair from O
     } else if (stage == MATTN_BWD_DKDV) {
-      hipLaunchKernelGGL((bwd_dkdv_simt<D, TPR, IT, OT>), dim3(kv_grid * SPLIT), dim3(512), 0, st, a);
+      if (a.precise)
+        hipLaunchKernelGGL((bwd_dkdv_simt<D, TPR, IT, OT, true>), dim3(kv_grid * SPLIT), dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((bwd_dkdv_simt<D, TPR, IT, OT, false>), dim3(kv_grid * SPLIT), dim3(512), 0, st, a);
     } else {
-      hipLaunchKernelGGL((bwd_dq_simt<D, TPR, IT, OT>), dim3(q_grid * SPLIT), dim3(512), 0, st, a);
+      if (a.precise)
+        hipLaunchKernelGGL((bwd_dq_simt<D, TPR, IT, OT, true>), dim3(q_grid * SPLIT), dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((bwd_dq_simt<D, TPR, IT, OT, false>), dim3(q_grid * SPLIT), dim3(512), 0, st, a);
     }
   }
 };

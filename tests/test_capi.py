@@ -262,8 +262,9 @@ def test_backward_checks_workspace_size_and_residual_flag(lib):
     # float32 arithmetic for 16-bit inputs: SIMT path, no residual, no stored dS
     p.flags = _lib.MATTN_PRECISE | _lib.MATTN_BWD_DS
     assert lib.mattn_validate(ctypes.byref(p), ctypes.byref(bm)) == 0
-    rows = p.B * p.Hq * p.Lq           # the residual: each row's lse rounding error
-    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == (rows * 4 + 255) // 256 * 256
+    rows = p.B * p.Hq * p.Lq           # the residual: what each row's lse and O round off
+    a256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == a256(rows * 4) + a256(rows * p.D * 4)
     p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
     assert lib.mattn_bwd_workspace_bytes(ctypes.byref(p), ctypes.byref(bm)) == \
         lib.mattn_workspace_bytes(ctypes.byref(p32))
