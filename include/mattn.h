@@ -49,7 +49,7 @@ enum mattn_status {
   MATTN_OK = 0,
   MATTN_ERR_NULL = -1,          /* a required pointer is NULL                  */
   MATTN_ERR_SHAPE = -2,         /* non-positive size or Hq % Hkv != 0          */
-  MATTN_ERR_HEAD_DIM = -3,      /* D not in {64, 128, 256}                     */
+  MATTN_ERR_HEAD_DIM = -3,      /* D not in {64, 128, 256, 512}                */
   MATTN_ERR_DTYPE = -4,         /* unsupported dtype / o_dtype combination     */
   MATTN_ERR_STRIDE = -5,        /* misaligned pointer or stride                */
   MATTN_ERR_BLOCKMAP = -6,      /* tile map inconsistent with the problem      */
@@ -164,7 +164,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm);
  * aligned pointer); with it, mattn_bwd_workspace_bytes(p, bm).  0 for an
  * invalid problem.
  * Head dimensions 64 and 128 with 16-bit inputs run on the MFMA kernels;
- * float32 inputs, D = 256 for every dtype (the host pads d in (128, 256]
+ * float32 inputs, D = 256 and 512 for every dtype (the host pads d in (128, 512]
  * with zeros) and MATTN_PRECISE problems run on float32 SIMT kernels, whose
  * workspace is one float32 per query row. */
 size_t mattn_workspace_bytes(const mattn_problem* p);
@@ -179,7 +179,7 @@ size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* b
  * copies of V and (with MATTN_FWD_FOR_BWD) Q, each times a power of two per
  * 128-row tile, which the forward's P V product and the backward read (16-bit
  * inputs at D <= 128); (1 + D) float32 per query row under MATTN_PRECISE;
- * 0 otherwise (float32 inputs, D = 256). */
+ * 0 otherwise (float32 inputs, D >= 256). */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
 
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).

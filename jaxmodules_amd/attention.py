@@ -478,11 +478,11 @@ class _MaskedAttention(torch.autograd.Function):
 
 
 def _kernel_dim(d: int) -> int:
-    """Head dimension the kernels run at: 64, 128 or 256 (d zero-padded up to it)."""
-    for D in (64, 128, 256):
+    """Head dimension the kernels run at: 64, 128, 256 or 512 (d zero-padded up to it)."""
+    for D in (64, 128, 256, 512):
         if d <= D:
             return D
-    raise NotImplementedError(f"head dimension {d} > 256 is not supported by the HIP kernels")
+    raise NotImplementedError(f"head dimension {d} > 512 is not supported by the HIP kernels")
 
 
 def _pad_dim(x: torch.Tensor, D: int) -> torch.Tensor:

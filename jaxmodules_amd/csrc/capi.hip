@@ -2,7 +2,7 @@
 // workspace layouts, kernel-argument packing and launch selection.  Host code
 // only; the kernels live in fwd.hip, bwd_pre.hip, bwd_dkdv.hip, bwd_dq.hip
 // (16-bit inputs, D = 64 and 128: MFMA) and simt.hip (float32 inputs, and
-// every input dtype at D = 256: float32 SIMT arithmetic).
+// every input dtype at D = 256 and 512: float32 SIMT arithmetic).
 #include <math.h>
 
 #include <mutex>
@@ -156,7 +156,7 @@ const char* mattn_strerror(int status) {
     case MATTN_OK: return "success";
     case MATTN_ERR_NULL: return "a required pointer is NULL";
     case MATTN_ERR_SHAPE: return "invalid shape (sizes must be positive and Hq divisible by Hkv)";
-    case MATTN_ERR_HEAD_DIM: return "unsupported head dimension (supported: 64, 128, 256)";
+    case MATTN_ERR_HEAD_DIM: return "unsupported head dimension (supported: 64, 128, 256, 512)";
     case MATTN_ERR_DTYPE: return "unsupported dtype combination";
     case MATTN_ERR_STRIDE: return "pointer or stride not 16-byte aligned";
     case MATTN_ERR_BLOCKMAP: return "block map inconsistent with the problem";
@@ -175,7 +175,7 @@ int mattn_validate(const mattn_problem* p, const mattn_blockmap* bm) {
   if (p->B <= 0 || p->Lq <= 0 || p->Lk <= 0 || p->Hq <= 0 || p->Hkv <= 0 || p->D <= 0)
     return MATTN_ERR_SHAPE;
   if (p->Hq % p->Hkv != 0) return MATTN_ERR_SHAPE;
-  if (p->D != 64 && p->D != 128 && p->D != 256) return MATTN_ERR_HEAD_DIM;
+  if (p->D != 64 && p->D != 128 && p->D != 256 && p->D != 512) return MATTN_ERR_HEAD_DIM;
   if (p->dtype != MATTN_BF16 && p->dtype != MATTN_F16 && p->dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (p->o_dtype != p->dtype && p->o_dtype != MATTN_F32) return MATTN_ERR_DTYPE;
   if (!(p->scale > 0.f) || isinf(p->scale)) return MATTN_ERR_SHAPE;  // positive, finite

@@ -2,8 +2,9 @@
 // stages in float32 arithmetic, for
 //   * float32 inputs, whose 1e-5 tolerance rules out 16-bit operands, at head
 //     dimensions 64, 128 and 256;
-//   * 16-bit inputs at head dimension 256 (any d in (128, 256], zero-padded by
-//     the host), which the MFMA kernels' register and LDS tiling does not hold.
+//   * 16-bit inputs at head dimensions 256 and 512 (any d in (128, 512],
+//     zero-padded by the host), which the MFMA kernels' register and LDS
+//     tiling does not hold.
 //   * 16-bit inputs at D = 64 and 128 under MATTN_PRECISE (callers whose
 //     kernels are too sharp for float16 operands).
 // Same maths and tile walk as the MFMA path (/root/reference/jaxmodules/
@@ -16,7 +17,8 @@
 // |dO| |V|) would be all that is left of their difference.
 // TPR threads share a row (query or key), each holding D / TPR head dims; a
 // workgroup of 512 threads owns 512 / TPR rows of a 128-row map tile, so a
-// tile takes 128 TPR / 512 workgroups (one for TPR = 4, two for TPR = 8).
+// tile takes 128 TPR / 512 workgroups (one for TPR = 4, two for TPR = 8 at
+// D = 256, four for TPR = 16 at D = 512).
 #include <type_traits>
 
 #include "common.hpp"
@@ -56,7 +58,19 @@ struct Mem<bf16_tag> : Mem16<bf16_tag> {};
 template <>
 struct Mem<f16_tag> : Mem16<f16_tag> {};
 
-constexpr int SB = 32;  // keys (forward, dQ) or queries (dK/dV) per sub-block
+// keys (forward, dQ) or queries (dK/dV) per sub-block: 32, or 16 at D = 512,
+// where four [SB, D] float32 LDS tiles (the dK/dV kernel's Q, dO, O and O's
+// low parts) must fit 160 KiB
+template <int D>
+constexpr int sub_block() { return D > 256 ? 16 : 32; }
+
+// mask bits of sub-block sb (SB keys or queries) of a partial tile's 128-bit
+// row (or column) at `row`, one bit per element (words [mask][64-half][row])
+template <int SB>
+__device__ __forceinline__ uint32_t sub_bits(const uint64_t* bits, int mask, int sb, int row) {
+  const int first = sb * SB;
+  return (uint32_t)(bits[((int64_t)mask * 2 + (first >> 6)) * TILE + row] >> (first & 63));
+}
 
 // sum over the TPR lanes of a row (consecutive lanes)
 template <int TPR>
@@ -113,7 +127,7 @@ __device__ __forceinline__ void score(const float* qv, const float* y, bool comp
 
 // rows [r0, r0 + SB) of a [rows, D] tensor slice (row stride rs) as floats in
 // LDS; rows past n - 1 re-read row n - 1 (their scores are masked)
-template <int D, class T>
+template <int D, class T, int SB = sub_block<D>()>
 __device__ __forceinline__ void stage_rows(float* dst, const void* base, int64_t rs, int r0, int n) {
   for (int c = threadIdx.x; c < SB * D / 4; c += 512) {
     const int r = c / (D / 4), col = 4 * (c % (D / 4));
@@ -131,7 +145,7 @@ template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void fwd_simt(KArgs a) {
   using acc_t = typename std::conditional<PREC, double, float>::type;
-  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW, SB = sub_block<D>();
   constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
   __shared__ __attribute__((aligned(16))) float Ks[SB * D];
   __shared__ __attribute__((aligned(16))) float Vs[SB * D];
@@ -172,7 +186,7 @@ void fwd_simt(KArgs a) {
       __syncthreads();
       uint32_t bits = 0xffffffffu;
       if (mask >= 0)
-        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+        bits = sub_bits<SB>(a.row_bits, mask, sb, row);
       float sc[SB], sl[SB];  // scores s (scaled: s * scale_log2 = sc + sl)
       float mx = NEG_INF;
 #pragma unroll
@@ -231,7 +245,7 @@ void fwd_simt(KArgs a) {
 template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_dq_simt(KArgs a) {
-  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW, SB = sub_block<D>();
   constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
   __shared__ __attribute__((aligned(16))) float Ks[SB * D];
   __shared__ __attribute__((aligned(16))) float Vs[SB * D];
@@ -277,7 +291,7 @@ void bwd_dq_simt(KArgs a) {
       __syncthreads();
       uint32_t bits = 0xffffffffu;
       if (mask >= 0)
-        bits = (uint32_t)(a.row_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+        bits = sub_bits<SB>(a.row_bits, mask, sb, row);
       for (int j = 0; j < SB; ++j) {
         float g = 0.f;
 #pragma unroll
@@ -302,7 +316,7 @@ void bwd_dq_simt(KArgs a) {
 template <int D, int TPR, class IT, class OT, bool PREC>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void bwd_dkdv_simt(KArgs a) {
-  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW;
+  constexpr int DP = D / TPR, RPW = 512 / TPR, SPLIT = TILE / RPW, SB = sub_block<D>();
   constexpr int ES = std::is_same<IT, float>::value ? 4 : 2;
   constexpr int EO = std::is_same<OT, float>::value ? 4 : 2;
   __shared__ __attribute__((aligned(16))) float Qs[SB * D];
@@ -356,7 +370,7 @@ void bwd_dkdv_simt(KArgs a) {
         __syncthreads();
         uint32_t bits = 0xffffffffu;
         if (mask >= 0)
-          bits = (uint32_t)(a.col_bits[((int64_t)mask * 2 + (sb >> 1)) * TILE + row] >> (32 * (sb & 1)));
+          bits = sub_bits<SB>(a.col_bits, mask, sb, row);
         for (int j = 0; j < SB; ++j) {
           float gd = 0.f;
 #pragma unroll
@@ -422,7 +436,8 @@ template <class Tag, class F>
 void dispatch16(int D, bool of32, F&& f) {
   if (D == 64) { if (of32) f(Simt<64, 4, Tag, float>{}); else f(Simt<64, 4, Tag, Tag>{}); }
   else if (D == 128) { if (of32) f(Simt<128, 4, Tag, float>{}); else f(Simt<128, 4, Tag, Tag>{}); }
-  else { if (of32) f(Simt<256, 8, Tag, float>{}); else f(Simt<256, 8, Tag, Tag>{}); }
+  else if (D == 256) { if (of32) f(Simt<256, 8, Tag, float>{}); else f(Simt<256, 8, Tag, Tag>{}); }
+  else { if (of32) f(Simt<512, 16, Tag, float>{}); else f(Simt<512, 16, Tag, Tag>{}); }
 }
 template <class F>
 hipError_t dispatch(int D, int dtype, int o_dtype, F&& f) {
@@ -430,7 +445,8 @@ hipError_t dispatch(int D, int dtype, int o_dtype, F&& f) {
   if (dtype == MATTN_F32) {
     if (D == 64) f(Simt<64, 4, float, float>{});
     else if (D == 128) f(Simt<128, 4, float, float>{});
-    else f(Simt<256, 8, float, float>{});
+    else if (D == 256) f(Simt<256, 8, float, float>{});
+    else f(Simt<512, 16, float, float>{});
   } else if (dtype == MATTN_BF16) {
     dispatch16<bf16_tag>(D, of32, f);
   } else {

@@ -91,7 +91,8 @@ def test_validate_codes(lib):
     assert _validate(lib, _problem(B=0)) == -2
     assert _validate(lib, _problem(D=96)) == -3
     assert _validate(lib, _problem(D=256)) == 0
-    assert _validate(lib, _problem(D=512)) == -3
+    assert _validate(lib, _problem(D=512)) == 0
+    assert _validate(lib, _problem(D=1024)) == -3
     assert _validate(lib, _problem(dtype=7)) == -4
     assert _validate(lib, _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_BF16)) == -4
     assert _validate(lib, _problem(o_dtype=_lib.MATTN_F16)) == -4   # bf16 in, fp16 out

@@ -247,10 +247,10 @@ def test_flex_slow_evaluates_elements_with_query_head():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d", [16, 32, 96, 160, 200])
+@pytest.mark.parametrize("d", [16, 32, 96, 160, 200, 384, 512])
 def test_masked_attention_padded_head_dim(d):
-    """Head dimensions other than 64/128/256 (zero-padded on the GPU to the
-    next of the three), fwd + bwd."""
+    """Head dimensions other than 64/128/256/512 (zero-padded on the GPU to the
+    next of the four; d > 128 runs on the float32 SIMT kernels), fwd + bwd."""
     import jaxmodules_amd as jm
     from tests.helpers import oracle, seeded_inputs
 

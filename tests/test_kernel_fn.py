@@ -63,3 +63,14 @@ def test_rejected_kernel_raises_before_gpu():
     Q = torch.zeros(8, 2, 16)
     with pytest.raises(NotImplementedError):
         jm.masked_attention_via_map(Q, Q, Q, kernel_fn=lambda q, k: np.dot(q, k) ** 2 + 1)
+
+
+def test_head_dims_up_to_512():
+    """The host pads d to the next kernel head dimension, 64, 128, 256 or 512;
+    beyond 512 it raises NotImplementedError before any GPU work."""
+    from jaxmodules_amd import attention as A
+
+    assert [A._kernel_dim(d) for d in (1, 64, 65, 128, 129, 256, 257, 512)] == [64, 64, 128, 128, 256, 256,
+                                                                               512, 512]
+    with pytest.raises(NotImplementedError):
+        A._kernel_dim(513)
