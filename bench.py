@@ -203,7 +203,7 @@ def inputs_of(name):
 class Runner:
     """Preallocated buffers and direct C ABI calls for one configuration."""
 
-    def __init__(self, name, seed=0):
+    def __init__(self, name, seed=0, precise=False):
         import torch
 
         from jaxmodules_amd import _lib
@@ -237,10 +237,11 @@ class Runner:
             self.lse = torch.empty((RESIDUE_P, Hq, L // RESIDUE_P), dtype=torch.float32, device=dev)
         self.p = A._problem(self.q, self.k, self.v, self.o, 1.0 / d ** 0.5, do=self.do, dq=self.dq,
                             dk=self.dk, dv=self.dv)
-        self.p.flags = _lib.MATTN_FWD_FOR_BWD
+        self.p.flags = _lib.MATTN_FWD_FOR_BWD | (_lib.MATTN_PRECISE if precise else 0)
+        self.precise = precise
         self.bm = A.device_blockmap(tm, dev)
         # the backward's flags as the autograd path picks them (stored dS at D = 128)
-        self.p.flags = _lib.MATTN_FWD_FOR_BWD | A.bwd_flags(self.p, self.bm)
+        self.p.flags = A.bwd_flags(self.p, self.bm)
         self.stored_ds = bool(self.p.flags & _lib.MATTN_BWD_DS)
         nws = int(self.lib.mattn_bwd_workspace_bytes(ctypes.byref(self.p), ctypes.byref(self.bm)))
         self.ws = torch.empty(nws + 256, dtype=torch.uint8, device=dev)
@@ -395,6 +396,7 @@ def summary(r, ms, kern):
                                 "masks": r.tm.n_masks, "built_by": r.trace_how,
                                 "build_s": round(r.trace_s, 3)},
                    "bwd_dq": "from stored dS" if r.stored_ds else "recomputes S and dP",
+                   "precision": "highest (float32 SIMT)" if r.precise else "default (float16-operand MFMA)",
                    "bwd_workspace_bytes": r.ws_bytes}
 
 
@@ -413,6 +415,9 @@ def main():
                     help="run dQ by recomputing S and dP (no stored dS) everywhere")
     ap.add_argument("--stored-ds", action="store_true",
                     help="run dQ from the stored dS wherever the kernels allow it (head dim <= 128)")
+    ap.add_argument("--precise", action="store_true",
+                    help="measure precision=\"highest\" (MATTN_PRECISE: float32 SIMT kernels, compensated "
+                         "scores) instead of the default MFMA path; not the headline")
     ap.add_argument("--tilemap", action="store_true",
                     help="instead: time the tile-map build of configs 3-5, host tracer vs GPU classifier")
     args = ap.parse_args()
@@ -433,7 +438,7 @@ def main():
     if args.tilemap:
         print(json.dumps(tilemap_build_times()), flush=True)
         return
-    r = Runner(args.config)
+    r = Runner(args.config, precise=args.precise)
     _PAIRS[args.config] = r.pairs
     ms, kern = r.measure(args.steps, args.warmup)
     if args.copy_probe:
