@@ -282,3 +282,37 @@ def test_reference_custom_kernel(dtype):
         assert_close(t.grad.float().cpu().numpy(), r, dtype, name)
     o_def = jm.masked_attention_via_map(q.detach(), k.detach(), v.detach())
     assert not torch.allclose(o.detach(), o_def, rtol=1e-2)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_residue_rewrite_gqa_and_layouts(causal):
+    """The residue-class rewrite (attention._residue_rewrite) with grouped heads,
+    bfloat16 inputs, a 16-bit output, 3-D inputs and both mask forms (with and
+    without causal), against the oracle: the strided views carry the same
+    attention as the original order."""
+    import jaxmodules_amd as jm
+    from jaxmodules_amd import masks
+
+    P, L, Hq, Hkv, d = 16, 512, 4, 2, 64
+    mf = masks.intersect(masks.same_residue(P), masks.causal()) if causal else masks.same_residue(P)
+    kw = dict(mask_fn=mf, block_size=64)
+    Q, K, V, dO = seeded_inputs(1, L, L, Hq, Hkv, d, 31)
+    # dO rounded to bfloat16 once: the float32-output run and the bfloat16 one see the same values
+    Qr, Kr, Vr, dO = (torch.from_numpy(x).to(torch.bfloat16).float().numpy() for x in (Q, K, V, dO))
+    O_ref, _, g_ref, _ = oracle(Qr, Kr, Vr, dO, kw)
+    floor = Floor()
+    for three, od in ((False, None), (True, torch.bfloat16)):
+        q, k, v = (torch.from_numpy(x[0] if three else x).to("cuda", torch.bfloat16).requires_grad_()
+                   for x in (Q, K, V))
+        o = jm.masked_attention_via_map(q, k, v, out_dtype=od, **kw)
+        assert o.shape == q.shape and o.dtype == (od or torch.float32)
+        sq = (lambda x: x[0]) if three else (lambda x: x)
+        out_name = "bfloat16" if od is not None else "float32"
+        assert_close(o.detach().float().cpu().numpy(), sq(np.asarray(O_ref)), "bfloat16", f"3d={three} O",
+                     out_name, mag=sq(O_ref.mag), floor=floor)
+        o.backward(torch.from_numpy(sq(dO)).to("cuda", o.dtype))
+        for name, t, r in (("dQ", q, g_ref[0]), ("dK", k, g_ref[1]), ("dV", v, g_ref[2])):
+            assert_close(t.grad.float().cpu().numpy(), sq(np.asarray(r)), "bfloat16", f"3d={three} {name}",
+                         mag=sq(r.mag), floor=floor)
+    torch.cuda.synchronize()
+    floor.finish()
