@@ -394,8 +394,10 @@ void bwd_dkdv_mfma(KArgs a) {
   auto iter = [&](int s, auto bufc) {
     constexpr int BUF = decltype(bufc)::value;
     if (s + 1 < tot) prep(std::integral_constant<int, 1 - BUF>{}, std::false_type{});
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
-    __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
+    if (s > 0) {  // (sub-block 0: the prologue's wait and barrier)
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
+      __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
+    }
     const bool masked = (BUF ? mid1 : mid0) >= 0;
     if (s + 1 < tot) launch(std::integral_constant<int, 1 - BUF>{});
     if constexpr (DS) {
@@ -411,24 +413,36 @@ void bwd_dkdv_mfma(KArgs a) {
   }
   {
     // K' tile: float16 times the tile's copy_scale, into the resident LDS tile
-    // and to kh for the dQ kernel.  4 threads per key row.
+    // and to kh for the dQ kernel.  4 threads per key row.  The tile's max
+    // |K| meets through an LDS-only barrier (the V' and first sub-block loads
+    // stay in flight); the kh stores go out after the barrier that completes
+    // the tiles, so that no wait before the first sub-block covers them.
     constexpr int CPL = TileRows<D>::CPL;
-    const float kscl = copy_scale(block_max2_512(f32x2{tile_absmax<D, Tag>(tkr), 0.f}, red)[0]);
+    float km = tile_absmax<D, Tag>(tkr);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) km = fmaxf(km, __shfl_xor(km, o));
+    if (lane == 0) red[wave] = f32x2{km, 0.f};
+    barrier_lds_dma_in_flight();
+#pragma unroll
+    for (int w = 0; w < 8; ++w) km = fmaxf(km, red[w][0]);
+    const float kscl = copy_scale(km);
     const int r = tid >> 2, part = tid & 3;
-    uint16_t* kd = a.kh + ((int64_t)col * TILE + r) * D;
+    u32x4 yk[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = TileRows<D>::chunk(part, j);
-      const u32x4 yk = chunk_f16<Tag>(tkr.x[j], kscl);
-      *(u32x4*)&Ks[sw_off<D>(r, c)] = yk;
-      __builtin_nontemporal_store(yk, (u32x4*)(kd + 8 * c));
+      yk[j] = chunk_f16<Tag>(tkr.x[j], kscl);
+      *(u32x4*)&Ks[sw_off<D>(r, c)] = yk[j];
     }
-    if (tid == 0) a.ksc[col] = kscl;
     ksc = kscl;
     ivs = pow2_rcp(a.vsc[col]);
     m2c = c2 * pow2_rcp(acc_r * ksc);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's V' loads have landed
-    __syncthreads();                // the K' / V' tiles are complete
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's V' and sub-block 0 loads have landed
+    barrier_lds();                               // the K' / V' tiles and sub-block 0 are complete
+    uint16_t* kd = a.kh + ((int64_t)col * TILE + r) * D;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) __builtin_nontemporal_store(yk[j], (u32x4*)(kd + 8 * TileRows<D>::chunk(part, j)));
+    if (tid == 0) a.ksc[col] = kscl;
   }
   if (tot > 0) {  // the first sub-block's scales, loaded with its entry
     cur_r = rh0 = first_r;
@@ -438,9 +452,6 @@ void bwd_dkdv_mfma(KArgs a) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});
   }
-  if constexpr (DS) {
-    if (dpend) store_ds();  // the last sub-block's fragments
-  }
 
   // dK / dV: the second query half's partials join the first's through LDS
   // (wave kg + 4 -> wave kg; per key group a dK slab in the K / V tiles and a
@@ -448,8 +459,11 @@ void bwd_dkdv_mfma(KArgs a) {
   // then writes the finished rows of its 32 keys, scaled and rounded, over its
   // own slabs as [32 keys][D + 8] tiles, and all 8 waves store the 128 x D
   // tiles with 16-byte accesses along the rows.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (the dS~ stores of the sub-block before the last)
+  barrier_lds();                               // every wave is done with the LDS
+  if constexpr (DS) {
+    if (dpend) store_ds();  // the last sub-block's fragments, in flight during the reduction below
+  }
   constexpr int SLAB = NMD * 16 * 64;  // floats
   constexpr int OR = D + 8;            // staged row (elements): 16-byte aligned, spreads banks
   static_assert(2 * SLAB * 4 <= TILE * D * 2 && SLAB * 4 <= BM * D * 2 && 32 * OR * 2 <= SLAB * 4,
@@ -466,7 +480,7 @@ void bwd_dkdv_mfma(KArgs a) {
         ((f32x4*)redv)[(mt * 4 + c) * 64 + lane] = f32x4{dv[mt][4 * c], dv[mt][4 * c + 1], dv[mt][4 * c + 2], dv[mt][4 * c + 3]};
       }
   }
-  __syncthreads();
+  barrier_lds();
   if (qh == 0) {
     // the slabs are this wave's alone: the rows overwrite them after the reads
     auto finish = [&](f32x16 (&acc)[NMD], float* red, float sc) {
@@ -491,7 +505,7 @@ void bwd_dkdv_mfma(KArgs a) {
     finish(dk, redk, a.scale * pow2_rcp(acc_s * acc_r));
     finish(dv, redv, pow2_rcp(acc_s));
   }
-  __syncthreads();
+  barrier_lds();
   constexpr int CPR = D / 8;  // 16-byte chunks per row
 #pragma unroll
   for (int i = 0; i < TILE * CPR / 512; ++i) {

@@ -523,6 +523,12 @@ __device__ __forceinline__ float tile_absmax(const TileRows<D>& t) {
 // also drains loads in flight (and stores); asm, so that the compiler moves no
 // memory operation across it.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The same barrier where global->LDS loads may stay in flight on purpose (it
+// hands no DMA-filled buffer to the other waves); the comment marks it for the
+// assembly check of tests/lds_waits.py.
+__device__ __forceinline__ void barrier_lds_dma_in_flight() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier ; lds-only: global->LDS loads may be in flight" ::: "memory");
+}
 
 // maximum over the 512 threads of a workgroup (red: 8 entries; one barrier
 // before the write guards a previous use of red)

@@ -142,7 +142,19 @@ _VMEM = ("global_load", "global_store", "global_atomic", "buffer_load", "buffer_
          "flat_", "scratch_")
 
 
-def _dma_walk(lines: list, loop_in: dict) -> tuple:
+def _fold(st: tuple, keep: int) -> tuple:
+    """A state with at most `keep` tracked operations: the older ones fold into
+    one leading ("old", line) entry when any of them is a global->LDS load.
+    Exact for this walk, since no wait in the kernel keeps more than `keep`
+    operations outstanding: the next vmcnt retires every folded operation."""
+    if len(st) <= keep:
+        return st
+    old = [e for e in st[:len(st) - keep] if e[0] in ("dma", "old")]
+    rest = st[len(st) - keep:] if keep else ()
+    return ((("old", old[0][1]),) if old else ()) + rest
+
+
+def _dma_walk(lines: list, loop_in: dict, keep: int = 0) -> tuple:
     """One layout-order walk for check_dma: (problems, back-edge states by label)."""
     problems = []
     states = [()]
@@ -183,14 +195,16 @@ def _dma_walk(lines: list, loop_in: dict) -> tuple:
                 states = [st[max(0, len(st) - lim):] if lim else () for st in states]
             continue
         if op == "s_barrier":
+            if "lds-only" in raw:  # a barrier that hands no DMA-filled buffer over (marked in the source)
+                continue
             for st in states:
                 for kind, ln in st:
-                    if kind == "dma":
+                    if kind in ("dma", "old"):
                         problems.append(f"line {n}: s_barrier with the global->LDS load of line {ln} outstanding")
             continue
         if op.startswith(_VMEM):
             kind = "dma" if re.search(r"\blds\b", t[len(op):]) or op.endswith("_lds_dwordx4") else "vmem"
-            states = [st + ((kind, n),) for st in states]
+            states = list(dict.fromkeys(_fold(st + ((kind, n),), keep) for st in states))
     for label in fwd:
         problems.append(f"branch to {label}, which is not in the walked code")
     return problems, back
@@ -199,9 +213,11 @@ def _dma_walk(lines: list, loop_in: dict) -> tuple:
 def check_dma(lines: list, max_rounds: int = 20) -> tuple:
     """(number of global->LDS loads seen, list of problem descriptions)."""
     dma = sum(1 for l in lines if re.search(r"^\s*(global_load_lds_\w+|buffer_load_\w+.*\blds\b)", l.split(";")[0]))
+    # the largest vmcnt any wait keeps outstanding bounds what a state must track
+    keep = max([int(m) for l in lines for m in re.findall(r"vmcnt\((\d+)\)", l.split(";")[0])] + [0])
     loop_in: dict = {}
     for _ in range(max_rounds):
-        problems, back = _dma_walk(lines, loop_in)
+        problems, back = _dma_walk(lines, loop_in, keep)
         grown = False
         for label, sts in back.items():
             cur = loop_in.setdefault(label, set())

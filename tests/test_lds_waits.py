@@ -145,3 +145,25 @@ def test_dma_checker_carries_loads_across_the_back_edge():
     assert problems and all("load of line 6 outstanding" in p for p in problems), problems
     fixed = _LOOP.replace("vmcnt(2)", "vmcnt(1)", 1)
     assert lds_waits.check_dma(fixed.split("\n"))[1] == []
+
+
+_MARKED = """\
+\tglobal_load_lds_dwordx4 v1, s[0:1]
+\ts_waitcnt lgkmcnt(0)
+\ts_barrier ; lds-only: global->LDS loads may be in flight
+\tglobal_store_dwordx4 v[2:3], v[4:7], off
+\tglobal_store_dwordx4 v[2:3], v[4:7], off
+\ts_barrier
+\ts_endpgm
+"""
+
+
+def test_dma_checker_exempts_only_marked_barriers():
+    """A barrier marked lds-only (barrier_lds_dma_in_flight) may have a DMA in
+    flight; the load is still tracked, through the stores that fold it away
+    (no wait in the code keeps any operation outstanding), to the next,
+    unmarked barrier, which is reported."""
+    _, problems = lds_waits.check_dma(_MARKED.split("\n"))
+    assert len(problems) == 1 and problems[0].startswith("line 5: s_barrier") and "line 0" in problems[0]
+    fixed = _MARKED.replace("\ts_barrier\n\ts_endpgm", "\ts_waitcnt vmcnt(0)\n\ts_barrier\n\ts_endpgm")
+    assert lds_waits.check_dma(fixed.split("\n"))[1] == []
