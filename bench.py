@@ -15,9 +15,9 @@ BlockMask.tile_map as BASELINE words it), cfg5 (packed documents), the
 target shape with 8 KV heads (GQA), and the regime of the reference's own
 benchmark script (check_attn.py: float16, one head, d=64, L=131072, block
 8192, mask k % 2048 == q % 2048 and k <= q), which runs as the library runs
-it: its 2048 residue classes as causal problems of length 64 over strided
-views of the same tensors (attention._residue_rewrite), outputs in the
-original order.
+it: its 2048 residue classes, two to a problem, as 1024 problems of 128
+positions over strided views of the same tensors (attention._residue_rewrite),
+outputs in the original order.
 
 Each kernel's time is measured with HIP events on the stream the kernels run
 on (torch's current stream, which the C ABI launches on).  The CPU baseline
@@ -173,11 +173,13 @@ def tile_map_of(name):
     B, L, Hq, Hkv, d, kw, _ = workload(name)
     t0 = time.perf_counter()
     if name == "check_attn":
-        # the residue classes as P causal problems of L / P (attention._residue_rewrite)
-        P = RESIDUE_P
-        shp = (P, L // P, Hq, d)
-        _, tm = A.trace_call(shp, (P, L // P, Hkv, d), (P, L // P, Hkv, d), is_causal=True, device="cuda:0")
-        return tm, time.perf_counter() - t0, f"GPU tile classifier, {P} residue classes as causal problems"
+        # the residue classes as problems of c L / P positions, c classes each
+        # (attention._residue_rewrite)
+        Pv, inner = A.residue_problem(L, RESIDUE_P, True)
+        n = L // Pv
+        _, tm = A.trace_call((Pv, n, Hq, d), (Pv, n, Hkv, d), (Pv, n, Hkv, d), device="cuda:0", **inner)
+        return tm, time.perf_counter() - t0, (f"GPU tile classifier, {RESIDUE_P} residue classes as {Pv} "
+                                              f"problems of {n} positions ({RESIDUE_P // Pv} classes each)")
     if name == "cfg4":
         bm = create_block_mask(kw["mask_fn"], B, Hq, L, L, 128)
         tm = bm.tile_map(B, Hq, Hkv)
@@ -231,10 +233,11 @@ class Runner:
         self.dq = torch.empty_like(self.q)
         self.dk = torch.empty_like(self.k)
         self.dv = torch.empty_like(self.v)
-        if name == "check_attn":   # strided [P, L / P, H, d] views: outputs land in the original order
+        if name == "check_attn":   # strided [P / c, c L / P, H, d] views: outputs land in the original order
+            Pv, _ = A.residue_problem(L, RESIDUE_P, True)
             for f in ("q", "k", "v", "do", "o", "dq", "dk", "dv"):
-                setattr(self, f, A.residue_view(getattr(self, f), RESIDUE_P))
-            self.lse = torch.empty((RESIDUE_P, Hq, L // RESIDUE_P), dtype=torch.float32, device=dev)
+                setattr(self, f, A.residue_view(getattr(self, f), Pv))
+            self.lse = torch.empty((Pv, Hq, L // Pv), dtype=torch.float32, device=dev)
         self.p = A._problem(self.q, self.k, self.v, self.o, 1.0 / d ** 0.5, do=self.do, dq=self.dq,
                             dk=self.dk, dv=self.dv)
         self.p.flags = _lib.MATTN_FWD_FOR_BWD | (_lib.MATTN_PRECISE if precise else 0)

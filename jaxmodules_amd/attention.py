@@ -511,20 +511,53 @@ def use_precise(precision: Optional[str], scale: float, d: int) -> bool:
     return precision == "highest"
 
 
+def residue_pack(L: int, P: int) -> int:
+    """How many residue classes c one rewritten problem carries: the largest
+    power of two dividing P with c L / P <= 128, so that a problem of c L / P
+    positions fills (at most) one 128 x 128 tile instead of padding L / P
+    rows to 128.  Rows of a problem are positions t (P / c) + r', classes
+    r' and r' + P / c, ... interleaved: step t of class r' + (t mod c) P / c."""
+    n, c = L // P, 1
+    while P % (2 * c) == 0 and 2 * c * n <= bmap.TILE:
+        c *= 2
+    return c
+
+
+def residue_problem(L: int, P: int, causal: bool):
+    """(view period, keyword arguments of the rewritten call) for the mask
+    k % P == q % P (and k <= q) on L positions: the tensors are viewed with
+    residue_view(x, P / c), and the c classes a problem interleaves are told
+    apart by (t_q - t_k) % c == 0 on its own positions t (with t_k <= t_q for
+    causal), c = residue_pack(L, P)."""
+    from . import masks
+
+    c = residue_pack(L, P)
+    if c == 1:
+        return P, dict(is_causal=causal)
+    inner = masks.same_residue(c)
+    if causal:
+        inner = masks.intersect(inner, masks.causal())
+    return P // c, dict(mask_fn=inner)
+
+
 def _residue_rewrite(Q, K, V, is_causal, kernel_fn, mask_fn, block_size, window_size, out_dtype,
                      precision):
     """The strided mask of the reference's benchmark, k % P == q % P (and
-    k <= q: check_attn.py:9-32), as P independent problems of length L / P.
+    k <= q: check_attn.py:9-32), as independent problems of L / P positions per
+    residue class, c classes per problem (residue_pack).
 
     Position q = s P + r is step s of residue class r, and a query attends only
-    keys of its own class, so the [1, L, H, d] tensors viewed as [P, L / P, H, d]
-    (batch = class, stride H d; sequence = step, stride P H d: views, no copy)
-    carry the same attention under a causal mask (or none).  The tiles of the
-    original problem each hold one allowed key per row in 128 (every present
-    tile partial); the rewritten problem's are dense causal.  Applies to a
-    closed-form mask (jaxmodules_amd.masks) that is a residue class, with or
-    without causal, and nothing else, no window_size, B = 1 (or 3-D inputs),
-    equal query and key lengths divisible by P; None otherwise."""
+    keys of its own class, so the [1, L, H, d] tensors viewed as
+    [P / c, c L / P, H, d] (batch r', stride H d; position t, stride (P / c) H d:
+    views, no copy) carry the same attention under the mask
+    (t_q - t_k) % c == 0 (and t_k <= t_q): position t of batch r' is
+    t (P / c) + r', and two such positions share a class exactly when
+    c divides t_q - t_k.  The tiles of the original problem each hold one
+    allowed key per row in 128 (every present tile partial); the rewritten
+    problem fills its tile.  Applies to a closed-form mask
+    (jaxmodules_amd.masks) that is a residue class, with or without causal,
+    and nothing else, no window_size, B = 1 (or 3-D inputs), equal query and
+    key lengths divisible by P; None otherwise."""
     from . import masks
 
     spec = masks.spec_of(mask_fn) if mask_fn is not None else None
@@ -540,11 +573,14 @@ def _residue_rewrite(Q, K, V, is_causal, kernel_fn, mask_fn, block_size, window_
     L, P = k4.shape[1], spec.period
     if B != 1 or N != L or L % P or v4.shape[1] != L:
         return None
+    Pv, inner = residue_problem(L, P, spec.causal)
+    if Pv == 1:  # one problem: the original one
+        return None
     # the reference's checks (and exception types) on the original call
     bmap.make_plan(tuple(Q.shape), tuple(K.shape), tuple(V.shape), mask_fn=mask_fn,
                    block_size=block_size, window_size=window_size)
-    out = masked_attention_via_map(*(residue_view(x, P) for x in (q4, k4, v4)), is_causal=spec.causal,
-                                   kernel_fn=kernel_fn, out_dtype=out_dtype, precision=precision)
+    out = _via_map(*(residue_view(x, Pv) for x in (q4, k4, v4)), kernel_fn=kernel_fn, block_size=None,
+                   window_size=None, out_dtype=out_dtype, precision=precision, **inner)
     out = residue_unview(out)
     return out[0] if three else out
 
@@ -603,6 +639,13 @@ def masked_attention_via_map(
     rw = _residue_rewrite(Q, K, V, is_causal, kernel_fn, mask_fn, block_size, window_size, out_dtype, precision)
     if rw is not None:
         return rw
+    return _via_map(Q, K, V, is_causal=is_causal, kernel_fn=kernel_fn, mask_fn=mask_fn, block_size=block_size,
+                    window_size=window_size, out_dtype=out_dtype, precision=precision)
+
+
+def _via_map(Q, K, V, *, is_causal=False, kernel_fn=default_kernel, mask_fn=None, block_size=None,
+             window_size=None, out_dtype=None, precision=None):
+    """masked_attention_via_map without the residue-class rewrite."""
     plan, tm = trace_call(tuple(Q.shape), tuple(K.shape), tuple(V.shape), is_causal=is_causal,
                           mask_fn=mask_fn, block_size=block_size, window_size=window_size,
                           device=Q.device if Q.is_cuda else None)

@@ -236,6 +236,38 @@ def test_residue_view_is_the_class_major_permutation():
         assert m[idx].sum() == m[np.ix_(idx, idx)].sum()      # no allowed key outside the class
 
 
+@pytest.mark.parametrize("L,P", [(131072, 2048), (512, 16), (48, 8), (96, 12), (1024, 4), (640, 10)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_residue_problem_packs_classes_without_changing_the_mask(L, P, causal):
+    """residue_problem's rewrite of k % P == q % P (& k <= q): c classes per
+    problem (the largest power of two dividing P with c L / P <= 128), and on
+    every problem of the [P / c, c L / P] view the inner mask equals the
+    original mask between the positions it stands for, while no allowed key
+    lies outside the problem (brute force over the original L x L mask, or over
+    the rows of a few problems at the largest size)."""
+    from jaxmodules_amd import attention as A
+
+    Pv, inner = A.residue_problem(L, P, causal)
+    c = P // Pv
+    assert Pv * c == P and c & (c - 1) == 0 and (c == 1 or c * (L // P) <= 128)
+    assert P % (2 * c) or 2 * c * (L // P) > 128           # the largest such c
+    n = L // Pv
+    t = np.arange(n)
+    if c == 1:
+        assert inner == dict(is_causal=causal)
+        im = np.tril(np.ones((n, n), bool)) if causal else np.ones((n, n), bool)
+    else:
+        spec = masks.spec_of(inner["mask_fn"])
+        assert spec.period == c and spec.causal == causal and "is_causal" not in inner
+        im = inner["mask_fn"](0, 0, t[:, None], t[None, :])
+    for r in (range(Pv) if L <= 4096 else (0, 1, Pv // 2, Pv - 1)):
+        pos = t * Pv + r
+        q, k = pos[:, None], np.arange(L)[None, :]
+        m = ((q - k) % P == 0) & ((k <= q) if causal else True)
+        assert np.array_equal(m[:, pos], im)
+        assert m.sum() == im.sum()                          # no allowed key outside the problem
+
+
 def test_residue_rewrite_applies_only_to_plain_residue_masks():
     import torch
 
