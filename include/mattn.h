@@ -76,7 +76,11 @@ enum mattn_status {
 /* mattn_problem.flags: float32 arithmetic for 16-bit inputs.  The problem runs
  * on the SIMT kernels (every product and sum in float32, the inputs read
  * exactly), as float32 inputs do, instead of the MFMA kernels, whose
- * operands P, dS and dO are rounded to float16 (11 significant bits).  Set it
+ * operands P, dS and dO are rounded to float16 (11 significant bits) -- except
+ * in split tiles: 128-row query tiles with a row whose largest attention
+ * weight reaches 1/8, whose O, lse and gradient terms the MFMA path forms
+ * again with those operands' rounded-off parts (22 significant bits) by
+ * kernels of their own, after the main ones.  Set it
  * for a forward and for its backward alike; the forward then has no residual.
  * For kernels sharper than the default scale 1/sqrt(d) (the reference's
  * threshold_kernel has scale 1, attention.py:18-36), where rows concentrate
@@ -223,12 +227,12 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
                     void* stream);
 
 /* Size of the library's static device scratch used by mattn_bwd_noalloc. */
-#define MATTN_SCRATCH_BYTES (256u << 20)
+#define MATTN_SCRATCH_BYTES (512u << 20)
 
 /* mattn_bwd without a workspace argument: the backward's workspace is a
- * static device array of MATTN_SCRATCH_BYTES (256 MiB) inside the library, one
+ * static device array of MATTN_SCRATCH_BYTES (512 MiB) inside the library, one
  * per device, so the call makes no allocation of any kind (B=1 L=8192 H=32
- * D=128 needs 130 MiB).  It has no
+ * D=128 needs 450 MiB).  It has no
  * counterpart in the reference (whose backward is a jax custom_vjp rule); it
  * is for callers that cannot allocate: code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Problems whose

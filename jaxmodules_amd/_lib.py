@@ -43,7 +43,7 @@ EXPORTS = ("mattn_validate", "mattn_workspace_bytes", "mattn_bwd_workspace_bytes
            "mattn_fwd", "mattn_bwd",
            "mattn_bwd_stage", "mattn_strerror", "mattn_abi_version", "mattn_maskspec_validate",
            "mattn_tilemap_classify", "mattn_tilemap_bits", "mattn_bwd_noalloc")
-SCRATCH_BYTES = 256 << 20  # MATTN_SCRATCH_BYTES
+SCRATCH_BYTES = 512 << 20  # MATTN_SCRATCH_BYTES
 BWD_PRE, BWD_DKDV, BWD_DQ = 0, 1, 2
 
 _I64x3 = ctypes.c_int64 * 3

@@ -42,9 +42,21 @@ namespace mattn {
 // (nontemporal: read once, much later) right after the next sub-block's
 // barrier, or after the loop, so that they have a whole step to complete
 // before the wait ahead of the following barrier, which counts stores too.
-template <int D, class Tag, bool DS>
+//
+// Split tiles.  A query tile whose rows put a weight of at least SPLIT_P on
+// a key is a split tile (bwd_pre marks it by a negative asc).  The kernel
+// (SPLIT = false) computes its sub-blocks like any other; a column whose walk
+// met one also leaves its reduced dK and dV unrounded (float32, free of the
+// accumulator scales) in kvp and sets its flag in scol.  The SPLIT = true
+// kernel, launched after it, takes those columns (its other workgroups
+// return at once), starts from kvp, and adds for each split sub-block the
+// products of what float16 rounded off there (correct() below), so that the
+// tile's terms enter dK and dV with 22 significant bits; it then stores the
+// column's dK and dV over the first kernel's.
+template <int D, class Tag, bool DS, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
+  static_assert(!(DS && SPLIT), "the split kernel stores no dS");
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
@@ -62,6 +74,8 @@ void bwd_dkdv_mfma(KArgs a) {
   // per buffer: Q' rows, then dO' rows (BM * D elements each); K' tile, then V' tile
   __shared__ __attribute__((aligned(16))) uint16_t QH0[2 * BM * D], QH1[2 * BM * D];
   __shared__ __attribute__((aligned(16))) uint16_t KV[2 * TILE * D];
+  // SPLIT: the rounded-off part of dO' of the split sub-block being corrected
+  __shared__ __attribute__((aligned(16))) uint16_t DL[SPLIT ? BM * D : 8];
   uint16_t* const Q0 = QH0;
   uint16_t* const H0 = QH0 + BM * D;
   uint16_t* const Q1 = QH1;
@@ -77,6 +91,9 @@ void bwd_dkdv_mfma(KArgs a) {
   const u32x4 dB = ((const u32x4*)a.kv_desc)[2 * blockIdx.x + 1];
   const int item = (int)dA[0];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
+  if constexpr (SPLIT) {
+    if (a.scol[item] == 0) return;  // no split tile in this column: the first kernel's dK, dV stand
+  }
   const int kt = item % a.nkt;
   const int bh = item / a.nkt;
   const int hk = bh % a.Hkv, b = bh / a.Hkv;
@@ -94,20 +111,24 @@ void bwd_dkdv_mfma(KArgs a) {
   const int col = item;  // (b * Hkv + hk) * nkt + kt
   {
     const uint16_t* vsrc = a.vh + (int64_t)col * TILE * D;
+    const uint16_t* ksrc = a.kh + (int64_t)col * TILE * D;  // SPLIT: the first kernel's K' tile
 #pragma unroll
     for (int i = 0; i < 2 * NS; ++i) {
       const int n = 2 * NS * wave + i;
-      lds_load16(vsrc + (int64_t)TL::row_of(n, lane) * D + 8 * TL::chunk_of(n, lane), Vs + n * BLK);
+      const int64_t off = (int64_t)TL::row_of(n, lane) * D + 8 * TL::chunk_of(n, lane);
+      lds_load16(vsrc + off, Vs + n * BLK);
+      if constexpr (SPLIT) lds_load16(ksrc + off, Ks + n * BLK);
     }
   }
   TileRows<D> tkr;
-  tile_load<D>(tkr, (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)(kt * TILE) * a.ks[1] +
-                        (int64_t)hk * a.ks[2], a.ks[1], a.Lk - kt * TILE);
+  if constexpr (!SPLIT)
+    tile_load<D>(tkr, (const uint16_t*)a.k + (int64_t)b * a.ks[0] + (int64_t)(kt * TILE) * a.ks[1] +
+                          (int64_t)hk * a.ks[2], a.ks[1], a.Lk - kt * TILE);
 
   // Flattened walk over (query head g of the group, column entry, half):
   // tot sub-blocks; the cursor of the next sub-block to load starts at the
   // descriptor's first entry
-  const int tot = (int)dB[0];
+  const int tot = SPLIT ? 0 : (int)dB[0];  // (the split kernel walks the split sub-blocks alone)
   int lg = (int)dA[1], le = (int)dA[2], lend = (int)dA[3], lhalf = 0;
 
   // loop-invariant source byte offsets of this lane's load slots (Q' and dO'
@@ -129,8 +150,11 @@ void bwd_dkdv_mfma(KArgs a) {
   const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
   EntryCache ec;
   int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
-  // dO' and Q' tile scales (s, r) of the sub-block in each buffer
+  // dO' and Q' tile scales (s, r) of the sub-block in each buffer, and
+  // whether its query tile is a split tile (the sign of asc)
   float sh0 = 1.f, rh0 = 1.f, sh1 = 1.f, rh1 = 1.f;
+  bool sp0 = false, sp1 = false;
+  bool any_split = false;  // the walk met a sub-block of a split tile
   // buffer resources of the current query head's Q' and dO' slices
   const int64_t hrows = (int64_t)a.nqt * TILE;  // rows per head in the copies
   const uint32_t hbytes = (uint32_t)(hrows * D * 2);
@@ -211,7 +235,8 @@ void bwd_dkdv_mfma(KArgs a) {
     if constexpr (DS)  // this query half's two dQ waves (2 lhalf, 2 lhalf + 1) of the tile's slot
       (BUF ? dsp1 : dsp0) = a.ds + (ds_rep(a, b, rh_head) + cur_ri) * DS_TILE + lhalf * (2 * 8 * 512);
     (BUF ? mid1 : mid0) = cur_mid;
-    (BUF ? sh1 : sh0) = cur_s;
+    (BUF ? sh1 : sh0) = fabsf(cur_s);
+    (BUF ? sp1 : sp0) = cur_s < 0.f;
     (BUF ? rh1 : rh0) = cur_r;
     nq0 = cur_qt * TILE + lhalf * BM;
     if (lhalf == 0) {
@@ -389,6 +414,174 @@ void bwd_dkdv_mfma(KArgs a) {
     }
   };
 
+  // SPLIT: one split sub-block in buffer 0 (Q', dO', lse - log2 f, delta,
+  // mask words) and DL (dO'_lo, the rounded-off part of dO' that bwd_pre
+  // left in dol; delta of a split tile is taken from the unrounded dO), with
+  // the accumulators in its scales: the products of what float16 rounded off
+  // when the first kernel's step() computed it.  S, dP, P~ and dS~ are formed
+  // again exactly as step() formed them (same operands, same order: the same
+  // float32 values), then
+  //   dP_e    = dP' + dO'_lo V'^T,   dS~_e = P~ (dP_e / v - delta s)
+  //   dV^T   += dO'^T (P~ - float16(P~)) + dO'_lo^T float16(P~)
+  //   dK^T   += Q'^T (dS~_e - float16(dS~))
+  // with P~ held as float16(P~) + its rounded-off part once packed.  Operands
+  // are read with a full wait each (rare work: at the target shape one query
+  // tile in 64 of every head).
+  auto correct = [&](bool masked) {
+    const float mc = m2c;
+    const float* Lb = L0 + 32 * qh;
+    const float* Gb = G0 + 32 * qh;
+    const int rxo = opaque(rx), tzo = opaque(tz);
+    const uint32_t qa0 = lds_addr(Q0) + 2 * (uint32_t)qrow;
+    const uint32_t la0 = lds_addr(DL) + 2 * (uint32_t)qrow;
+    const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
+    f32x16 st = f32x16{};
+    static_for<NKD>([&](auto kc) {
+      constexpr int kd = decltype(kc)::value;
+      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
+      u32x4 qa = ds_read128<0>(qa0 + x), ka = ds_read128<0>(ka0 + x);
+      lgkm_wait<0>();
+      hold(qa);
+      hold(ka);
+      st = H::mfma(qa, ka, st);
+      hold(st);
+    });
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st[4 * j + i] = fast_exp2(fmaf(st[4 * j + i], mc, -lv[i]));
+    }
+    if (masked) {
+      const uint64_t mw = M0[kloc];
+      const uint32_t w32 = (uint32_t)(mw >> (32 * qh)) >> (4 * hi);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        st[r] = mask_zero(st[r], mask_ones(w32, r));
+    }
+    u32x4 pk[2], plo[2], slo[2];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const uint32_t wp = H::pack2(st[r], st[r + 1]);
+      pk[r >> 3][(r & 7) >> 1] = wp;
+      plo[r >> 3][(r & 7) >> 1] = H::pack2(st[r] - H::to_f32(wp & 0xffffu), st[r + 1] - H::to_f32(wp >> 16));
+    }
+    f32x16 dp = f32x16{};
+    static_for<NKD>([&](auto kc) {
+      constexpr int kd = decltype(kc)::value;
+      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
+      u32x4 ha = ds_read128<2 * BM * D>(qa0 + x), va = ds_read128<2 * TILE * D>(ka0 + x);
+      lgkm_wait<0>();
+      hold(ha);
+      hold(va);
+      dp = H::mfma(ha, va, dp);
+      hold(dp);
+    });
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // step()'s dS~, in place of dP'
+      const f32x4 gv = *(const f32x4*)&Gb[8 * j + 4 * hi];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dp[4 * j + i] = st[4 * j + i] * fmaf(dp[4 * j + i], ivs, -gv[i]);
+    }
+    f32x16 dl = f32x16{};
+    static_for<NKD>([&](auto kc) {
+      constexpr int kd = decltype(kc)::value;
+      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
+      u32x4 la = ds_read128<0>(la0 + x), va = ds_read128<2 * TILE * D>(ka0 + x);
+      lgkm_wait<0>();
+      hold(la);
+      hold(va);
+      dl = H::mfma(la, va, dl);
+      hold(dl);
+    });
+    // dS~_e - float16(dS~) = (dS~ - float16(dS~)) + P~ (dO'_lo V'^T) / v
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const uint32_t ws = H::pack2(dp[r], dp[r + 1]), wp = pk[r >> 3][(r & 7) >> 1], wl = plo[r >> 3][(r & 7) >> 1];
+      const float p0 = H::to_f32(wp & 0xffffu) + H::to_f32(wl & 0xffffu);
+      const float p1 = H::to_f32(wp >> 16) + H::to_f32(wl >> 16);
+      slo[r >> 3][(r & 7) >> 1] = H::pack2(fmaf(p0 * dl[r], ivs, dp[r] - H::to_f32(ws & 0xffffu)),
+                                           fmaf(p1 * dl[r + 1], ivs, dp[r + 1] - H::to_f32(ws >> 16)));
+    }
+    const uint32_t qb0 = lds_addr(Q0), lb = lds_addr(DL);
+    static_for<2 * NMD>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD;
+      const uint32_t xm = 2 * (uint32_t)opaque((32 * mt) ^ tzo);
+      const uint32_t x0 = 2 * (uint32_t)tb0 + xm, x1 = 2 * (uint32_t)tb1 + xm;
+      u32x2 h0 = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x0), h1 = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x1);
+      u32x2 q0 = ds_read_tr8<32 * ks * D>(qb0 + x0), q1 = ds_read_tr8<32 * ks * D>(qb0 + x1);
+      u32x2 l0 = ds_read_tr8<32 * ks * D>(lb + x0), l1 = ds_read_tr8<32 * ks * D>(lb + x1);
+      lgkm_wait<0>();
+      hold(h0);
+      hold(h1);
+      hold(q0);
+      hold(q1);
+      hold(l0);
+      hold(l1);
+      dv[mt] = H::mfma(u32x4{h0[0], h0[1], h1[0], h1[1]}, plo[ks], dv[mt]);
+      hold(dv[mt]);
+      dv[mt] = H::mfma(u32x4{l0[0], l0[1], l1[0], l1[1]}, pk[ks], dv[mt]);
+      hold(dv[mt]);
+      dk[mt] = H::mfma(u32x4{q0[0], q0[1], q1[0], q1[1]}, slo[ks], dk[mt]);
+      hold(dk[mt]);
+    });
+  };
+  // SPLIT: the column's split sub-blocks (every wave finds the same ones: a
+  // ballot over the column list of each query head, 64 entries at a time),
+  // each loaded into buffer 0 and DL as launch() loads a sub-block, then
+  // correct() in that sub-block's scales.  The K' / V' tiles are resident.
+  auto split_pass = [&]() {
+    for (int g = 0; g < a.G; ++g) {
+      const int h = hk * a.G + g;
+      const int mc = map_row(a, b, h, a.nkt, kt);
+      const int c0 = a.col_ptr[mc], c1 = a.col_ptr[mc + 1];
+      const int64_t hb = (int64_t)b * a.Hq + h;
+      for (int base = c0; base < c1; base += 64) {
+        const int idx = min(base + lane, c1 - 1);
+        const int qt_l = a.col_ent[2 * idx], mk_l = a.col_ent[2 * idx + 1];
+        const float as_l = a.asc[hb * a.nqt + qt_l];
+        uint64_t todo = __ballot(base + lane < c1 && as_l < 0.f);
+        while (todo) {
+          const int j = __builtin_ctzll(todo);
+          todo &= todo - 1;
+          const int qt = __builtin_amdgcn_readlane(qt_l, j), mid = __builtin_amdgcn_readlane(mk_l, j);
+          const float sp_s = -__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, as_l), j));
+          const float sp_r = a.qsc[hb * a.nqt + qt];
+          for (int half = 0; half < 2; ++half) {
+            const int q0 = qt * TILE + half * BM;
+            const int64_t rows = (hb * hrows + q0) * D;
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+              lds_load16((const char*)(a.qh + rows) + qld[k], Q0 + wofs + k * BLK);
+              lds_load16((const char*)(a.doh + rows) + qld[k], H0 + wofs + k * BLK);
+              lds_load16((const char*)(a.dol + rows) + qld[k], DL + wofs + k * BLK);
+            }
+            if (mid >= 0 && wv < 4) {
+              const uint32_t* src = (const uint32_t*)(a.col_bits + ((int64_t)mid * 2 + half) * TILE + wv * 32);
+              __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void*)(M0 + wv * 32),
+                                               4, 0, 0);
+            }
+            if (wv >= 6)
+              __builtin_amdgcn_global_load_lds((wv == 6 ? a.lsf : a.delta) + hb * a.Lq + min(q0 + lane, a.Lq - 1),
+                                               (__attribute__((address_space(3))) void*)(wv == 6 ? L0 : G0), 4, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (sp_s != acc_s || sp_r != acc_r) {  // the sub-block's scales, as step() takes them
+              const float fv = sp_s / acc_s, fk = fv * (sp_r / acc_r);
+#pragma unroll
+              for (int i = 0; i < NMD; ++i) { dv[i] *= fv; dk[i] *= fk; }
+              acc_s = sp_s;
+              acc_r = sp_r;
+              m2c = c2 * pow2_rcp(sp_r * ksc);
+            }
+            correct(mid >= 0);
+            __syncthreads();  // buffer 0 and DL are read: the next loads may come
+          }
+        }
+      }
+    }
+  };
+
   // sub-block s computes from buffer s % 2 while s + 1 loads into the other;
   // the loop is unrolled by two so that every buffer index is static
   auto iter = [&](int s, auto bufc) {
@@ -403,6 +596,7 @@ void bwd_dkdv_mfma(KArgs a) {
     if constexpr (DS) {
       if (dpend) store_ds();  // sub-block s - 1's fragments
     }
+    any_split |= BUF ? sp1 : sp0;
     step(bufc, masked);
   };
   if (tot > 0) {
@@ -411,7 +605,13 @@ void bwd_dkdv_mfma(KArgs a) {
     static_for<2 * NS>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
     dma_on = false;
   }
-  {
+  if constexpr (SPLIT) {
+    ksc = a.ksc[col];
+    ivs = pow2_rcp(a.vsc[col]);
+    m2c = c2 * pow2_rcp(acc_r * ksc);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's K' and V' loads have landed
+    barrier_lds();                               // the K' / V' tiles are complete
+  } else {
     // K' tile: float16 times the tile's copy_scale, into the resident LDS tile
     // and to kh for the dQ kernel.  4 threads per key row.  The tile's max
     // |K| meets through an LDS-only barrier (the V' and first sub-block loads
@@ -446,11 +646,29 @@ void bwd_dkdv_mfma(KArgs a) {
   }
   if (tot > 0) {  // the first sub-block's scales, loaded with its entry
     cur_r = rh0 = first_r;
-    cur_s = sh0 = first_s;
+    cur_s = first_s;
+    sh0 = fabsf(first_s);
+    sp0 = first_s < 0.f;
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});
+  }
+  // the column's unrounded dK, dV (units of 1): wave kg's [2][NMD][64][16]
+  // floats of its 32 keys, dK then dV, each lane's 16 registers of an MFMA
+  // tile contiguous
+  float* const part = a.kvp + ((int64_t)col * 8 + 2 * kg) * (NMD * 16 * 64);
+  if constexpr (SPLIT) {
+    if (qh == 0) {  // the first kernel's sums (the other query half starts from zero)
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt) {
+        dk[mt] = *(const f32x16*)&part[(mt * 64 + lane) * 16];
+        dv[mt] = *(const f32x16*)&part[((NMD + mt) * 64 + lane) * 16];
+      }
+    }
+    split_pass();
+  } else {
+    if (tid == 0) a.scol[col] = any_split ? 1 : 0;
   }
 
   // dK / dV: the second query half's partials join the first's through LDS
@@ -483,7 +701,7 @@ void bwd_dkdv_mfma(KArgs a) {
   barrier_lds();
   if (qh == 0) {
     // the slabs are this wave's alone: the rows overwrite them after the reads
-    auto finish = [&](f32x16 (&acc)[NMD], float* red, float sc) {
+    auto finish = [&](f32x16 (&acc)[NMD], float* red, float sc, float unit, float* keep) {
 #pragma unroll
       for (int mt = 0; mt < NMD; ++mt)
 #pragma unroll
@@ -492,6 +710,12 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[mt][4 * c + j] += x[j];
         }
+      if constexpr (!SPLIT) {
+        if (any_split) {  // for the split kernel, in units of 1 (powers of two: exact)
+#pragma unroll
+          for (int mt = 0; mt < NMD; ++mt) *(f32x16*)&keep[(mt * 64 + lane) * 16] = acc[mt] * unit;
+        }
+      }
       uint16_t* o = (uint16_t*)red + l32 * OR;
 #pragma unroll
       for (int mt = 0; mt < NMD; ++mt) {
@@ -502,8 +726,8 @@ void bwd_dkdv_mfma(KArgs a) {
                     E::pack2(acc[mt][4 * j + 2] * sc, acc[mt][4 * j + 3] * sc)};
       }
     };
-    finish(dk, redk, a.scale * pow2_rcp(acc_s * acc_r));
-    finish(dv, redv, pow2_rcp(acc_s));
+    finish(dk, redk, a.scale * pow2_rcp(acc_s * acc_r), pow2_rcp(acc_s * acc_r), part);
+    finish(dv, redv, pow2_rcp(acc_s), pow2_rcp(acc_s), part + NMD * 16 * 64);
   }
   barrier_lds();
   constexpr int CPR = D / 8;  // 16-byte chunks per row
@@ -528,20 +752,22 @@ void bwd_dkdv_mfma(KArgs a) {
 // launcher
 // ---------------------------------------------------------------------------
 
-template <bool DS>
-static void launch_dkdv_t(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
-  if (dtype == MATTN_BF16) {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, bf16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, bf16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
-  } else {
-    if (D == 64) hipLaunchKernelGGL((bwd_dkdv_mfma<64, f16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dkdv_mfma<128, f16_tag, DS>), dim3(grid), dim3(512), 0, st, a);
-  }
+template <int D, class Tag>
+static void launch_dkdv_t(const KArgs& a, int grid, hipStream_t st) {
+  if (a.ds) hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, true, false>), dim3(grid), dim3(512), 0, st, a);
+  else hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, false, false>), dim3(grid), dim3(512), 0, st, a);
+  // the columns that met a split tile again (the others' workgroups return at once)
+  hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, false, true>), dim3(grid), dim3(512), 0, st, a);
 }
 
 hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
-  if (a.ds) launch_dkdv_t<true>(a, D, dtype, grid, st);
-  else launch_dkdv_t<false>(a, D, dtype, grid, st);
+  if (dtype == MATTN_BF16) {
+    if (D == 64) launch_dkdv_t<64, bf16_tag>(a, grid, st);
+    else launch_dkdv_t<128, bf16_tag>(a, grid, st);
+  } else {
+    if (D == 64) launch_dkdv_t<64, f16_tag>(a, grid, st);
+    else launch_dkdv_t<128, f16_tag>(a, grid, st);
+  }
   return hipGetLastError();
 }
 

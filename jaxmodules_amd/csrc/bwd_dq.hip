@@ -32,7 +32,13 @@ namespace mattn {
 // reads are pipelined by hand (asm LDS reads one or two k-steps ahead of their
 // MFMAs, counted lgkmcnt waits), and the dQ rows leave through an LDS-staged
 // tile, 16 bytes per lane along each row.
-template <int D, class Tag>
+// SPLIT: the kernel serves the split query tiles (bwd_pre's negative asc)
+// and skips the others, which the SPLIT = false kernel (or bwd_dq_ds) serves.
+// Its products also take what float16 rounds off: dP'^T += V' dO'_lo^T (the
+// rounded-off part of dO' that bwd_pre left in dol, B operands read from
+// global memory per k-step) and dQ^T += K'^T dS~_lo^T, dS~_lo = dS~ -
+// float16(dS~), by one more MFMA against the same K'^T operand.
+template <int D, class Tag, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {
   using E = Elt<Tag>;
@@ -51,6 +57,7 @@ void bwd_dq_mfma(KArgs a) {
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  if ((a.asc[item] < 0.f) != SPLIT) return;             // a tile the other dQ kernel serves
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -67,6 +74,8 @@ void bwd_dq_mfma(KArgs a) {
   const float c2 = a.scale_log2;
 
   u32x4 qf[NKD], df[NKD];
+  // SPLIT: this lane's dO'_lo^T operands (read per use, from L1 / L2)
+  const uint16_t* dlq = a.dol + (((int64_t)b * a.Hq + h) * a.nqt * TILE + q) * D + 8 * hi;
   {
     // the padded rows of the copies are zero, so q needs no clamp here
     const int64_t row = ((int64_t)b * a.Hq + h) * a.nqt * TILE + q;
@@ -208,6 +217,22 @@ void bwd_dq_mfma(KArgs a) {
         hold(st);
         hold(dp);
       });
+      if constexpr (SPLIT) {  // dP'^T += V' dO'_lo^T, the dO'_lo^T operands loaded four at a time
+        static_for<NKD / 4>([&](auto gc) {
+          constexpr int g = decltype(gc)::value;
+          u32x4 dl[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dl[i] = *(const u32x4*)(dlq + 16 * (4 * g + i));
+          static_for<4>([&](auto ic) {
+            constexpr int i = decltype(ic)::value, kd = 4 * g + i;
+            va[0] = ds_read128<2 * BN * D + 64 * t * D>(ra + 2 * (uint32_t)((16 * kd) ^ rxo));
+            lgkm_wait<0>();
+            hold(va[0]);
+            dp = H::mfma(va[0], dl[i], dp);
+            hold(dp);
+          });
+        });
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[r] = fast_exp2(fmaf(st[r], mq, nlv));
       if (masked) {
@@ -216,12 +241,15 @@ void bwd_dq_mfma(KArgs a) {
         for (int r = 0; r < 16; ++r)
           st[r] = mask_zero(st[r], mask_ones(w32, r));
       }
-      u32x4 pk[2];
+      u32x4 pk[2], pl[2];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float d0 = st[r] * dp[r];
         const float d1 = st[r + 1] * dp[r + 1];
-        pk[r >> 3][(r & 7) >> 1] = H::pack2(d0, d1);
+        const uint32_t w = H::pack2(d0, d1);
+        pk[r >> 3][(r & 7) >> 1] = w;
+        if constexpr (SPLIT)  // the rounded-off parts (the differences are exact in float32)
+          pl[r >> 3][(r & 7) >> 1] = H::pack2(d0 - H::to_f32(w & 0xffffu), d1 - H::to_f32(w >> 16));
       }
       // dQ^T += K^T dS^T over the half's two k-steps, K^T by transposed reads
       u32x2 lo[PQ + 1], up[PQ + 1];
@@ -238,8 +266,13 @@ void bwd_dq_mfma(KArgs a) {
         lgkm_wait<2 * (i + PQ < 2 * NMD ? PQ : 2 * NMD - 1 - i)>();
         hold(lo[sl]);
         hold(up[sl]);
-        acc[mt] = H::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[kk], acc[mt]);
+        const u32x4 aop = u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]};
+        acc[mt] = H::mfma(aop, pk[kk], acc[mt]);
         hold(acc[mt]);
+        if constexpr (SPLIT) {
+          acc[mt] = H::mfma(aop, pl[kk], acc[mt]);
+          hold(acc[mt]);
+        }
       });
     });
   };
@@ -307,6 +340,7 @@ void bwd_dq_ds(KArgs a) {
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  if (a.asc[item] < 0.f) return;  // a split tile: bwd_dq_mfma<SPLIT> serves it
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -486,23 +520,23 @@ void bwd_dq_ds(KArgs a) {
 // launcher
 // ---------------------------------------------------------------------------
 
+template <int D, class Tag>
+static void launch_dq_t(const KArgs& a, int grid, hipStream_t st) {
+  // the tiles that are not split (from the stored dS, or recomputing), then
+  // the split ones (recomputing, with the rounded-off parts); each kernel's
+  // workgroups of the other kind return at once
+  if (a.ds) hipLaunchKernelGGL((bwd_dq_ds<D, Tag>), dim3(grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, false>), dim3(grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
+}
+
 hipError_t launch_dq(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {
-  if (a.ds) {
-    if (dtype == MATTN_BF16) {
-      if (D == 64) hipLaunchKernelGGL((bwd_dq_ds<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((bwd_dq_ds<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
-    } else {
-      if (D == 64) hipLaunchKernelGGL((bwd_dq_ds<64, f16_tag>), dim3(grid), dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((bwd_dq_ds<128, f16_tag>), dim3(grid), dim3(256), 0, st, a);
-    }
-    return hipGetLastError();
-  }
   if (dtype == MATTN_BF16) {
-    if (D == 64) hipLaunchKernelGGL((bwd_dq_mfma<64, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dq_mfma<128, bf16_tag>), dim3(grid), dim3(256), 0, st, a);
+    if (D == 64) launch_dq_t<64, bf16_tag>(a, grid, st);
+    else launch_dq_t<128, bf16_tag>(a, grid, st);
   } else {
-    if (D == 64) hipLaunchKernelGGL((bwd_dq_mfma<64, f16_tag>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((bwd_dq_mfma<128, f16_tag>), dim3(grid), dim3(256), 0, st, a);
+    if (D == 64) launch_dq_t<64, f16_tag>(a, grid, st);
+    else launch_dq_t<128, f16_tag>(a, grid, st);
   }
   return hipGetLastError();
 }

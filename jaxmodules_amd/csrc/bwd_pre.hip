@@ -8,13 +8,18 @@
 //              doh = dO * dsc (a power of two from the tile's max |dO|),
 //              delta = rowsum(O * doh), the tile's bounds on the dS the other
 //              two kernels form, and the dK/dV kernel's dS scale f of the tile
-//              as lse - log2(f), so that its exp2 yields f P (this file);
+//              as lse - log2(f), so that its exp2 yields f P (this file); in a
+//              split tile (the forward found a row whose largest weight
+//              reaches SPLIT_P) also what doh rounds off (dol), with delta
+//              from the unrounded dO, and the tile marked by a negative asc;
 //   bwd_dkdv : one workgroup per 128-key map column of (b, kv head); it walks
 //              the column's present query tiles for every query head of the
-//              GQA group and accumulates dK, dV in registers -- each element
-//              written exactly once, no atomics (bwd_dkdv.hip);
+//              GQA group and accumulates dK, dV in registers -- no atomics;
+//              a second kernel redoes the columns that met a split tile, with
+//              the products of what float16 rounded off there (bwd_dkdv.hip);
 //   bwd_dq   : one workgroup per 128-query map row; dQ accumulated in
-//              registers (bwd_dq.hip).
+//              registers; the split tiles' rows by a kernel of their own
+//              (bwd_dq.hip).
 // With P = exp2(scale_log2 * S - lse) and dS = P * (dO V^T - delta):
 //   dV = P^T dO,  dK = scale * dS^T Q,  dQ = scale * dS K.
 // Every product of the 16-bit paths runs on float16 operands (11 significant
@@ -107,16 +112,23 @@ void bwd_pre(KArgs a) {
   for (int t = tid; t < a.nkt; t += 512) vm = fmaxf(vm, a.vmax[tb + t]);
   const f32x2 m1 = block_max2_512(f32x2{mx, vm}, red);
   const float s = copy_scale(m1[0]);
-  // the float16 copy; delta and the row's L1 norm from doh exactly as rounded,
+  // A split tile (the forward found a row whose largest weight reaches
+  // SPLIT_P; uniform per workgroup) also keeps what the float16 copy rounds
+  // off, and its products in the other kernels see dO' unrounded.
+  const bool split = a.pmx != nullptr && a.pmx[tile] >= SPLIT_P;
+  // the float16 copy; delta and the row's L1 norm from doh exactly as the
+  // products see it (rounded, or with the rounded-off part in a split tile),
   // so that dS = P (dP - delta) cancels exactly where the exact dS is zero
   // (a row with a single allowed key) and its rounding error scales with V - O
-  uint32_t hp[PER / 2];
+  uint32_t hp[PER / 2], lp[PER / 2];
   float dl = 0.f, l1 = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; i += 2) {
-    hp[i / 2] = H::pack2(g[i] * s, g[i + 1] * s);
+    const float e0 = g[i] * s, e1 = g[i + 1] * s;  // exact: s is a power of two
+    hp[i / 2] = H::pack2(e0, e1);
     const float h0 = H::to_f32(hp[i / 2] & 0xffffu), h1 = H::to_f32(hp[i / 2] >> 16);
-    dl = fmaf(o[i], h0, fmaf(o[i + 1], h1, dl));
+    lp[i / 2] = H::pack2(e0 - h0, e1 - h1);  // the rounded-off parts (differences exact in float32)
+    dl = split ? fmaf(o[i], e0, fmaf(o[i + 1], e1, dl)) : fmaf(o[i], h0, fmaf(o[i + 1], h1, dl));
     l1 += fabsf(h0) + fabsf(h1);
   }
 #pragma unroll
@@ -124,29 +136,33 @@ void bwd_pre(KArgs a) {
     dl += __shfl_xor(dl, m);
     l1 += __shfl_xor(l1, m);
   }
-  // doh row: 16-byte stores, the row's 4 threads covering 64 contiguous bytes each time
-  uint16_t* wd = a.doh + ((int64_t)bh * (a.nqt * TILE) + q) * D;
-  if constexpr (CS == 8) {
-    // chunk j (8 values) -> 8 halves at 8 (part + 4 j)
+  // a row of halves: 16-byte stores, the row's 4 threads covering 64 contiguous bytes each time
+  auto store_row = [&](uint16_t* wd, const uint32_t* hv) {
+    if constexpr (CS == 8) {
+      // chunk j (8 values) -> 8 halves at 8 (part + 4 j)
 #pragma unroll
-    for (int j = 0; j < PER / 8; ++j)
-      *(u32x4*)(wd + 8 * (part + 4 * j)) = u32x4{hp[4 * j], hp[4 * j + 1], hp[4 * j + 2], hp[4 * j + 3]};
-  } else {
-    // chunk j (4 values) -> 4 halves at 4 (part + 4 j).  Threads p and p ^ 1
-    // swap one chunk of each pair (2k, 2k + 1): the even thread then holds the
-    // 8 halves at 16 (2k) + 4 p, the odd thread those at 16 (2k + 1) + 4 (p - 1).
-    const bool odd = part & 1;
+      for (int j = 0; j < PER / 8; ++j)
+        *(u32x4*)(wd + 8 * (part + 4 * j)) = u32x4{hv[4 * j], hv[4 * j + 1], hv[4 * j + 2], hv[4 * j + 3]};
+    } else {
+      // chunk j (4 values) -> 4 halves at 4 (part + 4 j).  Threads p and p ^ 1
+      // swap one chunk of each pair (2k, 2k + 1): the even thread then holds the
+      // 8 halves at 16 (2k) + 4 p, the odd thread those at 16 (2k + 1) + 4 (p - 1).
+      const bool odd = part & 1;
 #pragma unroll
-    for (int k = 0; k < PER / 8; ++k) {
-      const u32x2 c0 = {hp[4 * k], hp[4 * k + 1]};        // chunk 2k
-      const u32x2 c1 = {hp[4 * k + 2], hp[4 * k + 3]};    // chunk 2k + 1
-      const u32x2 send = odd ? c0 : c1;
-      const u32x2 recv = {(uint32_t)__shfl_xor((int)send[0], 1), (uint32_t)__shfl_xor((int)send[1], 1)};
-      const u32x4 w = odd ? u32x4{recv[0], recv[1], c1[0], c1[1]} : u32x4{c0[0], c0[1], recv[0], recv[1]};
-      const int h0 = odd ? 16 * (2 * k + 1) + 4 * (part - 1) : 16 * (2 * k) + 4 * part;
-      *(u32x4*)(wd + h0) = w;
+      for (int k = 0; k < PER / 8; ++k) {
+        const u32x2 c0 = {hv[4 * k], hv[4 * k + 1]};        // chunk 2k
+        const u32x2 c1 = {hv[4 * k + 2], hv[4 * k + 3]};    // chunk 2k + 1
+        const u32x2 send = odd ? c0 : c1;
+        const u32x2 recv = {(uint32_t)__shfl_xor((int)send[0], 1), (uint32_t)__shfl_xor((int)send[1], 1)};
+        const u32x4 w = odd ? u32x4{recv[0], recv[1], c1[0], c1[1]} : u32x4{c0[0], c0[1], recv[0], recv[1]};
+        const int h0 = odd ? 16 * (2 * k + 1) + 4 * (part - 1) : 16 * (2 * k) + 4 * part;
+        *(u32x4*)(wd + h0) = w;
+      }
     }
-  }
+  };
+  const int64_t crow = ((int64_t)bh * (a.nqt * TILE) + q) * D;
+  store_row(a.doh + crow, hp);
+  if (split) store_row(a.dol + crow, lp);
   const f32x2 st = block_max2_512(f32x2{l1, fabsf(dl)}, red);
   // |dS s| <= |dP s| + |delta s| <= max_q |doh_q|_1 max |V| + max |delta s|
   const float f = ds_scale(fmaf(st[0], m1[1], st[1]));
@@ -158,7 +174,7 @@ void bwd_pre(KArgs a) {
   if (tid == 0) {
     a.dsc[tile] = s;
     a.tst[tile] = float2{st[0], st[1]};
-    a.asc[tile] = f * s;
+    a.asc[tile] = split ? -(f * s) : f * s;  // the sign marks a split tile
   }
 }
 

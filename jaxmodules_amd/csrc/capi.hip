@@ -52,11 +52,13 @@ size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
 // Forward residual (16-bit inputs, D <= 128): V as float16 times a power of two per
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
 // [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
-// scale, and each V tile's max |V|.
+// scale, each V tile's max |V|, and each query tile's largest attention
+// weight (which makes it a split tile: forward and backward free of the
+// float16 rounding of their operands there).
 // MATTN_PRECISE on the SIMT kernels: what the stored lse and O round off
 // (float32, [B, Hq, Lq] and [B, Hq, Lq, D]), which the backward adds back.
 struct FwdWs {
-  size_t vh, qh, vsc, vmax, qsc, lse_lo, o_lo, total;
+  size_t vh, qh, vsc, vmax, qsc, pmx, lse_lo, o_lo, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
@@ -76,7 +78,8 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
   w.vsc = w.qh + align256(qtiles * MATTN_TILE_Q * p->D * 2);
   w.vmax = w.vsc + align256(ktiles * sizeof(float));
   w.qsc = w.vmax + align256(ktiles * sizeof(float));
-  w.total = w.qsc + align256(qtiles * sizeof(float));
+  w.pmx = w.qsc + align256(qtiles * sizeof(float));
+  w.total = w.pmx + align256(qtiles * sizeof(float));
   return w;
 }
 
@@ -84,9 +87,13 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
 // (the MFMA kernels) also the
 // shifted lse (f32 per query row), the float16 copies dO' ([B, Hq, nqt * 128,
 // D]) and K' ([B, Hkv, nkt * 128, D]), and per 128-row tile the dO' scale, the
-// dS bounds and scale of the query tiles and the K' scale of the key tiles.
+// dS bounds and scale of the query tiles and the K' scale of the key tiles;
+// then the rounded-off part of dO' ([B, Hq, nqt * 128, D] float16, written and
+// read only in the rows of split tiles), a flag per key tile (its dK/dV
+// column met a split tile) and such a column's unrounded dK and dV (float32,
+// [ktiles][2][128][D], written and read only for those columns).
 struct WsLayout {
-  size_t delta, lsf, doh, kh, dsc, tst, asc, ksc, total;
+  size_t delta, lsf, doh, kh, dsc, tst, asc, ksc, dol, scol, kvp, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
@@ -104,7 +111,10 @@ WsLayout ws_layout(const mattn_problem* p) {
   w.tst = w.dsc + align256(qtiles * sizeof(float));
   w.asc = w.tst + align256(qtiles * 8);
   w.ksc = w.asc + align256(qtiles * sizeof(float));
-  w.total = w.ksc + align256(ktiles * sizeof(float));
+  w.dol = w.ksc + align256(ktiles * sizeof(float));
+  w.scol = w.dol + align256(qtiles * MATTN_TILE_Q * p->D * 2);
+  w.kvp = w.scol + align256(ktiles * sizeof(int));
+  w.total = w.kvp + align256(ktiles * MATTN_TILE_K * p->D * 2 * sizeof(float));
   return w;
 }
 
@@ -254,6 +264,7 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
     a.vmax = (float*)(ws + w.vmax);
     a.qsc = (float*)(ws + w.qsc);
     a.qh = (p->flags & MATTN_FWD_FOR_BWD) ? (uint16_t*)(ws + w.qh) : nullptr;
+    a.pmx = (float*)(ws + w.pmx);
   }
   hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, simt_path(p), bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
@@ -302,6 +313,9 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.tst = (float2*)(ws + w.tst);
     a.asc = (float*)(ws + w.asc);
     a.ksc = (float*)(ws + w.ksc);
+    a.dol = (uint16_t*)(ws + w.dol);
+    a.scol = (int*)(ws + w.scol);
+    a.kvp = (float*)(ws + w.kvp);
     const FwdWs r = fwd_ws_layout(p);
     const char* res = (const char*)residual;
     a.vh = (uint16_t*)(res + r.vh);
@@ -309,6 +323,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.vsc = (float*)(res + r.vsc);
     a.vmax = (float*)(res + r.vmax);
     a.qsc = (float*)(res + r.qsc);
+    a.pmx = (float*)(res + r.pmx);
     if (ds_path(p)) {  // dS after the workspace's other parts (w.total is 256-byte aligned)
       a.ds = (uint16_t*)(ws + w.total);
       a.col_row = bm->col_row;

@@ -98,7 +98,27 @@ struct KArgs {
   int precise;         // MATTN_PRECISE: the SIMT kernels form the scores as compensated dot products
   float* lse_lo;       // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq], (m + log2 l) - lse
   float* o_lo;         // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq, D], exact O - stored O
+  // Split tiles (MFMA path): per query tile the largest attention weight of
+  // any of its rows (forward residual, written with qh).  A tile whose
+  // largest weight reaches SPLIT_P is a split tile: bwd_pre stores the part
+  // of dO' that float16 rounds off (dol, [B, Hq, nqt*128, D], only such
+  // tiles' rows), takes delta from the unrounded dO and marks the tile by a
+  // negative asc; the dK/dV and dQ kernels then add the products of those
+  // rounded-off parts (of dO', P and dS), so that the tile's terms enter the
+  // gradients with 22 significant bits instead of 11.
+  float* pmx;
+  uint16_t* dol;
+  int* scol;           // [B*Hkv*nkt] per dK/dV column: its walk met a split tile
+  float* kvp;          // [B*Hkv*nkt][2][128][D] such a column's unrounded dK, dV (units of 1)
 };
+
+// Largest attention weight from which a query tile is a split tile.  Rows
+// whose weights are all below it put each key's gradient terms on many
+// queries, whose float16 rounding errors average out below the parity
+// gate's float32-accumulation slack; rows with a dominant key do not (a
+// bfloat16 gradient one ulp off where the exact value lies near a rounding
+// midpoint).
+constexpr float SPLIT_P = 0.125f;
 
 // dS storage slot base of (b, h): the map's entries are shared by the (b, h)
 // it broadcasts over, each of which has slots of its own

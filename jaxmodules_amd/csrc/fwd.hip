@@ -17,7 +17,9 @@
 // dP - delta = sum_j w_j (dP - dP_j) in the backward, without the rounding of
 // the normaliser, which rows dominated by one key would carry into dS.
 // When the backward will run, the workgroup also writes its 128 Q rows as
-// float16 times a power of two (qh, qsc): they are in registers here anyway.
+// float16 times a power of two (qh, qsc): they are in registers here anyway,
+// and the largest attention weight of its rows (pmx: the backward splits
+// float16 operands in tiles where it reaches SPLIT_P).
 // K and V' are double-buffered in LDS; the next sub-block's global loads are
 // in flight while the current one is computed.  K and V' tiles are moved by
 // direct global->LDS loads into swizzled row-major tiles; V'^T operands are
@@ -67,7 +69,16 @@ void cvt_v(KArgs a) {
   }
 }
 
-template <int D, class Tag, bool OUT_F32>
+// SPLIT: the kernel launched after the main one (SPLIT = false) for the
+// split tiles, the query tiles whose rows put a weight of at least SPLIT_P on
+// a key (pmx; its other workgroups return at once).  It walks such a row
+// again and overwrites O and the lse with values free of the float16
+// rounding of P: the row sum adds the unrounded weights, and O^T += V'^T P^T
+// takes P as float16(P) + the rounded-off part, by one more MFMA against the
+// same V'^T operand.  The backward's exp(S - lse) is then the exact softmax
+// of these rows, and O the exact convex combination under it, which its
+// split-tile products need.
+template <int D, class Tag, bool OUT_F32, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
   using E = Elt<Tag>;
@@ -86,10 +97,13 @@ void fwd_mfma(KArgs a) {
   // loads landing in one buffer cannot alias the reads of the other
   __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
-  __shared__ float QM[4];  // per-wave max |Q| (the float16 Q copy's scale)
+  __shared__ float QM[4];  // per wave: max |Q| (the float16 Q copy's scale), at the end the largest weight
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
+  if constexpr (SPLIT) {
+    if (!(a.pmx[item] >= SPLIT_P)) return;  // not a split tile: the main kernel's O and lse stand
+  }
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -113,7 +127,7 @@ void fwd_mfma(KArgs a) {
 #pragma unroll
     for (int kd = 0; kd < NKD; ++kd) qf[kd] = *(const u32x4*)(qp + 16 * kd);
   }
-  if (a.qh != nullptr) {
+  if (!SPLIT && a.qh != nullptr) {
     // float16 copy of the tile's Q rows for the backward (rows past Lq zero)
     float m = 0.f;
 #pragma unroll
@@ -208,6 +222,7 @@ void fwd_mfma(KArgs a) {
 #pragma unroll
   for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
   float m2 = NEG_INF, l = 0.f;  // running max (base-2 units) and partial row sum
+  float mtr = NEG_INF;          // the row's exact max (m2 trails it by up to RESCALE_SLACK)
   float nu = 1.f;               // V' scale the accumulators are in: acc = nu * sum P V
 
   auto step = [&](auto bufc, bool masked, float snu) {
@@ -266,6 +281,7 @@ void fwd_mfma(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
     const float mx2 = wave_max32(mx) * c2;
+    mtr = fmaxf(mtr, mx2);
     // a new V' tile scale (uniform) is folded into the same rescale
     if (snu != nu || __any(mx2 > m2 + RESCALE_SLACK)) {
       const float mn = fmaxf(m2, mx2);
@@ -278,7 +294,7 @@ void fwd_mfma(KArgs a) {
       nu = snu;
     }
     const float nmu = (m2 == NEG_INF) ? 0.f : -m2;
-    u32x4 pk[4];
+    u32x4 pk[4], plo[4];
     const f16x2 one2 = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -287,8 +303,14 @@ void fwd_mfma(KArgs a) {
         const float p0 = fast_exp2(fmaf(st[t][r], c2, nmu));
         const float p1 = fast_exp2(fmaf(st[t][r + 1], c2, nmu));
         const uint32_t w = H::pack2(p0, p1);
-        // the row sum of the rounded values the product uses (v_dot2_f32_f16)
-        l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one2, l, false);
+        if constexpr (SPLIT) {  // the unrounded sum, and what float16 rounds off P
+          l += p0;
+          l += p1;
+          plo[2 * t + (r >> 3)][(r & 7) >> 1] = H::pack2(p0 - H::to_f32(w & 0xffffu), p1 - H::to_f32(w >> 16));
+        } else {
+          // the row sum of the rounded values the product uses (v_dot2_f32_f16)
+          l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one2, l, false);
+        }
         pk[2 * t + (r >> 3)][(r & 7) >> 1] = w;
       }
     }
@@ -310,8 +332,13 @@ void fwd_mfma(KArgs a) {
         lgkm_wait<2 * (i + PV < 4 * NMD ? PV : 4 * NMD - 1 - i)>();
         hold(lo[sl]);
         hold(up[sl]);
-        acc[mt] = H::mfma(u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]}, pk[ks], acc[mt]);
+        const u32x4 aop = u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]};
+        acc[mt] = H::mfma(aop, pk[ks], acc[mt]);
         hold(acc[mt]);
+        if constexpr (SPLIT) {
+          acc[mt] = H::mfma(aop, plo[ks], acc[mt]);
+          hold(acc[mt]);
+        }
       });
     }
   };
@@ -342,9 +369,16 @@ void fwd_mfma(KArgs a) {
   const float inv = l > 0.f ? 1.f / (l * nu) : 0.f;
   if (hi == 0 && q < a.Lq)
     a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
+  if (!SPLIT && a.pmx != nullptr) {  // the tile's largest attention weight: exp2(max - lse) of its rows
+    float pm = l > 0.f ? fast_exp2(mtr - (m2 + __builtin_log2f(l))) : 0.f;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
+    if (lane == 0) QM[wave] = pm;
+  }
   // O through LDS (one K / V buffer per wave, free once every wave is done)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (!SPLIT && a.pmx != nullptr && tid == 0) a.pmx[item] = fmaxf(fmaxf(QM[0], QM[1]), fmaxf(QM[2], QM[3]));
   uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * BN * D;
   static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
   const int r0 = qt * TILE + 32 * wave;
@@ -360,10 +394,13 @@ void fwd_mfma(KArgs a) {
 template <int D, class Tag>
 static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStream_t st) {
   hipLaunchKernelGGL((cvt_v<D, Tag>), dim3(a.B * a.Hkv * a.nkt), dim3(512), 0, st, a);
-  if (out_f32)
-    hipLaunchKernelGGL((fwd_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((fwd_mfma<D, Tag, false>), dim3(grid), dim3(256), 0, st, a);
+  if (out_f32) {
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, true, false>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, true, true>), dim3(grid), dim3(256), 0, st, a);  // split tiles again
+  } else {
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, false, false>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((fwd_mfma<D, Tag, false, true>), dim3(grid), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

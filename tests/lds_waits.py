@@ -14,8 +14,11 @@ inline asm may be outstanding at a backward branch (a loop's back edge), so
 a loop header needs only the state of the path that enters it; the compiler's
 own reads pending at a back edge are then not tracked into the loop, which
 hides no newer read (older operations retire first).
-An ``lgkmcnt(N > 0)`` wait while a scalar-memory load is outstanding (those
-complete out of order) is reported as well.
+Scalar-memory loads share the counter but complete out of order: an
+``lgkmcnt(N)`` only guarantees that at most N operations are outstanding,
+which may all be LDS reads, so it retires every LDS operation older than the
+N most recent LDS operations (scalar loads not counted), and retires scalar
+loads only at N = 0.
 
 ``check_dma`` checks the other counter: every global->LDS load (the ``lds``
 forms of ``global_load`` / ``buffer_load``) must have retired at the next
@@ -108,11 +111,12 @@ def check(lines: list) -> tuple:
             m = re.search(r"lgkmcnt\((\d+)\)", t)
             if m or re.fullmatch(r"s_waitcnt\s+0", t):
                 lim = int(m.group(1)) if m else 0
-                for st in states:
-                    if lim > 0 and any(k == "smem" for k, _, _ in st):
-                        problems.append(f"line {n}: lgkmcnt({lim}) with a scalar load outstanding")
-                    while len(st) > lim:
-                        st.pop(0)
+                for i, st in enumerate(states):
+                    if lim == 0:
+                        st.clear()
+                        continue
+                    keep = [e for e in st if e[0] != "smem"][-lim:]
+                    states[i] = [e for e in st if e[0] == "smem" or any(e is x for x in keep)]
             continue
         store = op.startswith(("ds_write", "global_store", "buffer_store", "scratch_store"))
         has_dst = (op.startswith(("v_", "ds_read", "ds_bpermute", "global_load", "buffer_load", "scratch_load"))

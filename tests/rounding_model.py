@@ -12,7 +12,13 @@ roundings).  Two designs are modelled:
   float32 O and the float16 dO;
 * ``"bfloat16"`` -- the earlier operand choice for bfloat16 inputs: P in the
   input dtype for P V with the normaliser from the unrounded P, dS in
-  bfloat16 for dK and dQ, and dQ's dP from dO rounded to bfloat16.
+  bfloat16 for dK and dQ, and dQ's dP from dO rounded to bfloat16;
+* ``"split"`` -- the float16 design with split tiles, as the kernels run it
+  now: a 128-row query tile whose rows put a weight of at least SPLIT_P on a
+  key has its O and lse formed again from unrounded weights and their sum,
+  and enters the backward with its float16 operands' rounded-off parts (dO,
+  P and dS to 22 significant bits, i.e. unrounded here) and delta from the
+  unrounded dO; the other tiles as ``"float16"``.
 
 Operands the kernels scale by a power of two before rounding (dO, the
 backward's P and dS) are rounded to float16's 11 significant bits without its
@@ -54,6 +60,21 @@ def _expand(X, Hq):
     return np.repeat(X, Hq // X.shape[2], axis=2)
 
 
+SPLIT_P = 0.125  # largest weight from which a query tile is split (common.hpp SPLIT_P)
+TILE = 128
+
+
+def split_rows(P):
+    """[B, Hq, N] booleans: the rows of split query tiles (P: [B, Hq, N, L] weights)."""
+    B, Hq, N, _ = P.shape
+    pm = P.max(-1)
+    nt = -(-N // TILE)
+    pad = np.zeros((B, Hq, nt * TILE))
+    pad[..., :N] = pm
+    tile = pad.reshape(B, Hq, nt, TILE).max(-1) >= SPLIT_P
+    return np.repeat(tile, TILE, axis=-1)[..., :N]
+
+
 def kernel_model(Q, K, V, dO, allowed, scale, dtype, design="float16"):
     """(O float32, dQ, dK, dV in dtype) for inputs already rounded to dtype and
     dO in float32; allowed is the [B, Hq, N, L] effective mask."""
@@ -73,16 +94,22 @@ def kernel_model(Q, K, V, dO, allowed, scale, dtype, design="float16"):
         Ph = round_to(Pu, dtype)
         l = Pu.sum(-1, keepdims=True)
     ls = np.where(l > 0, l, 1.0)
+    split = split_rows(Pu / ls) if design == "split" else np.zeros(Pu.shape[:3], bool)
+    sq = split[..., None]                       # [B, Hq, N, 1]
+    if design == "split":  # split rows: the forward again with unrounded weights and their sum
+        Ph = np.where(sq, Pu, Ph)
+        ls = np.where(sq, Pu.sum(-1, keepdims=True), ls)
+        ls = np.where(ls > 0, ls, 1.0)
     O = round_to(np.einsum("bhqk,bkhd->bqhd", Ph, Vx) / ls.transpose(0, 2, 1, 3), "float32")
     P = Pu / ls                                 # the backward's exp(S - lse)
-    dOh = sig11(dO)
+    dOh = np.where(np.transpose(split, (0, 2, 1))[..., None], np.asarray(dO, np.float64), sig11(dO))
     Ot = np.transpose(O, (0, 2, 1, 3))
     delta = (np.transpose(dOh, (0, 2, 1, 3)) * Ot).sum(-1)[..., None]
     dP = np.einsum("bqhd,bkhd->bhqk", dOh, Vx)
     dS = P * (dP - delta)
-    dVx = np.einsum("bhqk,bqhd->bkhd", sig11(P), dOh)
-    if design == "float16":
-        dSk = dSq = sig11(dS)
+    dVx = np.einsum("bhqk,bqhd->bkhd", np.where(sq, P, sig11(P)), dOh)
+    if design in ("float16", "split"):
+        dSk = dSq = np.where(sq, dS, sig11(dS))
     else:
         dSk = bf16(dS)
         dO16 = bf16(dO)

@@ -130,14 +130,18 @@ def test_workspace_bytes(lib):
     """The documented layouts.  Backward workspace: delta, then (16-bit
     inputs) the shifted lse, float16 dO' padded to whole 128-row tiles per
     head, float16 K' per kv-head tile, and per tile the dO' scale, dS bounds
-    (2 floats), dS scale and K' scale.  Forward residual: float16 V' and Q', then V' scales and maxima and
-    Q' scales."""
+    (2 floats), dS scale and K' scale; then for the split tiles the
+    rounded-off part of dO' (float16, like dO'), a flag per key tile and the
+    unrounded dK and dV of a key tile (float32, 2 x 128 x D per key tile).
+    Forward residual: float16 V' and Q', then V' scales and maxima, Q' scales
+    and each query tile's largest attention weight."""
     align = lambda x: (x + 255) // 256 * 256
     B, L, Hq, Hkv, D = 2, 300, 8, 2, 128
     nqt = -(-L // 128)
     qtiles, ktiles = B * Hq * nqt, B * Hkv * nqt
     want = (2 * align(B * Hq * L * 4) + align(qtiles * 128 * D * 2) + align(ktiles * 128 * D * 2)
-            + align(qtiles * 4) + align(qtiles * 8) + align(qtiles * 4) + align(ktiles * 4))
+            + align(qtiles * 4) + align(qtiles * 8) + align(qtiles * 4) + align(ktiles * 4)
+            + align(qtiles * 128 * D * 2) + align(ktiles * 4) + align(ktiles * 2 * 128 * D * 4))
     p = _problem()
     assert lib.mattn_workspace_bytes(ctypes.byref(p)) == want
     p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
@@ -145,7 +149,7 @@ def test_workspace_bytes(lib):
     p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
     assert lib.mattn_workspace_bytes(ctypes.byref(p32)) == align(B * Hq * L * 4)
     res = (align(ktiles * 128 * D * 2) + align(qtiles * 128 * D * 2) + 2 * align(ktiles * 4)
-           + align(qtiles * 4))
+           + 2 * align(qtiles * 4))
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == res
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p32)) == 0
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
@@ -283,7 +287,7 @@ def test_library_missing_raises(monkeypatch, tmp_path):
 def test_noalloc_rejects_before_any_device_call(lib):
     """mattn_bwd_noalloc checks the problem and its workspace size against the
     static scratch on the host, before it touches a device."""
-    n, h = 32768, 32                     # dO' and K' copies: 2 x 256 MiB
+    n, h = 32768, 32                     # dO', its rounded-off part and K' copies: 3 x 256 MiB
     p = _problem(B=1, Lq=n, Lk=n, Hq=h, Hkv=h)
     for name in ("q", "k", "v", "dq", "dk", "dv", "o", "do"):
         setattr(p, f"{name}_stride", (ctypes.c_int64 * 3)(n * h * 128, h * 128, 128))
@@ -326,6 +330,10 @@ def test_stored_ds_default_stays_within_its_cap(lib):
             lib.mattn_workspace_bytes(ctypes.byref(p))
         assert extra <= A.DS_MAX_BYTES
         if not keeps:
-            # the recomputing backward's workspace: O(L) per head (delta, shifted lse,
-            # the float16 dO and K copies, per-tile scales)
-            assert lib.mattn_workspace_bytes(ctypes.byref(p)) < 2 * L * 32 * 128 * 2 + (8 << 20)
+            # the recomputing backward's workspace: O(L) per head -- per query row
+            # delta and the shifted lse (8 bytes) and the float16 dO' and its
+            # rounded-off part (4 D bytes), per key row the float16 K' (2 D bytes)
+            # and the split columns' float32 dK and dV (8 D bytes), plus per-tile
+            # scales and flags
+            rows = L * 32
+            assert lib.mattn_workspace_bytes(ctypes.byref(p)) < rows * (8 + 4 * 128) + rows * 10 * 128 + (8 << 20)
