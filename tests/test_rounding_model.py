@@ -4,11 +4,13 @@ the fp64 oracle, under the gate of the GPU tests (tests/helpers.py):
 
 * the known draws of the 600-problem sweep exceed the gate with bfloat16 dS
   and dO operands (the earlier kernels) by far more than with float16 ones;
-* draws that miss the gate with float16 operands (on the GPU those are
-  reported xfailed through tests/helpers.Floor) miss it in the model too, every
-  miss within the float16 operands' error bound (the Floor criterion), while
-  the same arithmetic without the operand roundings meets the gate: the misses
-  are the floor of 16-bit operands, not a kernel error.
+* draws that miss the gate with float16 operands everywhere miss it in the
+  model too, every miss within the float16 operands' error bound (the Floor
+  criterion), while the same arithmetic without the operand roundings meets
+  the gate: the misses are the floor of 16-bit operands, not a kernel error;
+* the kernels' split tiles (query tiles whose largest weight reaches SPLIT_P
+  run with their operands' rounded-off parts) remove that floor: the
+  split-tile model meets the gate on those draws and on unit-variance inputs.
 """
 import math
 
@@ -124,3 +126,44 @@ def test_residue_dv_model_without_roundings_is_exact(monkeypatch):
     for key, col in [(0, 3), (70, 5), (599, 0), (64, 15)]:
         assert math.isclose(rm.residue_dv_model(Q, K, dO, P, key, col, 1 / math.sqrt(d))[0], dV[key, col],
                             rel_tol=1e-12, abs_tol=1e-14)
+
+
+@pytest.mark.parametrize("case", FLOOR_DRAWS, ids=[str(c[0]) for c in FLOOR_DRAWS])
+def test_split_tiles_meet_the_gate_on_floor_draws(case):
+    """The kernels' split tiles (rounding_model design "split": query tiles
+    whose largest weight reaches SPLIT_P run with their operands' rounded-off
+    parts) remove the float16 floor of these draws."""
+    seed, dtype = case
+    Q, K, V, dO, kw, scale, out = _draw(seed, dtype)
+    assert max(_ratios(*_model_outputs(Q, K, V, dO, kw, dtype, scale, "split", out), dtype)) <= 1.0
+
+
+@pytest.mark.parametrize("mask", ["causal", "docs", "window"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_split_tiles_meet_the_gate_on_unit_normal_inputs(mask, d):
+    """Unit-variance bfloat16 inputs (the reference tests' regime), float32 and
+    bfloat16 outputs: the float16 design misses the gate in some of these
+    cases, the split-tile design in none."""
+    from tests.test_regimes_gpu import _mask_kw
+
+    B, N, Hq, Hkv = 2, 300, 4, 2
+    Q, K, V, dO = seeded_inputs(B, N, N, Hq, Hkv, d, 4242 + N + d, scaled=False)
+    kw = _mask_kw(mask, N, 64)
+    for out in ("float32", "bfloat16"):
+        r = _ratios(*_model_outputs(Q, K, V, dO, kw, "bfloat16", 1 / math.sqrt(d), "split", out), "bfloat16")
+        assert max(r) <= 1.0, (out, r)
+
+
+def test_split_rows_are_whole_query_tiles():
+    """split_rows marks every row of a 128-row query tile in which some row
+    puts a weight of at least SPLIT_P on a key, and no other row."""
+    from tests import rounding_model as rm
+
+    P = np.full((1, 2, 300, 50), 0.01)
+    P[0, 0, 5, 3] = rm.SPLIT_P          # tile 0 of head 0
+    P[0, 1, 299, 0] = 0.9               # the last (partial) tile of head 1
+    P[0, 1, 130, 0] = rm.SPLIT_P * 0.99
+    s = rm.split_rows(P)
+    assert s.shape == (1, 2, 300)
+    assert s[0, 0, :128].all() and not s[0, 0, 128:].any()
+    assert s[0, 1, 256:].all() and not s[0, 1, :256].any()
