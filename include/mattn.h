@@ -78,7 +78,7 @@ enum mattn_status {
  * exactly), as float32 inputs do, instead of the MFMA kernels, whose
  * operands P, dS and dO are rounded to float16 (11 significant bits) -- except
  * in split tiles: 128-row query tiles with a row whose largest attention
- * weight reaches 1/8, whose O, lse and gradient terms the MFMA path forms
+ * weight reaches 1/32, whose O, lse and gradient terms the MFMA path forms
  * again with those operands' rounded-off parts (22 significant bits) by
  * kernels of their own, after the main ones.  Set it
  * for a forward and for its backward alike; the forward then has no residual.

@@ -118,7 +118,7 @@ struct KArgs {
 // gate's float32-accumulation slack; rows with a dominant key do not (a
 // bfloat16 gradient one ulp off where the exact value lies near a rounding
 // midpoint).
-constexpr float SPLIT_P = 0.125f;
+constexpr float SPLIT_P = 0.03125f;
 
 // dS storage slot base of (b, h): the map's entries are shared by the (b, h)
 // it broadcasts over, each of which has slots of its own

@@ -60,7 +60,7 @@ def _expand(X, Hq):
     return np.repeat(X, Hq // X.shape[2], axis=2)
 
 
-SPLIT_P = 0.125  # largest weight from which a query tile is split (common.hpp SPLIT_P)
+SPLIT_P = 1 / 32  # largest weight from which a query tile is split (common.hpp SPLIT_P)
 TILE = 128
 
 

@@ -7,8 +7,10 @@ reference's block window, packed documents, a per-head tile table, a
 head-specific lambda, or cross lengths.  The draw is fixed by the seed, so
 every run checks the same problems: seeds 0-23, the draws of a one-off
 600-problem run (seeds 24-623) that failed the gate with the kernels' earlier
-bfloat16 dS / dO operands (KNOWN_DRAWS), and the draws of two more one-off
-runs (seeds 624-1423) that missed it with float16 operands (LATER_DRAWS).
+bfloat16 dS / dO operands (KNOWN_DRAWS), the draws of two more one-off runs
+(seeds 624-1423) that missed it with float16 operands (LATER_DRAWS), and the
+draw of an 800-problem run (seeds 1424-2223) that missed it with split tiles
+at their first threshold (SPLIT_DRAWS).
 
 threshold_kernel is a softmax with scale 1 instead of 1/sqrt(d), so its
 draws see logits of unit variance (Q, K ~ N(0,1) d^-0.25), seven times
@@ -128,6 +130,17 @@ LATER_DRAWS = [647, 696, 976, 1060, 1067, 1073, 1120, 1193, 1201, 1246, 1271, 12
 
 @pytest.mark.parametrize("seed", LATER_DRAWS)
 def test_later_draw(seed):
+    run_draw(seed)
+
+
+# The one draw of a one-off 800-problem run (seeds 1424-2223) that missed the
+# gate with split tiles at a largest weight of 1/8: cross attention onto 12
+# keys, every weight about 1/12 (split tiles now start at 1/32).
+SPLIT_DRAWS = [2120]
+
+
+@pytest.mark.parametrize("seed", SPLIT_DRAWS)
+def test_split_draw(seed):
     run_draw(seed)
 
 
