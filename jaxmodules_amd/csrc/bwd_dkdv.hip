@@ -154,7 +154,11 @@ void bwd_dkdv_mfma(KArgs a) {
   // whether its query tile is a split tile (the sign of asc)
   float sh0 = 1.f, rh0 = 1.f, sh1 = 1.f, rh1 = 1.f;
   bool sp0 = false, sp1 = false;
-  bool any_split = false;  // the walk met a sub-block of a split tile
+  // the split rows among this wave's 32 queries of the sub-block in each
+  // buffer (srow), and whether the walk met a split row with an allowed key of
+  // this wave's 32 (then the split kernel redoes the column)
+  uint32_t sw0 = 0u, sw1 = 0u;
+  bool any_split = false;
   // buffer resources of the current query head's Q' and dO' slices
   const int64_t hrows = (int64_t)a.nqt * TILE;  // rows per head in the copies
   const uint32_t hbytes = (uint32_t)(hrows * D * 2);
@@ -237,6 +241,8 @@ void bwd_dkdv_mfma(KArgs a) {
     (BUF ? mid1 : mid0) = cur_mid;
     (BUF ? sh1 : sh0) = fabsf(cur_s);
     (BUF ? sp1 : sp0) = cur_s < 0.f;
+    if constexpr (!SPLIT)
+      (BUF ? sw1 : sw0) = cur_s < 0.f ? a.srow[((int64_t)(b * a.Hq + rh_head) * a.nqt + cur_qt) * 4 + 2 * lhalf + qh] : 0u;
     (BUF ? rh1 : rh0) = cur_r;
     nq0 = cur_qt * TILE + lhalf * BM;
     if (lhalf == 0) {
@@ -574,7 +580,11 @@ void bwd_dkdv_mfma(KArgs a) {
               acc_r = sp_r;
               m2c = c2 * pow2_rcp(sp_r * ksc);
             }
-            correct(mid >= 0);
+            {  // this wave's split rows of the sub-block, and their allowed keys among the wave's 32
+              const uint32_t ws = a.srow[(hb * a.nqt + qt) * 4 + 2 * half + qh];
+              const uint32_t w = mid >= 0 ? (uint32_t)(M0[kloc] >> (32 * qh)) : 0xffffffffu;
+              if (__any((w & ws) != 0u)) correct(mid >= 0);
+            }
             __syncthreads();  // buffer 0 and DL are read: the next loads may come
           }
         }
@@ -596,7 +606,10 @@ void bwd_dkdv_mfma(KArgs a) {
     if constexpr (DS) {
       if (dpend) store_ds();  // sub-block s - 1's fragments
     }
-    any_split |= BUF ? sp1 : sp0;
+    if (BUF ? sp1 : sp0) {  // a split tile: do split rows of this wave have allowed keys here?
+      const uint32_t w = masked ? (uint32_t)((BUF ? M1 : M0)[kloc] >> (32 * qh)) : 0xffffffffu;
+      any_split |= __any((w & (BUF ? sw1 : sw0)) != 0u);
+    }
     step(bufc, masked);
   };
   if (tot > 0) {
@@ -649,6 +662,8 @@ void bwd_dkdv_mfma(KArgs a) {
     cur_s = first_s;
     sh0 = fabsf(first_s);
     sp0 = first_s < 0.f;
+    if constexpr (!SPLIT)
+      sw0 = sp0 ? a.srow[((int64_t)(b * a.Hq + hk * a.G + (int)dA[1]) * a.nqt + (int)dB[1]) * 4 + qh] : 0u;
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
@@ -668,7 +683,7 @@ void bwd_dkdv_mfma(KArgs a) {
     }
     split_pass();
   } else {
-    if (tid == 0) a.scol[col] = any_split ? 1 : 0;
+    if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};  // (read after the barrier below)
   }
 
   // dK / dV: the second query half's partials join the first's through LDS
@@ -679,6 +694,12 @@ void bwd_dkdv_mfma(KArgs a) {
   // tiles with 16-byte accesses along the rows.
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (the dS~ stores of the sub-block before the last)
   barrier_lds();                               // every wave is done with the LDS
+  if constexpr (!SPLIT) {  // the column met a split row with an allowed key: the split kernel redoes it
+    any_split = false;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) any_split |= red[w][0] != 0.f;
+    if (tid == 0) a.scol[col] = any_split ? 1 : 0;
+  }
   if constexpr (DS) {
     if (dpend) store_ds();  // the last sub-block's fragments, in flight during the reduction below
   }

@@ -32,12 +32,14 @@ namespace mattn {
 // reads are pipelined by hand (asm LDS reads one or two k-steps ahead of their
 // MFMAs, counted lgkmcnt waits), and the dQ rows leave through an LDS-staged
 // tile, 16 bytes per lane along each row.
-// SPLIT: the kernel serves the split query tiles (bwd_pre's negative asc)
-// and skips the others, which the SPLIT = false kernel (or bwd_dq_ds) serves.
-// Its products also take what float16 rounds off: dP'^T += V' dO'_lo^T (the
-// rounded-off part of dO' that bwd_pre left in dol, B operands read from
-// global memory per k-step) and dQ^T += K'^T dS~_lo^T, dS~_lo = dS~ -
-// float16(dS~), by one more MFMA against the same K'^T operand.
+// SPLIT: the kernel launched after the other dQ kernel (SPLIT = false, or
+// bwd_dq_ds), which serves every row, for the split rows (srow; the
+// workgroups of tiles without one return at once): it walks the tile's
+// entries where a split row has an allowed key and overwrites the split rows'
+// dQ.  Its products also take what float16 rounds off: dP'^T += V' dO'_lo^T
+// (the rounded-off part of dO' that bwd_pre left in dol, B operands read from
+// global memory four k-steps at a time) and dQ^T += K'^T dS~_lo^T, dS~_lo =
+// dS~ - float16(dS~), by one more MFMA against the same K'^T operand.
 template <int D, class Tag, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {
@@ -55,15 +57,24 @@ void bwd_dq_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];
 
-  const int item = a.q_order[blockIdx.x];
+  // (the split kernel takes the launch order backwards: split tiles are
+  // mostly short rows, which the order puts last)
+  const int item = a.q_order[SPLIT ? gridDim.x - 1 - blockIdx.x : blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
-  if ((a.asc[item] < 0.f) != SPLIT) return;             // a tile the other dQ kernel serves
+  if (SPLIT && !(a.asc[item] < 0.f)) return;            // no split row: the other kernel's dQ stands
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
   const int mrow = map_row(a, b, h, a.nqt, qt);
   const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
-  const int nsb = 2 * (e1 - e0);
+  // SPLIT: only the entries where a split row has an allowed key
+  uint64_t need = ~0ull;
+  int nsb = 2 * (e1 - e0);
+  if constexpr (SPLIT) {
+    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
+    nsb = split_subblocks(need, e0, e1);
+  }
+  int ecur = e0 - 1;  // SPLIT: the entry of the last prepared sub-block
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -132,7 +143,12 @@ void bwd_dq_mfma(KArgs a) {
   float nks = 1.f, nvs = 1.f;   // its tile's K' and V' scales
   auto prep = [&](int s) {
     int kt;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask, ksc, vsc, nks, nvs);
+    int e = e0 + (s >> 1);
+    if constexpr (SPLIT) {  // the next entry the split rows need
+      if ((s & 1) == 0) ecur = split_next(need, ecur, e0);
+      e = ecur;
+    }
+    ec.get(a.row_ent, e, e1, lane, kt, nmask, ksc, vsc, nks, nvs);
     nkey0 = kt * TILE + (s & 1) * BN;
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
@@ -304,7 +320,7 @@ void bwd_dq_mfma(KArgs a) {
   const int r0 = qt * TILE + 32 * wave;
   store_rows<D, 2, true>(acc, a.scale * pow2_rcp(tds * ds_s * kcur), stage, a.dq,
                    (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2], a.dqs[1],
-                   min(32, a.Lq - r0), lane, E::pack2);
+                   min(32, a.Lq - r0), lane, E::pack2, SPLIT ? a.srow[item * 4 + wave] : 0xffffffffu);
 }
 
 // ---------------------------------------------------------------------------
@@ -340,7 +356,6 @@ void bwd_dq_ds(KArgs a) {
 
   const int item = a.q_order[blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
-  if (a.asc[item] < 0.f) return;  // a split tile: bwd_dq_mfma<SPLIT> serves it
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -358,7 +373,7 @@ void bwd_dq_ds(KArgs a) {
   int64_t orow = (int64_t)b * a.dqs[0] + (int64_t)r0 * a.dqs[1] + (int64_t)h * a.dqs[2];
   int64_t ostr = a.dqs[1];
   void* odq = a.dq;
-  float osc = a.scale * pow2_rcp(a.asc[item]);
+  float osc = a.scale * pow2_rcp(fabsf(a.asc[item]));  // (negative for a split tile)
   asm volatile("" : "+s"(nrows), "+s"(orow), "+s"(ostr), "+s"(odq), "+v"(osc));
 
   const int tb = (b * a.Hkv + hk) * a.nkt;  // first tile of this kv head in the per-tile arrays
@@ -522,9 +537,9 @@ void bwd_dq_ds(KArgs a) {
 
 template <int D, class Tag>
 static void launch_dq_t(const KArgs& a, int grid, hipStream_t st) {
-  // the tiles that are not split (from the stored dS, or recomputing), then
-  // the split ones (recomputing, with the rounded-off parts); each kernel's
-  // workgroups of the other kind return at once
+  // every row (from the stored dS, or recomputing), then the split rows again
+  // (recomputing, with the rounded-off parts; workgroups of tiles without a
+  // split row return at once)
   if (a.ds) hipLaunchKernelGGL((bwd_dq_ds<D, Tag>), dim3(grid), dim3(256), 0, st, a);
   else hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, false>), dim3(grid), dim3(256), 0, st, a);
   hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);

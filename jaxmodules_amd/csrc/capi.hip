@@ -52,13 +52,14 @@ size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
 // Forward residual (16-bit inputs, D <= 128): V as float16 times a power of two per
 // 128-key tile, [B, Hkv, nkt * 128, D]; Q likewise per 128-query tile,
 // [B, Hq, nqt * 128, D] (written when MATTN_FWD_FOR_BWD is set); each tile's
-// scale, each V tile's max |V|, and each query tile's largest attention
-// weight (which makes it a split tile: forward and backward free of the
-// float16 rounding of their operands there).
+// scale, each V tile's max |V|, and per query tile the largest attention
+// weight of its rows and the mask of its split rows (rows whose largest
+// weight reaches SPLIT_P: their forward and backward terms are formed free of
+// the float16 rounding of their operands).
 // MATTN_PRECISE on the SIMT kernels: what the stored lse and O round off
 // (float32, [B, Hq, Lq] and [B, Hq, Lq, D]), which the backward adds back.
 struct FwdWs {
-  size_t vh, qh, vsc, vmax, qsc, pmx, lse_lo, o_lo, total;
+  size_t vh, qh, vsc, vmax, qsc, pmx, srow, lse_lo, o_lo, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
@@ -79,7 +80,8 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
   w.vmax = w.vsc + align256(ktiles * sizeof(float));
   w.qsc = w.vmax + align256(ktiles * sizeof(float));
   w.pmx = w.qsc + align256(qtiles * sizeof(float));
-  w.total = w.pmx + align256(qtiles * sizeof(float));
+  w.srow = w.pmx + align256(qtiles * sizeof(float));
+  w.total = w.srow + align256(qtiles * 4 * sizeof(uint32_t));
   return w;
 }
 
@@ -265,6 +267,7 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
     a.qsc = (float*)(ws + w.qsc);
     a.qh = (p->flags & MATTN_FWD_FOR_BWD) ? (uint16_t*)(ws + w.qh) : nullptr;
     a.pmx = (float*)(ws + w.pmx);
+    a.srow = (uint32_t*)(ws + w.srow);
   }
   hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, simt_path(p), bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
@@ -324,6 +327,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.vmax = (float*)(res + r.vmax);
     a.qsc = (float*)(res + r.qsc);
     a.pmx = (float*)(res + r.pmx);
+    a.srow = (uint32_t*)(res + r.srow);
     if (ds_path(p)) {  // dS after the workspace's other parts (w.total is 256-byte aligned)
       a.ds = (uint16_t*)(ws + w.total);
       a.col_row = bm->col_row;

@@ -98,15 +98,18 @@ struct KArgs {
   int precise;         // MATTN_PRECISE: the SIMT kernels form the scores as compensated dot products
   float* lse_lo;       // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq], (m + log2 l) - lse
   float* o_lo;         // MATTN_PRECISE (SIMT, forward residual): [B, Hq, Lq, D], exact O - stored O
-  // Split tiles (MFMA path): per query tile the largest attention weight of
-  // any of its rows (forward residual, written with qh).  A tile whose
-  // largest weight reaches SPLIT_P is a split tile: bwd_pre stores the part
-  // of dO' that float16 rounds off (dol, [B, Hq, nqt*128, D], only such
-  // tiles' rows), takes delta from the unrounded dO and marks the tile by a
-  // negative asc; the dK/dV and dQ kernels then add the products of those
-  // rounded-off parts (of dO', P and dS), so that the tile's terms enter the
-  // gradients with 22 significant bits instead of 11.
+  // Split rows (MFMA path): a row whose largest attention weight reaches
+  // SPLIT_P.  The forward leaves per query tile the largest weight of its
+  // rows (pmx) and a 128-bit mask of its split rows (srow, 4 words, bit i of
+  // word w = row 32 w + i); a tile with a split row is a split tile.  bwd_pre
+  // stores the part of dO' that float16 rounds off in a split tile's rows
+  // (dol, [B, Hq, nqt*128, D]), takes the split rows' delta from the
+  // unrounded dO and marks the tile by a negative asc; kernels of their own
+  // then form the split rows' O, lse and dQ, and the dK / dV terms of the
+  // split rows' allowed pairs, with the products of those rounded-off parts
+  // (of dO', P and dS): 22 significant bits instead of 11.
   float* pmx;
+  uint32_t* srow;
   uint16_t* dol;
   int* scol;           // [B*Hkv*nkt] per dK/dV column: its walk met a split tile
   float* kvp;          // [B*Hkv*nkt][2][128][D] such a column's unrounded dK, dV (units of 1)
@@ -126,6 +129,48 @@ __device__ __forceinline__ int64_t ds_rep(const KArgs& a, int b, int h) {
   const int rb = a.map_b == 1 ? b : 0, rh = a.map_h == 1 ? h : 0;
   return ((int64_t)rb * (a.map_h == 1 ? a.Hq : 1) + rh) * a.ds_nnz;
 }
+// Row walks of the split kernels (forward, dQ): of the first 64 entries of
+// map row [e0, e1) of query tile `item`, those where a split row of the tile
+// has an allowed key (a full tile, or a mask word of a split row not zero),
+// as a bit mask (entries past the first 64 always count).  Every wave finds
+// the same mask: lane l checks rows l and l + 64 (the words of the mask id
+// met last are reused, as the entries of a row often share one).
+__device__ __forceinline__ uint64_t split_entries(const KArgs& a, int item, int e0, int e1, int lane) {
+  const uint32_t sr0 = a.srow[item * 4 + (lane >> 5)], sr1 = a.srow[item * 4 + 2 + (lane >> 5)];
+  const bool s0 = (sr0 >> (lane & 31)) & 1u, s1 = (sr1 >> (lane & 31)) & 1u;
+  const int n64 = min(e1 - e0, 64);
+  const int mk = a.row_ent[2 * min(e0 + lane, e1 - 1) + 1];
+  uint64_t need = 0ull;
+  int last = -2;
+  bool last_need = true;
+  for (int i = 0; i < n64; ++i) {
+    const int m = __builtin_amdgcn_readlane(mk, i);
+    if (m != last) {
+      last = m;
+      if (m < 0) {
+        last_need = true;
+      } else {
+        const uint64_t* w = a.row_bits + (int64_t)m * 2 * TILE;
+        const bool hit = (s0 && (w[lane] | w[TILE + lane]) != 0) || (s1 && (w[64 + lane] | w[TILE + 64 + lane]) != 0);
+        last_need = __any(hit);
+      }
+    }
+    if (last_need) need |= 1ull << i;
+  }
+  return need;
+}
+// The entry after `e` that split_entries counts (e0 - 1 for the first).
+__device__ __forceinline__ int split_next(uint64_t need, int e, int e0) {
+  const int i = e + 1 - e0;
+  if (i >= 64) return e + 1;
+  const uint64_t rest = need >> i;
+  return rest ? e + 1 + (int)__builtin_ctzll(rest) : e0 + 64;
+}
+// Sub-blocks (two per entry) of such a walk.
+__device__ __forceinline__ int split_subblocks(uint64_t need, int e0, int e1) {
+  return 2 * (__builtin_popcountll(need) + max(e1 - e0 - 64, 0));
+}
+
 // Elements of one tile's dS (128 x 128 float16), as the dK/dV kernel's waves
 // hold it (lane = key): per 32-query group w, 32-key group kg and 16-query
 // half t, a 1 KiB block at (8 w + 2 kg + t) * 512 elements of 64 16-byte
@@ -405,9 +450,11 @@ struct EntryCache {
 // goes to out + ES * (row0 + r * rstride) when r < nrows.  ES = 4 stores
 // float32, ES = 2 the 16-bit values pack2 makes.  NT: nontemporal stores
 // (rows that no kernel of the step reads back soon).
+// Rows whose bit in rmask is clear are not stored.
 template <int D, int ES, bool NT, class Pack>
 __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc, void* lds, void* out,
-                                           int64_t row0, int64_t rstride, int nrows, int lane, Pack pack2) {
+                                           int64_t row0, int64_t rstride, int nrows, int lane, Pack pack2,
+                                           uint32_t rmask = 0xffffffffu) {
   constexpr int RB = D * ES;     // bytes per row
   constexpr int CPR = RB / 16;   // 16-byte chunks per row
   const int r = lane & 31, hi = lane >> 5;
@@ -432,7 +479,7 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc
     const int row = n / CPR, c = n % CPR;
     const u32x4 v = *(const u32x4*)(L + row * RB + ((c ^ (row & (CPR - 1))) << 4));
     u32x4* dst = (u32x4*)((char*)out + (int64_t)ES * (row0 + (int64_t)row * rstride) + 16 * c);
-    if (row < nrows) {
+    if (row < nrows && ((rmask >> row) & 1u)) {
       if constexpr (NT) __builtin_nontemporal_store(v, dst);
       else *dst = v;
     }

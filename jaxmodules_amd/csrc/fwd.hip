@@ -70,14 +70,16 @@ void cvt_v(KArgs a) {
 }
 
 // SPLIT: the kernel launched after the main one (SPLIT = false) for the
-// split tiles, the query tiles whose rows put a weight of at least SPLIT_P on
-// a key (pmx; its other workgroups return at once).  It walks such a row
-// again and overwrites O and the lse with values free of the float16
-// rounding of P: the row sum adds the unrounded weights, and O^T += V'^T P^T
-// takes P as float16(P) + the rounded-off part, by one more MFMA against the
-// same V'^T operand.  The backward's exp(S - lse) is then the exact softmax
-// of these rows, and O the exact convex combination under it, which its
-// split-tile products need.
+// split rows, the rows that put a weight of at least SPLIT_P on a key (srow;
+// the workgroups of tiles without one return at once).  It walks the tile's
+// entries where a split row has an allowed key again and overwrites the
+// split rows' O and lse with values free of the float16 rounding of P: the
+// row sum adds the unrounded weights, and O^T += V'^T P^T takes P as
+// float16(P) + the rounded-off part, by one more MFMA against the same V'^T
+// operand.  The backward's exp(S - lse) is then the exact softmax of these
+// rows, and O the exact convex combination under it, which their split
+// products need.  (The other rows of the tile keep the main kernel's O and
+// lse: the entries skipped here may hold their keys.)
 template <int D, class Tag, bool OUT_F32, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
@@ -99,17 +101,26 @@ void fwd_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
   __shared__ float QM[4];  // per wave: max |Q| (the float16 Q copy's scale), at the end the largest weight
 
-  const int item = a.q_order[blockIdx.x];
+  // (the split kernel takes the launch order backwards: split tiles are
+  // mostly short rows, which the order puts last)
+  const int item = a.q_order[SPLIT ? gridDim.x - 1 - blockIdx.x : blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
   if constexpr (SPLIT) {
-    if (!(a.pmx[item] >= SPLIT_P)) return;  // not a split tile: the main kernel's O and lse stand
+    if (!(a.pmx[item] >= SPLIT_P)) return;  // no split row: the main kernel's O and lse stand
   }
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
   const int mrow = map_row(a, b, h, a.nqt, qt);
   const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
-  const int nsb = 2 * (e1 - e0);
+  // SPLIT: only the entries where a split row has an allowed key
+  uint64_t need = ~0ull;
+  int nsb = 2 * (e1 - e0);
+  if constexpr (SPLIT) {
+    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
+    nsb = split_subblocks(need, e0, e1);
+  }
+  int ecur = e0 - 1;  // SPLIT: the entry of the last prepared sub-block
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -190,7 +201,12 @@ void fwd_mfma(KArgs a) {
   auto prep = [&](int s) {
     int kt;
     float unused;
-    ec.get(a.row_ent, e0 + (s >> 1), e1, lane, kt, nmask, vsc, vsc, nnu, unused);
+    int e = e0 + (s >> 1);
+    if constexpr (SPLIT) {  // the next entry the split rows need
+      if ((s & 1) == 0) ecur = split_next(need, ecur, e0);
+      e = ecur;
+    }
+    ec.get(a.row_ent, e, e1, lane, kt, nmask, vsc, vsc, nnu, unused);
     nkey0 = kt * TILE + (s & 1) * BN;
   };
   auto launch = [&](int s, auto bufc) {  // global -> LDS loads of sub-block s into buffer bufc
@@ -367,13 +383,19 @@ void fwd_mfma(KArgs a) {
 
   l = wave_sum32(l);
   const float inv = l > 0.f ? 1.f / (l * nu) : 0.f;
-  if (hi == 0 && q < a.Lq)
+  // SPLIT: only the split rows' lse and O (the wave's 32 rows, bit r = row r)
+  const uint32_t keep = SPLIT ? a.srow[item * 4 + wave] : 0xffffffffu;
+  if (hi == 0 && q < a.Lq && ((keep >> l32) & 1u))
     a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
   if (!SPLIT && a.pmx != nullptr) {  // the tile's largest attention weight: exp2(max - lse) of its rows
     float pm = l > 0.f ? fast_exp2(mtr - (m2 + __builtin_log2f(l))) : 0.f;
+    const uint32_t split_rows = (uint32_t)__ballot(pm >= SPLIT_P);  // lanes 0-31: the wave's rows
 #pragma unroll
     for (int o = 16; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
-    if (lane == 0) QM[wave] = pm;
+    if (lane == 0) {
+      QM[wave] = pm;
+      a.srow[item * 4 + wave] = split_rows;
+    }
   }
   // O through LDS (one K / V buffer per wave, free once every wave is done)
   __builtin_amdgcn_s_waitcnt(0);
@@ -384,7 +406,7 @@ void fwd_mfma(KArgs a) {
   const int r0 = qt * TILE + 32 * wave;
   store_rows<D, OUT_F32 ? 4 : 2, true>(acc, inv, stage, a.out,
                                  (int64_t)b * a.os[0] + (int64_t)r0 * a.os[1] + (int64_t)h * a.os[2], a.os[1],
-                                 min(32, a.Lq - r0), lane, E::pack2);
+                                 min(32, a.Lq - r0), lane, E::pack2, keep);
 }
 
 // ---------------------------------------------------------------------------

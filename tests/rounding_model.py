@@ -13,12 +13,14 @@ roundings).  Two designs are modelled:
 * ``"bfloat16"`` -- the earlier operand choice for bfloat16 inputs: P in the
   input dtype for P V with the normaliser from the unrounded P, dS in
   bfloat16 for dK and dQ, and dQ's dP from dO rounded to bfloat16;
-* ``"split"`` -- the float16 design with split tiles, as the kernels run it
-  now: a 128-row query tile whose rows put a weight of at least SPLIT_P on a
-  key has its O and lse formed again from unrounded weights and their sum,
-  and enters the backward with its float16 operands' rounded-off parts (dO,
-  P and dS to 22 significant bits, i.e. unrounded here) and delta from the
-  unrounded dO; the other tiles as ``"float16"``.
+* ``"split"`` -- the float16 design with split rows, as the kernels run it
+  now: a row that puts a weight of at least SPLIT_P on a key has its O and
+  lse formed again from unrounded weights and their sum, and enters the
+  backward with its float16 operands' rounded-off parts (dO, P and dS to 22
+  significant bits, i.e. unrounded here) and delta from the unrounded dO;
+  the other rows as ``"float16"`` (the kernels also take the rounded-off parts
+  of those rows' terms where they share a sub-block with a split row's
+  allowed pairs; the model leaves them rounded, the weaker case).
 
 Operands the kernels scale by a power of two before rounding (dO, the
 backward's P and dS) are rounded to float16's 11 significant bits without its
@@ -65,14 +67,18 @@ TILE = 128
 
 
 def split_rows(P):
-    """[B, Hq, N] booleans: the rows of split query tiles (P: [B, Hq, N, L] weights)."""
+    """[B, Hq, N] booleans: the split rows, whose largest weight reaches SPLIT_P
+    (P: [B, Hq, N, L] weights)."""
+    return P.max(-1) >= SPLIT_P
+
+
+def split_tiles(P):
+    """[B, Hq, N] booleans: the rows of the 128-row query tiles holding a split row."""
     B, Hq, N, _ = P.shape
-    pm = P.max(-1)
     nt = -(-N // TILE)
-    pad = np.zeros((B, Hq, nt * TILE))
-    pad[..., :N] = pm
-    tile = pad.reshape(B, Hq, nt, TILE).max(-1) >= SPLIT_P
-    return np.repeat(tile, TILE, axis=-1)[..., :N]
+    pad = np.zeros((B, Hq, nt * TILE), bool)
+    pad[..., :N] = split_rows(P)
+    return np.repeat(pad.reshape(B, Hq, nt, TILE).any(-1), TILE, axis=-1)[..., :N]
 
 
 def kernel_model(Q, K, V, dO, allowed, scale, dtype, design="float16"):

@@ -154,16 +154,17 @@ def test_split_tiles_meet_the_gate_on_unit_normal_inputs(mask, d):
         assert max(r) <= 1.0, (out, r)
 
 
-def test_split_rows_are_whole_query_tiles():
-    """split_rows marks every row of a 128-row query tile in which some row
-    puts a weight of at least SPLIT_P on a key, and no other row."""
+def test_split_rows_and_tiles():
+    """split_rows marks the rows that put a weight of at least SPLIT_P on a key;
+    split_tiles every row of a 128-row query tile holding one."""
     from tests import rounding_model as rm
 
     P = np.full((1, 2, 300, 50), 0.01)
     P[0, 0, 5, 3] = rm.SPLIT_P          # tile 0 of head 0
     P[0, 1, 299, 0] = 0.9               # the last (partial) tile of head 1
     P[0, 1, 130, 0] = rm.SPLIT_P * 0.99
-    s = rm.split_rows(P)
-    assert s.shape == (1, 2, 300)
-    assert s[0, 0, :128].all() and not s[0, 0, 128:].any()
-    assert s[0, 1, 256:].all() and not s[0, 1, :256].any()
+    r = rm.split_rows(P)
+    assert r.shape == (1, 2, 300) and r.sum() == 2 and r[0, 0, 5] and r[0, 1, 299]
+    t = rm.split_tiles(P)
+    assert t[0, 0, :128].all() and not t[0, 0, 128:].any()
+    assert t[0, 1, 256:].all() and not t[0, 1, :256].any()

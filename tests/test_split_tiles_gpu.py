@@ -7,8 +7,9 @@ bfloat16 gradient one ulp past the parity gate).
 * pmx, read from the residual at its documented place (after the float16 V'
   and Q' copies, the V' scales and maxima and the Q' scales, each block
   256-byte aligned), equals the oracle's largest softmax weight over each
-  tile's rows (to float16 rounding of the forward's normaliser), for causal,
-  document and unit-variance problems, padding included;
+  tile's rows (to float16 rounding of the forward's normaliser), and the
+  split-row mask after it flags exactly the rows whose largest weight reaches
+  SPLIT_P, for causal, document and unit-variance problems;
 * the split-tile problems these masks make (a quarter to all of the tiles
   split) meet the parity gate in every output, with a float32 and a bfloat16
   output, without the float16-floor allowance.
@@ -32,12 +33,17 @@ def _align(x):
 
 
 def _pmx(res, B, Hq, Hkv, N, L, D):
-    """The residual's [B, Hq, nqt] per-tile largest weights."""
+    """The residual's [B, Hq, nqt] per-tile largest weights and [B, Hq, nqt * 128]
+    split-row flags (the 128-bit mask per tile that follows them)."""
     nqt, nkt = -(-N // 128), -(-L // 128)
     qt, kt = B * Hq * nqt, B * Hkv * nkt
     off = _align(kt * 128 * D * 2) + _align(qt * 128 * D * 2) + 2 * _align(kt * 4) + _align(qt * 4)
     base = (res.data_ptr() + 255) // 256 * 256 - res.data_ptr()
-    return res[base + off:base + off + qt * 4].view(torch.float32).cpu().numpy().reshape(B, Hq, nqt)
+    pmx = res[base + off:base + off + qt * 4].view(torch.float32).cpu().numpy().reshape(B, Hq, nqt)
+    off += _align(qt * 4)
+    words = res[base + off:base + off + qt * 16].view(torch.int32).cpu().numpy().astype(np.uint32)
+    bits = (words.reshape(qt, 4)[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1
+    return pmx, bits.reshape(B, Hq, nqt * 128).astype(bool)
 
 
 def _masks():
@@ -64,7 +70,7 @@ def test_pmx_is_each_query_tiles_largest_weight(mask, scaled):
     plan, tm = A.trace_call(tuple(q.shape), tuple(k.shape), tuple(v.shape), device=q.device, **kw)
     o, lse, res = A.mattn_forward(q, k, v, tm, 1 / math.sqrt(d), torch.float32, for_backward=True)
     torch.cuda.synchronize()
-    got = _pmx(res, B, Hq, Hkv, N, N, d)
+    got, split = _pmx(res, B, Hq, Hkv, N, N, d)
     # the oracle's weights on the same (rounded) inputs
     Qr, Kr, Vr = (x.float().cpu().numpy().astype(np.float64) for x in (q, k, v))
     _, _, _, allowed = oracle(Qr, Kr, Vr, None, kw, grads=False)
@@ -79,6 +85,13 @@ def test_pmx_is_each_query_tiles_largest_weight(mask, scaled):
     pm[..., :P.shape[2]] = P.max(-1)
     want = pm.reshape(B, Hq, nqt, 128).max(-1)
     np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-7)
+    # the split rows: largest weight at least SPLIT_P (rows within rounding of it excepted)
+    rowmax = P.max(-1)
+    clear = np.abs(rowmax / SPLIT_P - 1) > 2e-3
+    assert np.array_equal(split[..., :N][clear], (rowmax >= SPLIT_P)[clear])
+    # a tile with a split row has its largest weight at least SPLIT_P
+    nq = split.shape[-1] // 128
+    assert np.array_equal(split.reshape(B, Hq, nq, 128).any(-1), got >= SPLIT_P)
     frac = (want >= SPLIT_P).mean()
     print(f"[split] {mask} scaled={scaled}: {frac:.2f} of the tiles split", flush=True)
     assert frac > 0  # every one of these masks has rows with a dominant key
