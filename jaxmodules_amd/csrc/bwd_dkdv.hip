@@ -275,6 +275,21 @@ void bwd_dkdv_mfma(KArgs a) {
   f32x16 dk[NMD], dv[NMD];
 #pragma unroll
   for (int i = 0; i < NMD; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+  // the column's unrounded dK, dV (units of 1): wave kg's [2][NMD][64][16]
+  // floats of its 32 keys, dK then dV, each lane's 16 registers of an MFMA
+  // tile contiguous
+  float* const part = a.kvp + ((int64_t)col * 8 + 2 * kg) * (NMD * 16 * 64);
+  if constexpr (SPLIT) {
+    // the first kernel's sums (the other query half starts from zero), loaded
+    // while the K' / V' tiles come
+    if (qh == 0) {
+#pragma unroll
+      for (int mt = 0; mt < NMD; ++mt) {
+        dk[mt] = *(const f32x16*)&part[(mt * 64 + lane) * 16];
+        dv[mt] = *(const f32x16*)&part[((NMD + mt) * 64 + lane) * 16];
+      }
+    }
+  }
 
   const int dsp_l0 = ds_pos(lane, 0) * 8, dsp_l1 = 512 + ds_pos(lane, 1) * 8;  // chunk offsets per t
   auto store_ds = [&]() {
@@ -554,6 +569,8 @@ void bwd_dkdv_mfma(KArgs a) {
           const float sp_s = -__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, as_l), j));
           const float sp_r = a.qsc[hb * a.nqt + qt];
           for (int half = 0; half < 2; ++half) {
+            const uint32_t* sr = a.srow + (hb * a.nqt + qt) * 4 + 2 * half;
+            if ((sr[0] | sr[1]) == 0u) continue;  // no split row in this half (uniform)
             const int q0 = qt * TILE + half * BM;
             const int64_t rows = (hb * hrows + q0) * D;
 #pragma unroll
@@ -581,7 +598,7 @@ void bwd_dkdv_mfma(KArgs a) {
               m2c = c2 * pow2_rcp(sp_r * ksc);
             }
             {  // this wave's split rows of the sub-block, and their allowed keys among the wave's 32
-              const uint32_t ws = a.srow[(hb * a.nqt + qt) * 4 + 2 * half + qh];
+              const uint32_t ws = sr[qh];
               const uint32_t w = mid >= 0 ? (uint32_t)(M0[kloc] >> (32 * qh)) : 0xffffffffu;
               if (__any((w & ws) != 0u)) correct(mid >= 0);
             }
@@ -669,18 +686,7 @@ void bwd_dkdv_mfma(KArgs a) {
     iter(s, std::integral_constant<int, 0>{});
     if (s + 1 < tot) iter(s + 1, std::integral_constant<int, 1>{});
   }
-  // the column's unrounded dK, dV (units of 1): wave kg's [2][NMD][64][16]
-  // floats of its 32 keys, dK then dV, each lane's 16 registers of an MFMA
-  // tile contiguous
-  float* const part = a.kvp + ((int64_t)col * 8 + 2 * kg) * (NMD * 16 * 64);
   if constexpr (SPLIT) {
-    if (qh == 0) {  // the first kernel's sums (the other query half starts from zero)
-#pragma unroll
-      for (int mt = 0; mt < NMD; ++mt) {
-        dk[mt] = *(const f32x16*)&part[(mt * 64 + lane) * 16];
-        dv[mt] = *(const f32x16*)&part[((NMD + mt) * 64 + lane) * 16];
-      }
-    }
     split_pass();
   } else {
     if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};  // (read after the barrier below)

@@ -70,10 +70,6 @@ void bwd_dq_mfma(KArgs a) {
   // SPLIT: only the entries where a split row has an allowed key
   uint64_t need = ~0ull;
   int nsb = 2 * (e1 - e0);
-  if constexpr (SPLIT) {
-    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
-    nsb = split_subblocks(need, e0, e1);
-  }
   int ecur = e0 - 1;  // SPLIT: the entry of the last prepared sub-block
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -97,6 +93,10 @@ void bwd_dq_mfma(KArgs a) {
       qf[kd] = *(const u32x4*)(qp + 16 * kd);
       df[kd] = *(const u32x4*)(dp + 16 * kd);
     }
+  }
+  if constexpr (SPLIT) {  // (after the operand loads above, whose latency it overlaps)
+    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
+    nsb = split_subblocks(need, e0, e1);
   }
   const int64_t rs = ((int64_t)b * a.Hq + h) * a.Lq + qc;
   const float nlse = -a.lse[rs];

@@ -116,10 +116,6 @@ void fwd_mfma(KArgs a) {
   // SPLIT: only the entries where a split row has an allowed key
   uint64_t need = ~0ull;
   int nsb = 2 * (e1 - e0);
-  if constexpr (SPLIT) {
-    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
-    nsb = split_subblocks(need, e0, e1);
-  }
   int ecur = e0 - 1;  // SPLIT: the entry of the last prepared sub-block
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -137,6 +133,10 @@ void fwd_mfma(KArgs a) {
                          (int64_t)h * a.qs[2] + 8 * hi;
 #pragma unroll
     for (int kd = 0; kd < NKD; ++kd) qf[kd] = *(const u32x4*)(qp + 16 * kd);
+  }
+  if constexpr (SPLIT) {  // (after the operand loads above, whose latency it overlaps)
+    need = split_entries(a, item, e0, e1, threadIdx.x & 63);
+    nsb = split_subblocks(need, e0, e1);
   }
   if (!SPLIT && a.qh != nullptr) {
     // float16 copy of the tile's Q rows for the backward (rows past Lq zero)
