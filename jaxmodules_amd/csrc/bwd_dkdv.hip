@@ -52,11 +52,15 @@ namespace mattn {
 // return at once), starts from kvp, and adds for each split sub-block the
 // products of what float16 rounded off there (correct() below), so that the
 // tile's terms enter dK and dV with 22 significant bits; it then stores the
-// column's dK and dV over the first kernel's.
+// column's dK and dV over the first kernel's.  At D = 64 the registers allow
+// both in one kernel (FUSED): a column whose walk met a split row runs the
+// same correction pass right after its walk, from the accumulators it holds
+// and the resident K' / V' tiles, and no second kernel is launched.
 template <int D, class Tag, bool DS, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void bwd_dkdv_mfma(KArgs a) {
   static_assert(!(DS && SPLIT), "the split kernel stores no dS");
+  constexpr bool FUSED = !SPLIT && D == 64;  // the correction pass in this kernel
   using E = Elt<Tag>;
   using H = Elt<f16_tag>;
   using TL = TileLoad<D>;
@@ -75,7 +79,7 @@ void bwd_dkdv_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t QH0[2 * BM * D], QH1[2 * BM * D];
   __shared__ __attribute__((aligned(16))) uint16_t KV[2 * TILE * D];
   // SPLIT: the rounded-off part of dO' of the split sub-block being corrected
-  __shared__ __attribute__((aligned(16))) uint16_t DL[SPLIT ? BM * D : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t DL[SPLIT || FUSED ? BM * D : 8];
   uint16_t* const Q0 = QH0;
   uint16_t* const H0 = QH0 + BM * D;
   uint16_t* const Q1 = QH1;
@@ -688,6 +692,24 @@ void bwd_dkdv_mfma(KArgs a) {
   }
   if constexpr (SPLIT) {
     split_pass();
+  } else if constexpr (FUSED) {
+    // every wave is done with the LDS of the walk; a column that met a split
+    // row with an allowed key corrects its split sub-blocks now (uniform)
+    if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (no load is in flight after the walk; stores may be)
+    barrier_lds();
+    bool col_split = false;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) col_split |= red[w][0] != 0.f;
+    if (col_split) {
+      if constexpr (DS) {
+        if (dpend) {  // the last sub-block's fragments, before the pass reuses the registers
+          store_ds();
+          dpend = nullptr;
+        }
+      }
+      split_pass();
+    }
   } else {
     if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};  // (read after the barrier below)
   }
@@ -700,7 +722,7 @@ void bwd_dkdv_mfma(KArgs a) {
   // tiles with 16-byte accesses along the rows.
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (the dS~ stores of the sub-block before the last)
   barrier_lds();                               // every wave is done with the LDS
-  if constexpr (!SPLIT) {  // the column met a split row with an allowed key: the split kernel redoes it
+  if constexpr (!SPLIT && !FUSED) {  // the column met a split row with an allowed key: the split kernel redoes it
     any_split = false;
 #pragma unroll
     for (int w = 0; w < 8; ++w) any_split |= red[w][0] != 0.f;
@@ -737,7 +759,7 @@ void bwd_dkdv_mfma(KArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[mt][4 * c + j] += x[j];
         }
-      if constexpr (!SPLIT) {
+      if constexpr (!SPLIT && !FUSED) {
         if (any_split) {  // for the split kernel, in units of 1 (powers of two: exact)
 #pragma unroll
           for (int mt = 0; mt < NMD; ++mt) *(f32x16*)&keep[(mt * 64 + lane) * 16] = acc[mt] * unit;
@@ -783,8 +805,9 @@ template <int D, class Tag>
 static void launch_dkdv_t(const KArgs& a, int grid, hipStream_t st) {
   if (a.ds) hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, true, false>), dim3(grid), dim3(512), 0, st, a);
   else hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, false, false>), dim3(grid), dim3(512), 0, st, a);
-  // the columns that met a split tile again (the others' workgroups return at once)
-  hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, false, true>), dim3(grid), dim3(512), 0, st, a);
+  // the columns that met a split tile again (the others' workgroups return at
+  // once); at D = 64 the first kernel corrects them itself
+  if constexpr (D != 64) hipLaunchKernelGGL((bwd_dkdv_mfma<D, Tag, false, true>), dim3(grid), dim3(512), 0, st, a);
 }
 
 hipError_t launch_dkdv(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {

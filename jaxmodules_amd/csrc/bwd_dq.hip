@@ -40,6 +40,10 @@ namespace mattn {
 // (the rounded-off part of dO' that bwd_pre left in dol, B operands read from
 // global memory four k-steps at a time) and dQ^T += K'^T dS~_lo^T, dS~_lo =
 // dS~ - float16(dS~), by one more MFMA against the same K'^T operand.
+// FUSED (the recomputing kernel at D = 64, where the registers allow both
+// step forms in one kernel): the one dQ kernel.  A split tile walks all its
+// entries with the SPLIT products and stores every row (its other rows then
+// also take the rounded-off parts), the other tiles walk as SPLIT = false.
 template <int D, class Tag, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_mfma(KArgs a) {
@@ -59,9 +63,11 @@ void bwd_dq_mfma(KArgs a) {
 
   // (the split kernel takes the launch order backwards: split tiles are
   // mostly short rows, which the order puts last)
+  constexpr bool FUSED = !SPLIT && D == 64;
   const int item = a.q_order[SPLIT ? gridDim.x - 1 - blockIdx.x : blockIdx.x];
   if (item < 0 || item >= a.B * a.Hq * a.nqt) return;  // idle slot (or an entry out of range)
   if (SPLIT && !(a.asc[item] < 0.f)) return;            // no split row: the other kernel's dQ stands
+  const bool fsplit = FUSED && a.asc[item] < 0.f;       // FUSED: a split tile (uniform)
   const int qt = item % a.nqt;
   const int bh = item / a.nqt;
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
@@ -181,8 +187,9 @@ void bwd_dq_mfma(KArgs a) {
   float vcur = 0.f, nlv = 0.f;
   f32x16 cvec = f32x16{};
 
-  auto step = [&](auto bufc, bool masked, float sks, float svs) {
+  auto step = [&](auto bufc, auto spc, bool masked, float sks, float svs) {
     constexpr int BUF = decltype(bufc)::value;
+    constexpr bool SP = decltype(spc)::value;  // with the split products
     if (sks != kcur) {  // a tile with another K' scale (uniform; powers of two: exact)
       const float f = sks / kcur;
 #pragma unroll
@@ -233,7 +240,7 @@ void bwd_dq_mfma(KArgs a) {
         hold(st);
         hold(dp);
       });
-      if constexpr (SPLIT) {  // dP'^T += V' dO'_lo^T, the dO'_lo^T operands loaded four at a time
+      if constexpr (SP) {  // dP'^T += V' dO'_lo^T, the dO'_lo^T operands loaded four at a time
         static_for<NKD / 4>([&](auto gc) {
           constexpr int g = decltype(gc)::value;
           u32x4 dl[4];
@@ -264,7 +271,7 @@ void bwd_dq_mfma(KArgs a) {
         const float d1 = st[r + 1] * dp[r + 1];
         const uint32_t w = H::pack2(d0, d1);
         pk[r >> 3][(r & 7) >> 1] = w;
-        if constexpr (SPLIT)  // the rounded-off parts (the differences are exact in float32)
+        if constexpr (SP)  // the rounded-off parts (the differences are exact in float32)
           pl[r >> 3][(r & 7) >> 1] = H::pack2(d0 - H::to_f32(w & 0xffffu), d1 - H::to_f32(w >> 16));
       }
       // dQ^T += K^T dS^T over the half's two k-steps, K^T by transposed reads
@@ -285,7 +292,7 @@ void bwd_dq_mfma(KArgs a) {
         const u32x4 aop = u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]};
         acc[mt] = H::mfma(aop, pk[kk], acc[mt]);
         hold(acc[mt]);
-        if constexpr (SPLIT) {
+        if constexpr (SP) {
           acc[mt] = H::mfma(aop, pl[kk], acc[mt]);
           hold(acc[mt]);
         }
@@ -301,7 +308,12 @@ void bwd_dq_mfma(KArgs a) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, masked, sks, svs);
+    if constexpr (FUSED) {
+      if (fsplit) step(bufc, std::true_type{}, masked, sks, svs);
+      else step(bufc, std::false_type{}, masked, sks, svs);
+    } else {
+      step(bufc, std::integral_constant<bool, SPLIT>{}, masked, sks, svs);
+    }
   };
   if (nsb > 0) {
     prep(0);
@@ -539,10 +551,11 @@ template <int D, class Tag>
 static void launch_dq_t(const KArgs& a, int grid, hipStream_t st) {
   // every row (from the stored dS, or recomputing), then the split rows again
   // (recomputing, with the rounded-off parts; workgroups of tiles without a
-  // split row return at once)
+  // split row return at once).  The recomputing kernel at D = 64 serves the
+  // split tiles itself.
   if (a.ds) hipLaunchKernelGGL((bwd_dq_ds<D, Tag>), dim3(grid), dim3(256), 0, st, a);
   else hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, false>), dim3(grid), dim3(256), 0, st, a);
-  hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
+  if (a.ds || D != 64) hipLaunchKernelGGL((bwd_dq_mfma<D, Tag, true>), dim3(grid), dim3(256), 0, st, a);
 }
 
 hipError_t launch_dq(const KArgs& a, int D, int dtype, int grid, hipStream_t st) {

@@ -135,8 +135,9 @@ __device__ __forceinline__ int64_t ds_rep(const KArgs& a, int b, int h) {
 // as a bit mask (entries past the first 64 always count).  Every wave finds
 // the same mask: lane l checks rows l and l + 64 (the words of the mask id
 // met last are reused, as the entries of a row often share one).
-__device__ __forceinline__ uint64_t split_entries(const KArgs& a, int item, int e0, int e1, int lane) {
-  const uint32_t sr0 = a.srow[item * 4 + (lane >> 5)], sr1 = a.srow[item * 4 + 2 + (lane >> 5)];
+// (sr0, sr1: the split-row words of the waves whose rows are lane and lane + 64)
+__device__ __forceinline__ uint64_t split_entries_w(const KArgs& a, uint32_t sr0, uint32_t sr1, int e0, int e1,
+                                                    int lane) {
   const bool s0 = (sr0 >> (lane & 31)) & 1u, s1 = (sr1 >> (lane & 31)) & 1u;
   const int n64 = min(e1 - e0, 64);
   const int mk = a.row_ent[2 * min(e0 + lane, e1 - 1) + 1];
@@ -158,6 +159,9 @@ __device__ __forceinline__ uint64_t split_entries(const KArgs& a, int item, int 
     if (last_need) need |= 1ull << i;
   }
   return need;
+}
+__device__ __forceinline__ uint64_t split_entries(const KArgs& a, int item, int e0, int e1, int lane) {
+  return split_entries_w(a, a.srow[item * 4 + (lane >> 5)], a.srow[item * 4 + 2 + (lane >> 5)], e0, e1, lane);
 }
 // The entry after `e` that split_entries counts (e0 - 1 for the first).
 __device__ __forceinline__ int split_next(uint64_t need, int e, int e0) {

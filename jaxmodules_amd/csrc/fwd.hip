@@ -80,6 +80,10 @@ void cvt_v(KArgs a) {
 // rows, and O the exact convex combination under it, which their split
 // products need.  (The other rows of the tile keep the main kernel's O and
 // lse: the entries skipped here may hold their keys.)
+// FUSED (the main kernel at D = 64, where the registers allow both walks in
+// one kernel): a tile with split rows stores its other rows, then walks again
+// as the SPLIT kernel would and stores the split rows; no second kernel is
+// launched.
 template <int D, class Tag, bool OUT_F32, bool SPLIT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void fwd_mfma(KArgs a) {
@@ -100,6 +104,9 @@ void fwd_mfma(KArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t KV0[2 * BN * D], KV1[2 * BN * D];
   __shared__ __attribute__((aligned(16))) uint64_t M0[TILE], M1[TILE];  // partial-tile mask words
   __shared__ float QM[4];  // per wave: max |Q| (the float16 Q copy's scale), at the end the largest weight
+  __shared__ uint32_t SR[4];  // FUSED: per wave, its split rows
+  constexpr bool FUSED = !SPLIT && D == 64;
+  bool swalk = false;  // FUSED: the second walk (over the split rows' entries) is running
 
   // (the split kernel takes the launch order backwards: split tiles are
   // mostly short rows, which the order puts last)
@@ -202,7 +209,7 @@ void fwd_mfma(KArgs a) {
     int kt;
     float unused;
     int e = e0 + (s >> 1);
-    if constexpr (SPLIT) {  // the next entry the split rows need
+    if (SPLIT || (FUSED && swalk)) {  // the next entry the split rows need
       if ((s & 1) == 0) ecur = split_next(need, ecur, e0);
       e = ecur;
     }
@@ -241,8 +248,9 @@ void fwd_mfma(KArgs a) {
   float mtr = NEG_INF;          // the row's exact max (m2 trails it by up to RESCALE_SLACK)
   float nu = 1.f;               // V' scale the accumulators are in: acc = nu * sum P V
 
-  auto step = [&](auto bufc, bool masked, float snu) {
+  auto step = [&](auto bufc, auto spc, bool masked, float snu) {
     constexpr int BUF = decltype(bufc)::value;
+    constexpr bool SP = decltype(spc)::value;  // the split rows' walk
     // operand reads pipelined by hand (asm LDS reads issued PS / PV steps ahead
     // of their MFMAs, counted lgkmcnt waits); V sits BN * D elements after K
     constexpr int PS = 3, PV = 4;
@@ -319,7 +327,7 @@ void fwd_mfma(KArgs a) {
         const float p0 = fast_exp2(fmaf(st[t][r], c2, nmu));
         const float p1 = fast_exp2(fmaf(st[t][r + 1], c2, nmu));
         const uint32_t w = H::pack2(p0, p1);
-        if constexpr (SPLIT) {  // the unrounded sum, and what float16 rounds off P
+        if constexpr (SP) {  // the unrounded sum, and what float16 rounds off P
           l += p0;
           l += p1;
           plo[2 * t + (r >> 3)][(r & 7) >> 1] = H::pack2(p0 - H::to_f32(w & 0xffffu), p1 - H::to_f32(w >> 16));
@@ -351,7 +359,7 @@ void fwd_mfma(KArgs a) {
         const u32x4 aop = u32x4{lo[sl][0], lo[sl][1], up[sl][0], up[sl][1]};
         acc[mt] = H::mfma(aop, pk[ks], acc[mt]);
         hold(acc[mt]);
-        if constexpr (SPLIT) {
+        if constexpr (SP) {
           acc[mt] = H::mfma(aop, plo[ks], acc[mt]);
           hold(acc[mt]);
         }
@@ -361,52 +369,82 @@ void fwd_mfma(KArgs a) {
 
   // sub-block s computes from buffer s % 2 while s + 1 loads into the other;
   // the loop is unrolled by two so that every buffer index is static
-  auto iter = [&](int s, auto bufc) {
+  auto iter = [&](int s, auto bufc, auto spc) {
     const bool masked = nmask >= 0;  // sub-block s, prepared one iteration ago
     const float snu = nnu;
     if (s + 1 < nsb) prep(s + 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, masked, snu);
+    step(bufc, spc, masked, snu);
   };
-  if (nsb > 0) {
-    prep(0);
-    launch(0, std::integral_constant<int, 0>{});
-    static_for<2 * NI>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
-    dma_on = false;
-  }
-  for (int s = 0; s < nsb; s += 2) {
-    iter(s, std::integral_constant<int, 0>{});
-    if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{});
-  }
+  auto walk = [&](auto spc) {
+    if (nsb > 0) {
+      prep(0);
+      launch(0, std::integral_constant<int, 0>{});
+      static_for<2 * NI>([&](auto ic) { dma(std::integral_constant<int, 0>{}, ic); });  // no step to carry them
+      dma_on = false;
+    }
+    for (int s = 0; s < nsb; s += 2) {
+      iter(s, std::integral_constant<int, 0>{}, spc);
+      if (s + 1 < nsb) iter(s + 1, std::integral_constant<int, 1>{}, spc);
+    }
+  };
+  const int r0 = qt * TILE + 32 * wave;
+  uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * BN * D;
+  static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
+  // lse and O of the rows in `keep` (the wave's 32 rows, bit r = row r), O
+  // through LDS (one K / V buffer per wave, free once every wave is done)
+  auto store = [&](uint32_t keep) {
+    const float inv = l > 0.f ? 1.f / (l * nu) : 0.f;
+    if (hi == 0 && q < a.Lq && ((keep >> l32) & 1u))
+      a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
+    store_rows<D, OUT_F32 ? 4 : 2, true>(acc, inv, stage, a.out,
+                                   (int64_t)b * a.os[0] + (int64_t)r0 * a.os[1] + (int64_t)h * a.os[2], a.os[1],
+                                   min(32, a.Lq - r0), lane, E::pack2, keep);
+  };
 
+  walk(std::integral_constant<bool, SPLIT>{});
   l = wave_sum32(l);
-  const float inv = l > 0.f ? 1.f / (l * nu) : 0.f;
-  // SPLIT: only the split rows' lse and O (the wave's 32 rows, bit r = row r)
-  const uint32_t keep = SPLIT ? a.srow[item * 4 + wave] : 0xffffffffu;
-  if (hi == 0 && q < a.Lq && ((keep >> l32) & 1u))
-    a.lse[((int64_t)b * a.Hq + h) * a.Lq + q] = l > 0.f ? m2 + __builtin_log2f(l) : NEG_INF;
+  // SPLIT: only the split rows' lse and O
+  uint32_t keep = SPLIT ? a.srow[item * 4 + wave] : 0xffffffffu;
+  uint32_t split_rows = 0u;
   if (!SPLIT && a.pmx != nullptr) {  // the tile's largest attention weight: exp2(max - lse) of its rows
     float pm = l > 0.f ? fast_exp2(mtr - (m2 + __builtin_log2f(l))) : 0.f;
-    const uint32_t split_rows = (uint32_t)__ballot(pm >= SPLIT_P);  // lanes 0-31: the wave's rows
+    split_rows = (uint32_t)__ballot(pm >= SPLIT_P);  // lanes 0-31: the wave's rows
 #pragma unroll
     for (int o = 16; o >= 1; o >>= 1) pm = fmaxf(pm, __shfl_xor(pm, o));
     if (lane == 0) {
       QM[wave] = pm;
+      if constexpr (FUSED) SR[wave] = split_rows;
       a.srow[item * 4 + wave] = split_rows;
     }
   }
-  // O through LDS (one K / V buffer per wave, free once every wave is done)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (!SPLIT && a.pmx != nullptr && tid == 0) a.pmx[item] = fmaxf(fmaxf(QM[0], QM[1]), fmaxf(QM[2], QM[3]));
-  uint16_t* stage = (wave < 2 ? KV0 : KV1) + (wave & 1) * BN * D;
-  static_assert(32 * D * (OUT_F32 ? 4 : 2) <= BN * D * 2, "output staging");
-  const int r0 = qt * TILE + 32 * wave;
-  store_rows<D, OUT_F32 ? 4 : 2, true>(acc, inv, stage, a.out,
-                                 (int64_t)b * a.os[0] + (int64_t)r0 * a.os[1] + (int64_t)h * a.os[2], a.os[1],
-                                 min(32, a.Lq - r0), lane, E::pack2, keep);
+  const float tmx = fmaxf(fmaxf(QM[0], QM[1]), fmaxf(QM[2], QM[3]));
+  if (!SPLIT && a.pmx != nullptr && tid == 0) a.pmx[item] = tmx;
+  const bool again = FUSED && a.pmx != nullptr && tmx >= SPLIT_P;  // (uniform)
+  store(again ? ~split_rows : keep);
+  if constexpr (FUSED) {
+    if (again) {  // the split rows' walk, as the SPLIT kernel runs it
+      need = split_entries_w(a, SR[lane >> 5], SR[2 + (lane >> 5)], e0, e1, lane);
+      nsb = split_subblocks(need, e0, e1);
+      ecur = e0 - 1;
+      swalk = true;
+#pragma unroll
+      for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
+      m2 = NEG_INF;
+      l = 0.f;
+      nu = 1.f;
+      __syncthreads();  // every wave's staged O is read: the buffers may be refilled
+      walk(std::true_type{});
+      l = wave_sum32(l);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      store(split_rows);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -418,10 +456,11 @@ static hipError_t launch_fwd_mfma(const KArgs& a, int grid, bool out_f32, hipStr
   hipLaunchKernelGGL((cvt_v<D, Tag>), dim3(a.B * a.Hkv * a.nkt), dim3(512), 0, st, a);
   if (out_f32) {
     hipLaunchKernelGGL((fwd_mfma<D, Tag, true, false>), dim3(grid), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((fwd_mfma<D, Tag, true, true>), dim3(grid), dim3(256), 0, st, a);  // split tiles again
+    // split tiles again (at D = 64 the first kernel walks them again itself)
+    if constexpr (D != 64) hipLaunchKernelGGL((fwd_mfma<D, Tag, true, true>), dim3(grid), dim3(256), 0, st, a);
   } else {
     hipLaunchKernelGGL((fwd_mfma<D, Tag, false, false>), dim3(grid), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((fwd_mfma<D, Tag, false, true>), dim3(grid), dim3(256), 0, st, a);
+    if constexpr (D != 64) hipLaunchKernelGGL((fwd_mfma<D, Tag, false, true>), dim3(grid), dim3(256), 0, st, a);
   }
   return hipGetLastError();
 }

@@ -48,12 +48,16 @@ def _kernels(asm, stem="13bwd_dkdv_mfma"):
 @pytest.mark.parametrize("which", ["dkdv", "dq", "dq_ds", "fwd"])
 def test_every_instantiation_waits_before_use(which, dkdv_asm, dq_asm, fwd_asm):
     asm, stem, least, count = {
-        # D = 64 / 128 x bfloat16 / float16 x (storing dS, not storing it, the split kernel)
-        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 60, 12),
-        # D = 64 / 128 x bfloat16 / float16 x (other tiles, split tiles)
+        # D = 64 / 128 x bfloat16 / float16 x (storing dS, not storing it), and the split
+        # kernel at D = 128 (at D = 64 the first kernel corrects the split columns itself)
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 60, 10),
+        # D = 64 / 128 x bfloat16 / float16 x (other tiles, split tiles); at D = 64 the
+        # first also serves the split tiles when dS is not stored
         "dq": (dq_asm, "11bwd_dq_mfma", 60, 8),
         "dq_ds": (dq_asm, "9bwd_dq_ds", 40, 4),
-        "fwd": (fwd_asm, "8fwd_mfma", 50, 16),           # ... x float32 / 16-bit output x (main, split tiles)
+        # ... x float32 / 16-bit output x (main, split tiles at D = 128; at D = 64 the main
+        # kernel walks its split rows again itself)
+        "fwd": (fwd_asm, "8fwd_mfma", 50, 12),
     }[which]
     names = _kernels(asm, stem)
     assert len(names) == count, names
@@ -98,10 +102,10 @@ def test_checker_follows_forward_branches():
 @pytest.mark.parametrize("which", ["dkdv", "dq", "dq_ds", "fwd"])
 def test_every_instantiation_retires_its_lds_dma_before_each_barrier(which, dkdv_asm, dq_asm, fwd_asm):
     asm, stem, least, count = {
-        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 6, 12),
+        "dkdv": (dkdv_asm, "13bwd_dkdv_mfma", 6, 10),
         "dq": (dq_asm, "11bwd_dq_mfma", 10, 8),
         "dq_ds": (dq_asm, "9bwd_dq_ds", 6, 4),      # D = 64: 2 K' loads x (prologue + 2 unrolled steps)
-        "fwd": (fwd_asm, "8fwd_mfma", 10, 16),
+        "fwd": (fwd_asm, "8fwd_mfma", 10, 12),
     }[which]
     names = _kernels(asm, stem)
     assert len(names) == count, names
