@@ -181,9 +181,10 @@ size_t mattn_bwd_workspace_bytes(const mattn_problem* p, const mattn_blockmap* b
 
 /* Bytes of the forward's residual buffer (256-byte aligned pointer): float16
  * copies of V and (with MATTN_FWD_FOR_BWD) Q, each times a power of two per
- * 128-row tile, which the forward's P V product and the backward read (16-bit
- * inputs at D <= 128); (1 + D) float32 per query row under MATTN_PRECISE;
- * 0 otherwise (float32 inputs, D >= 256). */
+ * 128-row tile, which the forward's P V product and the backward read, with
+ * the split tiles' rows and key tiles (16-bit inputs at D <= 128); (1 + D)
+ * float32 per query row under MATTN_PRECISE; 0 otherwise (float32 inputs,
+ * D >= 256). */
 size_t mattn_fwd_workspace_bytes(const mattn_problem* p);
 
 /* Forward (replaces the custom_vjp primal and fwd rule, attention.py:180-264).

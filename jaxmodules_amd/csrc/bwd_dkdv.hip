@@ -44,10 +44,11 @@ namespace mattn {
 // before the wait ahead of the following barrier, which counts stores too.
 //
 // Split tiles.  A query tile whose rows put a weight of at least SPLIT_P on
-// a key is a split tile (bwd_pre marks it by a negative asc).  The kernel
-// (SPLIT = false) computes its sub-blocks like any other; a column whose walk
-// met one also leaves its reduced dK and dV unrounded (float32, free of the
-// accumulator scales) in kvp and sets its flag in scol.  The SPLIT = true
+// a key is a split tile (bwd_pre marks it by a negative asc); the forward's
+// walk of its split rows flags the columns where they have allowed keys
+// (scol).  The kernel (SPLIT = false) computes its sub-blocks like any other;
+// a flagged column also leaves its reduced dK and dV unrounded (float32, free
+// of the accumulator scales) in kvp.  The SPLIT = true
 // kernel, launched after it, takes those columns (its other workgroups
 // return at once), starts from kvp, and adds for each split sub-block the
 // products of what float16 rounded off there (correct() below), so that the
@@ -95,8 +96,9 @@ void bwd_dkdv_mfma(KArgs a) {
   const u32x4 dB = ((const u32x4*)a.kv_desc)[2 * blockIdx.x + 1];
   const int item = (int)dA[0];
   if (item < 0 || item >= a.B * a.Hkv * a.nkt) return;  // idle slot (or an entry out of range)
+  const bool col_split = a.scol[item] != 0;  // a split row has an allowed key in this column
   if constexpr (SPLIT) {
-    if (a.scol[item] == 0) return;  // no split tile in this column: the first kernel's dK, dV stand
+    if (!col_split) return;  // the first kernel's dK, dV stand
   }
   const int kt = item % a.nkt;
   const int bh = item / a.nkt;
@@ -154,15 +156,8 @@ void bwd_dkdv_mfma(KArgs a) {
   const int wofs = __builtin_amdgcn_readfirstlane(NS * wave * BLK);  // this wave's load block
   EntryCache ec;
   int mid0 = -1, mid1 = -1;  // mask id of the sub-block in each buffer (-1: full tile)
-  // dO' and Q' tile scales (s, r) of the sub-block in each buffer, and
-  // whether its query tile is a split tile (the sign of asc)
+  // dO' and Q' tile scales (s, r) of the sub-block in each buffer
   float sh0 = 1.f, rh0 = 1.f, sh1 = 1.f, rh1 = 1.f;
-  bool sp0 = false, sp1 = false;
-  // the split rows among this wave's 32 queries of the sub-block in each
-  // buffer (srow), and whether the walk met a split row with an allowed key of
-  // this wave's 32 (then the split kernel redoes the column)
-  uint32_t sw0 = 0u, sw1 = 0u;
-  bool any_split = false;
   // buffer resources of the current query head's Q' and dO' slices
   const int64_t hrows = (int64_t)a.nqt * TILE;  // rows per head in the copies
   const uint32_t hbytes = (uint32_t)(hrows * D * 2);
@@ -243,10 +238,7 @@ void bwd_dkdv_mfma(KArgs a) {
     if constexpr (DS)  // this query half's two dQ waves (2 lhalf, 2 lhalf + 1) of the tile's slot
       (BUF ? dsp1 : dsp0) = a.ds + (ds_rep(a, b, rh_head) + cur_ri) * DS_TILE + lhalf * (2 * 8 * 512);
     (BUF ? mid1 : mid0) = cur_mid;
-    (BUF ? sh1 : sh0) = fabsf(cur_s);
-    (BUF ? sp1 : sp0) = cur_s < 0.f;
-    if constexpr (!SPLIT)
-      (BUF ? sw1 : sw0) = cur_s < 0.f ? a.srow[((int64_t)(b * a.Hq + rh_head) * a.nqt + cur_qt) * 4 + 2 * lhalf + qh] : 0u;
+    (BUF ? sh1 : sh0) = fabsf(cur_s);  // (negative for a split tile)
     (BUF ? rh1 : rh0) = cur_r;
     nq0 = cur_qt * TILE + lhalf * BM;
     if (lhalf == 0) {
@@ -627,10 +619,6 @@ void bwd_dkdv_mfma(KArgs a) {
     if constexpr (DS) {
       if (dpend) store_ds();  // sub-block s - 1's fragments
     }
-    if (BUF ? sp1 : sp0) {  // a split tile: do split rows of this wave have allowed keys here?
-      const uint32_t w = masked ? (uint32_t)((BUF ? M1 : M0)[kloc] >> (32 * qh)) : 0xffffffffu;
-      any_split |= __any((w & (BUF ? sw1 : sw0)) != 0u);
-    }
     step(bufc, masked);
   };
   if (tot > 0) {
@@ -682,9 +670,6 @@ void bwd_dkdv_mfma(KArgs a) {
     cur_r = rh0 = first_r;
     cur_s = first_s;
     sh0 = fabsf(first_s);
-    sp0 = first_s < 0.f;
-    if constexpr (!SPLIT)
-      sw0 = sp0 ? a.srow[((int64_t)(b * a.Hq + hk * a.G + (int)dA[1]) * a.nqt + (int)dB[1]) * 4 + qh] : 0u;
   }
   for (int s = 0; s < tot; s += 2) {
     iter(s, std::integral_constant<int, 0>{});
@@ -693,15 +678,11 @@ void bwd_dkdv_mfma(KArgs a) {
   if constexpr (SPLIT) {
     split_pass();
   } else if constexpr (FUSED) {
-    // every wave is done with the LDS of the walk; a column that met a split
-    // row with an allowed key corrects its split sub-blocks now (uniform)
-    if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (no load is in flight after the walk; stores may be)
-    barrier_lds();
-    bool col_split = false;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) col_split |= red[w][0] != 0.f;
+    // a flagged column corrects its split sub-blocks now, once every wave is
+    // done with the LDS of the walk (uniform)
     if (col_split) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (no load is in flight after the walk; stores may be)
+      barrier_lds();
       if constexpr (DS) {
         if (dpend) {  // the last sub-block's fragments, before the pass reuses the registers
           store_ds();
@@ -710,8 +691,6 @@ void bwd_dkdv_mfma(KArgs a) {
       }
       split_pass();
     }
-  } else {
-    if (lane == 0) red[wave] = f32x2{any_split ? 1.f : 0.f, 0.f};  // (read after the barrier below)
   }
 
   // dK / dV: the second query half's partials join the first's through LDS
@@ -722,12 +701,6 @@ void bwd_dkdv_mfma(KArgs a) {
   // tiles with 16-byte accesses along the rows.
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // (the dS~ stores of the sub-block before the last)
   barrier_lds();                               // every wave is done with the LDS
-  if constexpr (!SPLIT && !FUSED) {  // the column met a split row with an allowed key: the split kernel redoes it
-    any_split = false;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) any_split |= red[w][0] != 0.f;
-    if (tid == 0) a.scol[col] = any_split ? 1 : 0;
-  }
   if constexpr (DS) {
     if (dpend) store_ds();  // the last sub-block's fragments, in flight during the reduction below
   }
@@ -760,7 +733,7 @@ void bwd_dkdv_mfma(KArgs a) {
           for (int j = 0; j < 4; ++j) acc[mt][4 * c + j] += x[j];
         }
       if constexpr (!SPLIT && !FUSED) {
-        if (any_split) {  // for the split kernel, in units of 1 (powers of two: exact)
+        if (col_split) {  // for the split kernel, in units of 1 (powers of two: exact)
 #pragma unroll
           for (int mt = 0; mt < NMD; ++mt) *(f32x16*)&keep[(mt * 64 + lane) * 16] = acc[mt] * unit;
         }

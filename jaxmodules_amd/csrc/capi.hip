@@ -55,11 +55,13 @@ size_t ds_slots(const mattn_problem* p, const mattn_blockmap* bm) {
 // scale, each V tile's max |V|, and per query tile the largest attention
 // weight of its rows and the mask of its split rows (rows whose largest
 // weight reaches SPLIT_P: their forward and backward terms are formed free of
-// the float16 rounding of their operands).
+// the float16 rounding of their operands), and per key tile a flag: a split
+// row has an allowed key there (its dK/dV column then takes the split
+// products; cleared by the V' conversion, set by the split rows' walk).
 // MATTN_PRECISE on the SIMT kernels: what the stored lse and O round off
 // (float32, [B, Hq, Lq] and [B, Hq, Lq, D]), which the backward adds back.
 struct FwdWs {
-  size_t vh, qh, vsc, vmax, qsc, pmx, srow, lse_lo, o_lo, total;
+  size_t vh, qh, vsc, vmax, qsc, pmx, srow, scol, lse_lo, o_lo, total;
 };
 
 FwdWs fwd_ws_layout(const mattn_problem* p) {
@@ -81,7 +83,8 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
   w.qsc = w.vmax + align256(ktiles * sizeof(float));
   w.pmx = w.qsc + align256(qtiles * sizeof(float));
   w.srow = w.pmx + align256(qtiles * sizeof(float));
-  w.total = w.srow + align256(qtiles * 4 * sizeof(uint32_t));
+  w.scol = w.srow + align256(qtiles * 4 * sizeof(uint32_t));
+  w.total = w.scol + align256(ktiles * sizeof(int));
   return w;
 }
 
@@ -91,11 +94,11 @@ FwdWs fwd_ws_layout(const mattn_problem* p) {
 // D]) and K' ([B, Hkv, nkt * 128, D]), and per 128-row tile the dO' scale, the
 // dS bounds and scale of the query tiles and the K' scale of the key tiles;
 // then the rounded-off part of dO' ([B, Hq, nqt * 128, D] float16, written and
-// read only in the rows of split tiles), a flag per key tile (its dK/dV
-// column met a split tile) and such a column's unrounded dK and dV (float32,
-// [ktiles][2][128][D], written and read only for those columns).
+// read only in the rows of split tiles) and the unrounded dK and dV of a key
+// tile whose column a split row reaches (float32, [ktiles][2][128][D], written
+// and read only for those columns; the flags are in the forward's residual).
 struct WsLayout {
-  size_t delta, lsf, doh, kh, dsc, tst, asc, ksc, dol, scol, kvp, total;
+  size_t delta, lsf, doh, kh, dsc, tst, asc, ksc, dol, kvp, total;
 };
 
 WsLayout ws_layout(const mattn_problem* p) {
@@ -114,8 +117,7 @@ WsLayout ws_layout(const mattn_problem* p) {
   w.asc = w.tst + align256(qtiles * 8);
   w.ksc = w.asc + align256(qtiles * sizeof(float));
   w.dol = w.ksc + align256(ktiles * sizeof(float));
-  w.scol = w.dol + align256(qtiles * MATTN_TILE_Q * p->D * 2);
-  w.kvp = w.scol + align256(ktiles * sizeof(int));
+  w.kvp = w.dol + align256(qtiles * MATTN_TILE_Q * p->D * 2);
   w.total = w.kvp + align256(ktiles * MATTN_TILE_K * p->D * 2 * sizeof(float));
   return w;
 }
@@ -268,6 +270,7 @@ int mattn_fwd(const mattn_problem* p, const mattn_blockmap* bm, const void* q, c
     a.qh = (p->flags & MATTN_FWD_FOR_BWD) ? (uint16_t*)(ws + w.qh) : nullptr;
     a.pmx = (float*)(ws + w.pmx);
     a.srow = (uint32_t*)(ws + w.srow);
+    a.scol = (int*)(ws + w.scol);
   }
   hipError_t e = launch_fwd(a, p->D, p->dtype, p->o_dtype, simt_path(p), bm->n_q_order, (hipStream_t)stream);
   return e == hipSuccess ? MATTN_OK : MATTN_ERR_LAUNCH;
@@ -317,7 +320,6 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.asc = (float*)(ws + w.asc);
     a.ksc = (float*)(ws + w.ksc);
     a.dol = (uint16_t*)(ws + w.dol);
-    a.scol = (int*)(ws + w.scol);
     a.kvp = (float*)(ws + w.kvp);
     const FwdWs r = fwd_ws_layout(p);
     const char* res = (const char*)residual;
@@ -328,6 +330,7 @@ int mattn_bwd_stage(const mattn_problem* p, const mattn_blockmap* bm, int stage,
     a.qsc = (float*)(res + r.qsc);
     a.pmx = (float*)(res + r.pmx);
     a.srow = (uint32_t*)(res + r.srow);
+    a.scol = (int*)(res + r.scol);
     if (ds_path(p)) {  // dS after the workspace's other parts (w.total is 256-byte aligned)
       a.ds = (uint16_t*)(ws + w.total);
       a.col_row = bm->col_row;

@@ -111,7 +111,7 @@ struct KArgs {
   float* pmx;
   uint32_t* srow;
   uint16_t* dol;
-  int* scol;           // [B*Hkv*nkt] per dK/dV column: its walk met a split tile
+  int* scol;           // [B*Hkv*nkt] per dK/dV column: a split row has an allowed key in it
   float* kvp;          // [B*Hkv*nkt][2][128][D] such a column's unrounded dK, dV (units of 1)
 };
 

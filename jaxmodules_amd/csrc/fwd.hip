@@ -34,7 +34,8 @@
 namespace mattn {
 
 // V -> vh = float16 V * vsc[tile], one workgroup of 512 threads per
-// (b, kv head, 128-key tile); rows past Lk are zero.
+// (b, kv head, 128-key tile); rows past Lk are zero.  It also clears the
+// tile's split-column flag, which the split rows' walk of the forward sets.
 template <int D, class Tag>
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512)))
 void cvt_v(KArgs a) {
@@ -66,6 +67,7 @@ void cvt_v(KArgs a) {
   if (threadIdx.x == 0) {
     a.vsc[tile] = s;
     a.vmax[tile] = m[0];
+    if (a.scol) a.scol[tile] = 0;
   }
 }
 
@@ -79,7 +81,9 @@ void cvt_v(KArgs a) {
 // operand.  The backward's exp(S - lse) is then the exact softmax of these
 // rows, and O the exact convex combination under it, which their split
 // products need.  (The other rows of the tile keep the main kernel's O and
-// lse: the entries skipped here may hold their keys.)
+// lse: the entries skipped here may hold their keys.)  Where a split row has
+// an allowed key in a sub-block, the walk flags that key tile's dK/dV column
+// (scol), for the backward's split products.
 // FUSED (the main kernel at D = 64, where the registers allow both walks in
 // one kernel): a tile with split rows stores its other rows, then walks again
 // as the SPLIT kernel would and stores the split rows; no second kernel is
@@ -120,6 +124,7 @@ void fwd_mfma(KArgs a) {
   const int h = bh % a.Hq, b = bh / a.Hq, hk = h / a.G;
   const int mrow = map_row(a, b, h, a.nqt, qt);
   const int e0 = a.row_ptr[mrow], e1 = a.row_ptr[mrow + 1];
+  const int kcol0 = (b * a.Hkv + hk) * a.nkt;  // the kv head's first dK/dV column
   // SPLIT: only the entries where a split row has an allowed key
   uint64_t need = ~0ull;
   int nsb = 2 * (e1 - e0);
@@ -127,6 +132,8 @@ void fwd_mfma(KArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the split rows' walk: this wave's split rows (bit r = row r)
+  uint32_t swrow = SPLIT ? a.srow[item * 4 + wave] : 0u;
   const int l32 = lane & 31, hi = lane >> 5;
   const int qloc = wave * 32 + l32;
   const int q = qt * TILE + qloc;
@@ -248,7 +255,7 @@ void fwd_mfma(KArgs a) {
   float mtr = NEG_INF;          // the row's exact max (m2 trails it by up to RESCALE_SLACK)
   float nu = 1.f;               // V' scale the accumulators are in: acc = nu * sum P V
 
-  auto step = [&](auto bufc, auto spc, bool masked, float snu) {
+  auto step = [&](auto bufc, auto spc, bool masked, float snu, int skt) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr bool SP = decltype(spc)::value;  // the split rows' walk
     // operand reads pipelined by hand (asm LDS reads issued PS / PV steps ahead
@@ -291,6 +298,9 @@ void fwd_mfma(KArgs a) {
       // the next sub-block it computes).  Its S chain ran, as it carries the
       // wave's share of the next sub-block's loads.
       if (!__any(mw != 0)) return;
+      if constexpr (SP) {  // a split row of this wave with an allowed key here: flag the column
+        if (__any(((swrow >> l32) & 1u) && mw != 0) && lane == 0) a.scol[kcol0 + skt] = 1;
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint32_t w32 = (uint32_t)(mw >> (32 * t)) >> (4 * hi);
@@ -298,6 +308,9 @@ void fwd_mfma(KArgs a) {
         for (int r = 0; r < 16; ++r)
           st[t][r] = mask_neg_inf(st[t][r], mask_ones(w32, r));
       }
+    }
+    if constexpr (SP) {  // a full tile: every split row of the wave has allowed keys here
+      if (!masked && swrow != 0u && lane == 0) a.scol[kcol0 + skt] = 1;
     }
     float mx = NEG_INF;
 #pragma unroll
@@ -372,11 +385,12 @@ void fwd_mfma(KArgs a) {
   auto iter = [&](int s, auto bufc, auto spc) {
     const bool masked = nmask >= 0;  // sub-block s, prepared one iteration ago
     const float snu = nnu;
+    const int skt = nkey0 / TILE;    // its key tile
     if (s + 1 < nsb) prep(s + 1);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of sub-block s have landed
     __syncthreads();                // ... and every wave's; sub-block s-1 fully consumed
     if (s + 1 < nsb) launch(s + 1, std::integral_constant<int, 1 - decltype(bufc)::value>{});
-    step(bufc, spc, masked, snu);
+    step(bufc, spc, masked, snu, skt);
   };
   auto walk = [&](auto spc) {
     if (nsb > 0) {
@@ -407,7 +421,7 @@ void fwd_mfma(KArgs a) {
   walk(std::integral_constant<bool, SPLIT>{});
   l = wave_sum32(l);
   // SPLIT: only the split rows' lse and O
-  uint32_t keep = SPLIT ? a.srow[item * 4 + wave] : 0xffffffffu;
+  uint32_t keep = SPLIT ? swrow : 0xffffffffu;
   uint32_t split_rows = 0u;
   if (!SPLIT && a.pmx != nullptr) {  // the tile's largest attention weight: exp2(max - lse) of its rows
     float pm = l > 0.f ? fast_exp2(mtr - (m2 + __builtin_log2f(l))) : 0.f;
@@ -432,6 +446,7 @@ void fwd_mfma(KArgs a) {
       nsb = split_subblocks(need, e0, e1);
       ecur = e0 - 1;
       swalk = true;
+      swrow = split_rows;
 #pragma unroll
       for (int i = 0; i < NMD; ++i) acc[i] = f32x16{};
       m2 = NEG_INF;

@@ -131,18 +131,18 @@ def test_workspace_bytes(lib):
     inputs) the shifted lse, float16 dO' padded to whole 128-row tiles per
     head, float16 K' per kv-head tile, and per tile the dO' scale, dS bounds
     (2 floats), dS scale and K' scale; then for the split tiles the
-    rounded-off part of dO' (float16, like dO'), a flag per key tile and the
-    unrounded dK and dV of a key tile (float32, 2 x 128 x D per key tile).
-    Forward residual: float16 V' and Q', then V' scales and maxima, Q' scales,
-    each query tile's largest attention weight and its 128-bit mask of split
-    rows."""
+    rounded-off part of dO' (float16, like dO') and the unrounded dK and dV
+    of a key tile (float32, 2 x 128 x D per key tile).  Forward residual:
+    float16 V' and Q', then V' scales and maxima, Q' scales, each query
+    tile's largest attention weight and its 128-bit mask of split rows, and a
+    flag per key tile (a split row has an allowed key there)."""
     align = lambda x: (x + 255) // 256 * 256
     B, L, Hq, Hkv, D = 2, 300, 8, 2, 128
     nqt = -(-L // 128)
     qtiles, ktiles = B * Hq * nqt, B * Hkv * nqt
     want = (2 * align(B * Hq * L * 4) + align(qtiles * 128 * D * 2) + align(ktiles * 128 * D * 2)
             + align(qtiles * 4) + align(qtiles * 8) + align(qtiles * 4) + align(ktiles * 4)
-            + align(qtiles * 128 * D * 2) + align(ktiles * 4) + align(ktiles * 2 * 128 * D * 4))
+            + align(qtiles * 128 * D * 2) + align(ktiles * 2 * 128 * D * 4))
     p = _problem()
     assert lib.mattn_workspace_bytes(ctypes.byref(p)) == want
     p16 = _problem(dtype=_lib.MATTN_F16, o_dtype=_lib.MATTN_F16)
@@ -150,7 +150,7 @@ def test_workspace_bytes(lib):
     p32 = _problem(dtype=_lib.MATTN_F32, o_dtype=_lib.MATTN_F32)
     assert lib.mattn_workspace_bytes(ctypes.byref(p32)) == align(B * Hq * L * 4)
     res = (align(ktiles * 128 * D * 2) + align(qtiles * 128 * D * 2) + 2 * align(ktiles * 4)
-           + 2 * align(qtiles * 4) + align(qtiles * 16))
+           + 2 * align(qtiles * 4) + align(qtiles * 16) + align(ktiles * 4))
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p)) == res
     assert lib.mattn_fwd_workspace_bytes(ctypes.byref(p32)) == 0
     assert lib.mattn_workspace_bytes(ctypes.byref(_problem(D=80))) == 0
