@@ -9,10 +9,14 @@ bfloat16 gradient one ulp past the parity gate).
   256-byte aligned), equals the oracle's largest softmax weight over each
   tile's rows (to float16 rounding of the forward's normaliser), and the
   split-row mask after it flags exactly the rows whose largest weight reaches
-  SPLIT_P, for causal, document and unit-variance problems;
+  SPLIT_P, for causal, document and unit-variance problems, and the flag per
+  key tile after that (set by the split rows' walk of the forward) marks
+  exactly the dK/dV columns where a split row of the kv head's query heads
+  has an allowed key;
 * the split-tile problems these masks make (a quarter to all of the tiles
   split) meet the parity gate in every output, with a float32 and a bfloat16
-  output, without the float16-floor allowance.
+  output, without the float16-floor allowance, at d = 64 (split passes inside
+  the main kernels) and d = 128 (separate split kernels).
 """
 import math
 
@@ -33,8 +37,9 @@ def _align(x):
 
 
 def _pmx(res, B, Hq, Hkv, N, L, D):
-    """The residual's [B, Hq, nqt] per-tile largest weights and [B, Hq, nqt * 128]
-    split-row flags (the 128-bit mask per tile that follows them)."""
+    """The residual's [B, Hq, nqt] per-tile largest weights, [B, Hq, nqt * 128]
+    split-row flags (the 128-bit mask per tile that follows them) and
+    [B, Hkv, nkt] split-column flags (one int per key tile after those)."""
     nqt, nkt = -(-N // 128), -(-L // 128)
     qt, kt = B * Hq * nqt, B * Hkv * nkt
     off = _align(kt * 128 * D * 2) + _align(qt * 128 * D * 2) + 2 * _align(kt * 4) + _align(qt * 4)
@@ -43,7 +48,9 @@ def _pmx(res, B, Hq, Hkv, N, L, D):
     off += _align(qt * 4)
     words = res[base + off:base + off + qt * 16].view(torch.int32).cpu().numpy().astype(np.uint32)
     bits = (words.reshape(qt, 4)[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1
-    return pmx, bits.reshape(B, Hq, nqt * 128).astype(bool)
+    off += _align(qt * 16)
+    scol = res[base + off:base + off + kt * 4].view(torch.int32).cpu().numpy().reshape(B, Hkv, nkt)
+    return pmx, bits.reshape(B, Hq, nqt * 128).astype(bool), scol != 0
 
 
 def _masks():
@@ -57,20 +64,21 @@ def _masks():
     }
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("scaled", [True, False], ids=["scaled", "unit"])
 @pytest.mark.parametrize("mask", ["causal", "documents", "window"])
-def test_pmx_is_each_query_tiles_largest_weight(mask, scaled):
+def test_pmx_is_each_query_tiles_largest_weight(mask, scaled, d):
     from jaxmodules_amd import attention as A
 
-    B, N, Hq, Hkv, d = 2, 300, 4, 2, 64
+    B, N, Hq, Hkv = 2, 300, 4, 2
     kw = _masks()[mask]
-    print(f"[split] pmx mask={mask} scaled={scaled}", flush=True)
+    print(f"[split] pmx mask={mask} scaled={scaled} d={d}", flush=True)
     Q, K, V, _ = seeded_inputs(B, N, N, Hq, Hkv, d, 97, scaled=scaled)
     q, k, v = (torch.from_numpy(x).to("cuda", torch.bfloat16) for x in (Q, K, V))
     plan, tm = A.trace_call(tuple(q.shape), tuple(k.shape), tuple(v.shape), device=q.device, **kw)
     o, lse, res = A.mattn_forward(q, k, v, tm, 1 / math.sqrt(d), torch.float32, for_backward=True)
     torch.cuda.synchronize()
-    got, split = _pmx(res, B, Hq, Hkv, N, N, d)
+    got, split, scol = _pmx(res, B, Hq, Hkv, N, N, d)
     # the oracle's weights on the same (rounded) inputs
     Qr, Kr, Vr = (x.float().cpu().numpy().astype(np.float64) for x in (q, k, v))
     _, _, _, allowed = oracle(Qr, Kr, Vr, None, kw, grads=False)
@@ -92,21 +100,30 @@ def test_pmx_is_each_query_tiles_largest_weight(mask, scaled):
     # a tile with a split row has its largest weight at least SPLIT_P
     nq = split.shape[-1] // 128
     assert np.array_equal(split.reshape(B, Hq, nq, 128).any(-1), got >= SPLIT_P)
+    # the split columns: key tiles where a split row of a query head of the kv
+    # head's group has an allowed key
+    nkt = scol.shape[-1]
+    reach = np.zeros((B, Hq, nkt * 128), bool)
+    reach[..., :N] = (np.broadcast_to(allowed, (B, Hq, N, N)) & split[..., :N, None]).any(2)
+    want_col = reach.reshape(B, Hkv, Hq // Hkv, nkt, 128).any((2, 4))
+    assert np.array_equal(scol, want_col), (scol.sum(), want_col.sum())
     frac = (want >= SPLIT_P).mean()
-    print(f"[split] {mask} scaled={scaled}: {frac:.2f} of the tiles split", flush=True)
+    print(f"[split] {mask} scaled={scaled}: {frac:.2f} of the tiles split, "
+          f"{want_col.mean():.2f} of the columns", flush=True)
     assert frac > 0  # every one of these masks has rows with a dominant key
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("out", [None, "bfloat16"], ids=["out_f32", "out_bf16"])
 @pytest.mark.parametrize("mask", ["causal", "documents", "window"])
-def test_split_tile_problems_meet_the_gate(mask, out):
+def test_split_tile_problems_meet_the_gate(mask, out, d):
     """Unit-variance bfloat16 inputs, where many tiles are split: every output
     within the gate, no float16-floor allowance."""
     import jaxmodules_amd as jm
 
-    B, N, Hq, Hkv, d = 2, 300, 4, 2, 64
+    B, N, Hq, Hkv = 2, 300, 4, 2
     kw = _masks()[mask]
-    print(f"[split] gate mask={mask} out={out}", flush=True)
+    print(f"[split] gate mask={mask} out={out} d={d}", flush=True)
     Q, K, V, dO = seeded_inputs(B, N, N, Hq, Hkv, d, 101, scaled=False)
     q, k, v = (torch.from_numpy(x).to("cuda", torch.bfloat16).requires_grad_() for x in (Q, K, V))
     od = None if out is None else torch.bfloat16
