@@ -80,7 +80,7 @@ enum mattn_status {
  * in split tiles: 128-row query tiles with a row whose largest attention
  * weight reaches 1/32, whose O, lse and gradient terms the MFMA path forms
  * again with those operands' rounded-off parts (22 significant bits) by
- * kernels of their own, after the main ones.  Set it
+ * kernels of their own after the main ones (at D = 64 inside them).  Set it
  * for a forward and for its backward alike; the forward then has no residual.
  * For kernels sharper than the default scale 1/sqrt(d) (the reference's
  * threshold_kernel has scale 1, attention.py:18-36), where rows concentrate

@@ -15,11 +15,13 @@
 //   bwd_dkdv : one workgroup per 128-key map column of (b, kv head); it walks
 //              the column's present query tiles for every query head of the
 //              GQA group and accumulates dK, dV in registers -- no atomics;
-//              a second kernel redoes the columns that met a split tile, with
-//              the products of what float16 rounded off there (bwd_dkdv.hip);
+//              the columns where a split row has an allowed key (flagged by
+//              the forward) then take the products of what float16 rounded
+//              off there: by a second kernel at D = 128, in the same kernel
+//              at D = 64 (bwd_dkdv.hip);
 //   bwd_dq   : one workgroup per 128-query map row; dQ accumulated in
-//              registers; the split tiles' rows by a kernel of their own
-//              (bwd_dq.hip).
+//              registers; the split tiles' rows by a kernel of their own, or
+//              at D = 64 without stored dS in the same kernel (bwd_dq.hip).
 // With P = exp2(scale_log2 * S - lse) and dS = P * (dO V^T - delta):
 //   dV = P^T dO,  dK = scale * dS^T Q,  dQ = scale * dS K.
 // Every product of the 16-bit paths runs on float16 operands (11 significant
