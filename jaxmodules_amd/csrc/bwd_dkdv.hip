@@ -452,17 +452,33 @@ void bwd_dkdv_mfma(KArgs a) {
     const uint32_t qa0 = lds_addr(Q0) + 2 * (uint32_t)qrow;
     const uint32_t la0 = lds_addr(DL) + 2 * (uint32_t)qrow;
     const uint32_t ka0 = lds_addr(Ks) + 2 * (uint32_t)krow_l;
+    // acc += A B over the head dimension, A and B row reads at base + offset:
+    // at D = 64 each k-step's two reads are issued one step ahead (counted
+    // waits); at D = 128, where the split kernel's registers are spent, each
+    // read is waited for at once
+    constexpr int PC = D == 64 ? 1 : 0;
+    auto chain = [&](f32x16& acc, uint32_t ab, auto aoc, uint32_t bb, auto boc) {
+      constexpr int AO = decltype(aoc)::value, BO = decltype(boc)::value;
+      u32x4 ra[PC + 1], rb[PC + 1];
+      auto rd = [&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PC + 1);
+        const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
+        ra[sl] = ds_read128<AO>(ab + x);
+        rb[sl] = ds_read128<BO>(bb + x);
+      };
+      static_for<PC>(rd);
+      static_for<NKD>([&](auto kc) {
+        constexpr int kd = decltype(kc)::value, sl = kd % (PC + 1);
+        if constexpr (kd + PC < NKD) rd(std::integral_constant<int, kd + PC>{});
+        lgkm_wait<2 * (kd + PC < NKD ? PC : NKD - 1 - kd)>();
+        hold(ra[sl]);
+        hold(rb[sl]);
+        acc = H::mfma(ra[sl], rb[sl], acc);
+        hold(acc);
+      });
+    };
     f32x16 st = f32x16{};
-    static_for<NKD>([&](auto kc) {
-      constexpr int kd = decltype(kc)::value;
-      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
-      u32x4 qa = ds_read128<0>(qa0 + x), ka = ds_read128<0>(ka0 + x);
-      lgkm_wait<0>();
-      hold(qa);
-      hold(ka);
-      st = H::mfma(qa, ka, st);
-      hold(st);
-    });
+    chain(st, qa0, std::integral_constant<int, 0>{}, ka0, std::integral_constant<int, 0>{});
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4 lv = *(const f32x4*)&Lb[8 * j + 4 * hi];
@@ -484,16 +500,7 @@ void bwd_dkdv_mfma(KArgs a) {
       plo[r >> 3][(r & 7) >> 1] = H::pack2(st[r] - H::to_f32(wp & 0xffffu), st[r + 1] - H::to_f32(wp >> 16));
     }
     f32x16 dp = f32x16{};
-    static_for<NKD>([&](auto kc) {
-      constexpr int kd = decltype(kc)::value;
-      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
-      u32x4 ha = ds_read128<2 * BM * D>(qa0 + x), va = ds_read128<2 * TILE * D>(ka0 + x);
-      lgkm_wait<0>();
-      hold(ha);
-      hold(va);
-      dp = H::mfma(ha, va, dp);
-      hold(dp);
-    });
+    chain(dp, qa0, std::integral_constant<int, 2 * BM * D>{}, ka0, std::integral_constant<int, 2 * TILE * D>{});
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // step()'s dS~, in place of dP'
       const f32x4 gv = *(const f32x4*)&Gb[8 * j + 4 * hi];
@@ -501,16 +508,7 @@ void bwd_dkdv_mfma(KArgs a) {
       for (int i = 0; i < 4; ++i) dp[4 * j + i] = st[4 * j + i] * fmaf(dp[4 * j + i], ivs, -gv[i]);
     }
     f32x16 dl = f32x16{};
-    static_for<NKD>([&](auto kc) {
-      constexpr int kd = decltype(kc)::value;
-      const uint32_t x = 2 * (uint32_t)opaque((16 * kd) ^ rxo);
-      u32x4 la = ds_read128<0>(la0 + x), va = ds_read128<2 * TILE * D>(ka0 + x);
-      lgkm_wait<0>();
-      hold(la);
-      hold(va);
-      dl = H::mfma(la, va, dl);
-      hold(dl);
-    });
+    chain(dl, la0, std::integral_constant<int, 0>{}, ka0, std::integral_constant<int, 2 * TILE * D>{});
     // dS~_e - float16(dS~) = (dS~ - float16(dS~)) + P~ (dO'_lo V'^T) / v
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
@@ -521,25 +519,32 @@ void bwd_dkdv_mfma(KArgs a) {
                                            fmaf(p1 * dl[r + 1], ivs, dp[r + 1] - H::to_f32(ws >> 16)));
     }
     const uint32_t qb0 = lds_addr(Q0), lb = lds_addr(DL);
-    static_for<2 * NMD>([&](auto ic) {
-      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD;
+    // the six transposed reads of step i (dO', Q', dO'_lo), issued PC steps ahead
+    u32x2 tr[PC + 1][6];
+    auto rt = [&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PC + 1);
       const uint32_t xm = 2 * (uint32_t)opaque((32 * mt) ^ tzo);
       const uint32_t x0 = 2 * (uint32_t)tb0 + xm, x1 = 2 * (uint32_t)tb1 + xm;
-      u32x2 h0 = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x0), h1 = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x1);
-      u32x2 q0 = ds_read_tr8<32 * ks * D>(qb0 + x0), q1 = ds_read_tr8<32 * ks * D>(qb0 + x1);
-      u32x2 l0 = ds_read_tr8<32 * ks * D>(lb + x0), l1 = ds_read_tr8<32 * ks * D>(lb + x1);
-      lgkm_wait<0>();
-      hold(h0);
-      hold(h1);
-      hold(q0);
-      hold(q1);
-      hold(l0);
-      hold(l1);
-      dv[mt] = H::mfma(u32x4{h0[0], h0[1], h1[0], h1[1]}, plo[ks], dv[mt]);
+      tr[sl][0] = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x0);
+      tr[sl][1] = ds_read_tr8<2 * BM * D + 32 * ks * D>(qb0 + x1);
+      tr[sl][2] = ds_read_tr8<32 * ks * D>(qb0 + x0);
+      tr[sl][3] = ds_read_tr8<32 * ks * D>(qb0 + x1);
+      tr[sl][4] = ds_read_tr8<32 * ks * D>(lb + x0);
+      tr[sl][5] = ds_read_tr8<32 * ks * D>(lb + x1);
+    };
+    static_for<PC>(rt);
+    static_for<2 * NMD>([&](auto ic) {
+      constexpr int i = decltype(ic)::value, ks = i / NMD, mt = i % NMD, sl = i % (PC + 1);
+      if constexpr (i + PC < 2 * NMD) rt(std::integral_constant<int, i + PC>{});
+      lgkm_wait<6 * (i + PC < 2 * NMD ? PC : 2 * NMD - 1 - i)>();
+#pragma unroll
+      for (int r = 0; r < 6; ++r) hold(tr[sl][r]);
+      const u32x2* t = tr[sl];
+      dv[mt] = H::mfma(u32x4{t[0][0], t[0][1], t[1][0], t[1][1]}, plo[ks], dv[mt]);
       hold(dv[mt]);
-      dv[mt] = H::mfma(u32x4{l0[0], l0[1], l1[0], l1[1]}, pk[ks], dv[mt]);
+      dv[mt] = H::mfma(u32x4{t[4][0], t[4][1], t[5][0], t[5][1]}, pk[ks], dv[mt]);
       hold(dv[mt]);
-      dk[mt] = H::mfma(u32x4{q0[0], q0[1], q1[0], q1[1]}, slo[ks], dk[mt]);
+      dk[mt] = H::mfma(u32x4{t[2][0], t[2][1], t[3][0], t[3][1]}, slo[ks], dk[mt]);
       hold(dk[mt]);
     });
   };

@@ -10,7 +10,8 @@ every run checks the same problems: seeds 0-23, the draws of a one-off
 bfloat16 dS / dO operands (KNOWN_DRAWS), the draws of two more one-off runs
 (seeds 624-1423) that missed it with float16 operands (LATER_DRAWS), and the
 draw of an 800-problem run (seeds 1424-2223) that missed it with split tiles
-at their first threshold (SPLIT_DRAWS).
+at their first threshold (SPLIT_DRAWS), and the draw of another (seeds
+2224-3023) that misses it within the float16 operands' bound (FLOOR_DRAWS).
 
 threshold_kernel is a softmax with scale 1 instead of 1/sqrt(d), so its
 draws see logits of unit variance (Q, K ~ N(0,1) d^-0.25), seven times
@@ -141,6 +142,21 @@ SPLIT_DRAWS = [2120]
 
 @pytest.mark.parametrize("seed", SPLIT_DRAWS)
 def test_split_draw(seed):
+    run_draw(seed)
+
+
+# The one draw of a one-off 800-problem run (seeds 2224-3023) that misses the
+# gate with split rows at 1/32: cross attention onto 56 keys (every weight
+# about 1/56: no split row), two query heads per kv head, bfloat16 dV
+# elements just above 1, where half a bfloat16 ulp (2^-8) leaves 1.5e-4 of the
+# gate and the float16 rounding of 664 comparable terms exceeds it: 1.003x
+# the gate, within the operands' bound.  Reported xfailed after "highest"
+# meets the gate.
+FLOOR_DRAWS = [2477]
+
+
+@pytest.mark.parametrize("seed", FLOOR_DRAWS)
+def test_floor_draw(seed):
     run_draw(seed)
 
 
