@@ -306,6 +306,11 @@ class Runner:
         return e0.elapsed_time(e1) / steps
 
     def measure(self, steps, warmup):
+        """(ms per step, per-stage ms).  The step time is the wall time of
+        ``steps`` steps between two synchronisations with nothing else queued;
+        the per-stage times come from a second pass of ``steps`` steps with an
+        event between the stages (median per stage), whose records lengthen
+        the short steps."""
         torch = self.torch
         names = ["fwd", "bwd_pre", "bwd_dkdv", "bwd_dq"]
         for _ in range(warmup):
@@ -313,8 +318,14 @@ class Runner:
             for s in range(3):
                 self.bwd(s)
         torch.cuda.synchronize()
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
         t0 = time.perf_counter()
+        for _ in range(steps):
+            self.fwd()
+            for s in range(3):
+                self.bwd(s)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
         for i in range(steps):
             e = ev[i]
             e[0].record()
@@ -324,7 +335,6 @@ class Runner:
                 self.bwd(s)
                 e[2 + s].record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
         per = {n: [] for n in names}
         for e in ev:
             for j, n in enumerate(names):
